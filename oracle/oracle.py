@@ -1,0 +1,404 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes bindings of the CPU oracle (liboracle.so)
+and of the compiled reference sources (_ref/libtsacref.so).
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's CPU baseline import
+this module, and only as the checker or the reported CPU baseline.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import pathlib
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+ORACLE_PATH = HERE / "liboracle.so"
+REF_PATH = HERE / "_ref" / "libtsacref.so"
+
+u8p = C.POINTER(C.c_uint8)
+u16p = C.POINTER(C.c_uint16)
+i8p = C.POINTER(C.c_int8)
+f32p = C.POINTER(C.c_float)
+sz = C.c_size_t
+
+
+class Header(C.Structure):
+    _fields_ = [("method", C.c_uint8), ("groups", C.c_uint8), ("model_channels", C.c_uint8),
+                ("codebooks", C.c_uint8), ("frames", C.c_uint64), ("batch", C.c_uint16)]
+
+
+class Geometry(C.Structure):
+    _fields_ = [(name, C.c_uint32) for name in (
+        "width", "heads", "head_width", "ffn", "temporal_layers", "codebook_layers", "latent",
+        "alphabet", "books", "channels", "context")] + [("attention_scale", C.c_float)]
+
+
+class Linear(C.Structure):
+    _fields_ = [("values", i8p), ("scales", f32p), ("bias", f32p)]
+
+
+class ModelDesc(C.Structure):
+    _fields_ = [("geometry", Geometry), ("projections", C.POINTER(Linear)),
+                ("norm_gain", C.POINTER(u16p)), ("norm_bias", C.POINTER(u16p)),
+                ("positions", u16p), ("rotations", u16p), ("embeddings", u16p)]
+
+
+def ptr(array: np.ndarray, ctype):
+    assert array.flags["C_CONTIGUOUS"]
+    return array.ctypes.data_as(C.POINTER(ctype))
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def _load(path: pathlib.Path):
+    if not path.exists():
+        raise FileNotFoundError(f"{path} is not built (run `make -C oracle`)")
+    return C.CDLL(str(path))
+
+
+def _declare(lib, prefix: str):
+    f = lambda name: getattr(lib, prefix + name)  # noqa: E731
+    f("last_error").restype = C.c_char_p
+    f("bf16").restype = C.c_uint16
+    f("bf16").argtypes = [C.c_float]
+    f("exp").restype = C.c_float
+    f("exp").argtypes = [C.c_float]
+    f("probability_sum").restype = C.c_float
+    f("probability_sum").argtypes = [f32p, sz]
+    f("conditional_q15").restype = C.c_uint16
+    f("conditional_q15").argtypes = [C.c_float, C.c_float]
+    f("bf8l").argtypes = [f32p, sz, i8p, u16p]
+    f("qlinear").argtypes = [i8p, f32p, f32p, sz, sz, u16p, sz, u16p]
+    f("layer_norm").argtypes = [u16p, u16p, u16p, sz, u16p]
+    f("gelu").restype = C.c_uint16
+    f("gelu").argtypes = [C.c_uint16]
+    f("add_bf16").restype = C.c_uint16
+    f("add_bf16").argtypes = [C.c_uint16, C.c_uint16]
+    f("rotary").argtypes = [u16p, u16p, sz, u16p]
+    f("softmax").argtypes = [u16p, sz, u16p]
+    f("token_crc32").restype = C.c_uint32
+    f("token_crc32").argtypes = [u16p, sz]
+    f("exp_batch").argtypes = [f32p, sz, f32p]
+    f("bf16_batch").argtypes = [f32p, sz, u16p]
+
+
+class _Kernels:
+    """Kernel-level calls shared by the oracle and the compiled reference."""
+
+    def __init__(self, lib, prefix):
+        self.lib, self.prefix = lib, prefix
+        _declare(lib, prefix)
+
+    def _f(self, name):
+        return getattr(self.lib, self.prefix + name)
+
+    def _check(self, status):
+        if status:
+            raise OracleError(self._f("last_error")().decode())
+
+    def bf16(self, x: float) -> int:
+        return self._f("bf16")(x)
+
+    def exp(self, z: float) -> float:
+        return self._f("exp")(z)
+
+    def exp_batch(self, z):
+        z = np.ascontiguousarray(z, np.float32)
+        out = np.empty_like(z)
+        self._f("exp_batch")(ptr(z, C.c_float), z.size, ptr(out, C.c_float))
+        return out
+
+    def bf16_batch(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.shape, np.uint16)
+        self._f("bf16_batch")(ptr(x, C.c_float), x.size, ptr(out, C.c_uint16))
+        return out
+
+    def probability_sum(self, values) -> float:
+        v = np.ascontiguousarray(values, np.float32)
+        return self._f("probability_sum")(ptr(v, C.c_float), v.size)
+
+    def conditional_q15(self, left: float, mass: float) -> int:
+        return self._f("conditional_q15")(left, mass)
+
+    def bf8l(self, values):
+        v = np.ascontiguousarray(values, np.float32)
+        q = np.zeros(v.size, np.int8)
+        s = np.zeros(v.size // 256 if v.size % 256 == 0 else 1, np.uint16)
+        self._check(self._f("bf8l")(ptr(v, C.c_float), v.size, ptr(q, C.c_int8), ptr(s, C.c_uint16)))
+        return q, s
+
+    def qlinear(self, weights, scales, bias, x):
+        n, k = weights.shape
+        x = np.ascontiguousarray(x, np.uint16).reshape(-1, k)
+        y = np.zeros((x.shape[0], n), np.uint16)
+        self._check(self._f("qlinear")(
+            ptr(np.ascontiguousarray(weights), C.c_int8), ptr(np.ascontiguousarray(scales), C.c_float),
+            ptr(np.ascontiguousarray(bias), C.c_float), k, n, ptr(x, C.c_uint16), x.shape[0],
+            ptr(y, C.c_uint16)))
+        return y
+
+    def layer_norm(self, x, gain, bias):
+        x = np.ascontiguousarray(x, np.uint16)
+        out = np.zeros_like(x)
+        self._check(self._f("layer_norm")(ptr(x, C.c_uint16), ptr(np.ascontiguousarray(gain), C.c_uint16),
+                                          ptr(np.ascontiguousarray(bias), C.c_uint16), x.size,
+                                          ptr(out, C.c_uint16)))
+        return out
+
+    def gelu(self, x: int) -> int:
+        return self._f("gelu")(x)
+
+    def add_bf16(self, a: int, b: int) -> int:
+        return self._f("add_bf16")(a, b)
+
+    def rotary(self, values, coefficients):
+        v = np.ascontiguousarray(values, np.uint16)
+        out = np.zeros_like(v)
+        self._check(self._f("rotary")(ptr(v, C.c_uint16),
+                                      ptr(np.ascontiguousarray(coefficients, np.uint16), C.c_uint16),
+                                      v.size, ptr(out, C.c_uint16)))
+        return out
+
+    def softmax(self, x):
+        x = np.ascontiguousarray(x, np.uint16)
+        out = np.zeros_like(x)
+        self._check(self._f("softmax")(ptr(x, C.c_uint16), x.size, ptr(out, C.c_uint16)))
+        return out
+
+    def token_crc32(self, tokens) -> int:
+        t = np.ascontiguousarray(tokens, np.uint16)
+        return self._f("token_crc32")(ptr(t, C.c_uint16), t.size)
+
+
+def model_desc(model):
+    """Builds a ModelDesc over the numpy arrays of a tsac_hip.synthetic.Model.
+    The returned tuple keeps every array alive while the descriptor is used."""
+    g = model.geometry
+    geometry = Geometry(g.width, g.heads, g.head_width, g.ffn, g.temporal_layers,
+                        g.codebook_layers, g.latent, g.alphabet, g.books, g.channels, g.context,
+                        g.attention_scale)
+    keep = []
+    linears = (Linear * len(model.projections))()
+    for i, (values, scales, bias) in enumerate(model.projections):
+        values, scales, bias = (np.ascontiguousarray(a) for a in (values, scales, bias))
+        keep += [values, scales, bias]
+        linears[i] = Linear(ptr(values, C.c_int8), ptr(scales, C.c_float), ptr(bias, C.c_float))
+    gains = (u16p * len(model.norm_gain))(*[ptr(np.ascontiguousarray(a), C.c_uint16) for a in model.norm_gain])
+    biases = (u16p * len(model.norm_bias))(*[ptr(np.ascontiguousarray(a), C.c_uint16) for a in model.norm_bias])
+    keep += [model.norm_gain, model.norm_bias, linears, gains, biases]
+    desc = ModelDesc(geometry, linears, gains, biases, ptr(model.positions, C.c_uint16),
+                     ptr(model.rotations, C.c_uint16), ptr(model.embeddings, C.c_uint16))
+    return desc, keep
+
+
+def header(frames, batch, groups, codebooks, model_channels=2, method=1) -> Header:
+    return Header(method, groups, model_channels, codebooks, frames, batch)
+
+
+class Oracle(_Kernels):
+    def __init__(self):
+        lib = _load(ORACLE_PATH)
+        super().__init__(lib, "orc_")
+        lib.orc_attention.argtypes = [u16p, u16p, u16p, sz, sz, sz, C.c_float, C.c_int, u16p]
+        lib.orc_gelu_batch.argtypes = [u16p, sz, u16p]
+        lib.orc_range_roundtrip_encode.argtypes = [f32p, u16p, sz, sz, u8p, sz, C.POINTER(sz)]
+        lib.orc_range_roundtrip_decode.argtypes = [f32p, sz, sz, u8p, sz, u16p]
+        lib.orc_parse_header.argtypes = [u8p, sz, C.POINTER(Header), C.POINTER(sz), C.POINTER(sz),
+                                         C.POINTER(C.c_uint32)]
+        lib.orc_model_create.argtypes = [C.POINTER(ModelDesc), C.POINTER(C.c_void_p)]
+        lib.orc_model_destroy.argtypes = [C.c_void_p]
+        lib.orc_backend_reset.argtypes = [C.c_void_p, C.POINTER(Header), sz]
+        lib.orc_backend_reset_temporal.argtypes = [C.c_void_p, sz]
+        lib.orc_backend_temporal_step.argtypes = [C.c_void_p, sz, sz, u16p, sz, C.c_int]
+        lib.orc_backend_reset_codebook.argtypes = [C.c_void_p, sz]
+        lib.orc_backend_codebook_step.argtypes = [C.c_void_p, sz, sz, u16p, sz, u16p]
+        lib.orc_pack_normal.argtypes = [C.c_void_p, C.POINTER(Header), u16p, sz, C.c_uint,
+                                        C.POINTER(u8p), C.POINTER(sz)]
+        lib.orc_unpack_normal.argtypes = [C.c_void_p, u8p, sz, C.c_uint, C.POINTER(u16p),
+                                          C.POINTER(sz)]
+        lib.orc_distributions_prefix.argtypes = [C.c_void_p, C.POINTER(Header), u16p, sz, C.c_uint,
+                                                 sz, u16p]
+        lib.orc_free.argtypes = [C.c_void_p]
+
+    def gelu_batch(self, x):
+        x = np.ascontiguousarray(x, np.uint16)
+        out = np.empty_like(x)
+        self.lib.orc_gelu_batch(ptr(x, C.c_uint16), x.size, ptr(out, C.c_uint16))
+        return out
+
+    def attention(self, q, k, v, heads, head_width, scale, prefill=False):
+        q, k, v = (np.ascontiguousarray(a, np.uint16) for a in (q, k, v))
+        width = heads * head_width
+        out = np.zeros(width, np.uint16)
+        self._check(self.lib.orc_attention(ptr(q, C.c_uint16), ptr(k, C.c_uint16), ptr(v, C.c_uint16),
+                                           k.size // width, heads, head_width, scale, int(prefill),
+                                           ptr(out, C.c_uint16)))
+        return out
+
+    def range_encode(self, probabilities, symbols):
+        p = np.ascontiguousarray(probabilities, np.float32)
+        s = np.ascontiguousarray(symbols, np.uint16)
+        out = np.zeros(64 + 4 * p.size, np.uint8)
+        n = sz()
+        self._check(self.lib.orc_range_roundtrip_encode(ptr(p, C.c_float), ptr(s, C.c_uint16), s.size,
+                                                        p.shape[-1], ptr(out, C.c_uint8), out.size,
+                                                        C.byref(n)))
+        return out[:n.value].tobytes()
+
+    def range_decode(self, probabilities, data: bytes):
+        p = np.ascontiguousarray(probabilities, np.float32)
+        count = p.shape[0]
+        b = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+        out = np.zeros(count, np.uint16)
+        self._check(self.lib.orc_range_roundtrip_decode(ptr(p, C.c_float), count, p.shape[-1],
+                                                        ptr(b, C.c_uint8), len(data),
+                                                        ptr(out, C.c_uint16)))
+        return out
+
+    def parse_header(self, data: bytes):
+        b = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+        h, off, n, crc = Header(), sz(), sz(), C.c_uint32()
+        self._check(self.lib.orc_parse_header(ptr(b, C.c_uint8), len(data), C.byref(h), C.byref(off),
+                                              C.byref(n), C.byref(crc)))
+        return h, off.value, n.value, crc.value
+
+    def model(self, model) -> "OracleModel":
+        return OracleModel(self, model)
+
+
+class OracleModel:
+    def __init__(self, oracle: Oracle, model):
+        self.oracle, self.lib = oracle, oracle.lib
+        self.model = model
+        self.desc, self._keep = model_desc(model)
+        self.handle = C.c_void_p()
+        oracle._check(self.lib.orc_model_create(C.byref(self.desc), C.byref(self.handle)))
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            self.lib.orc_model_destroy(self.handle)
+            self.handle = None
+
+    def pack_normal(self, h: Header, tokens, threads=1) -> bytes:
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out, n = u8p(), sz()
+        self.oracle._check(self.lib.orc_pack_normal(self.handle, C.byref(h), ptr(t, C.c_uint16), t.size,
+                                                    threads, C.byref(out), C.byref(n)))
+        data = C.string_at(out, n.value)
+        self.lib.orc_free(out)
+        return data
+
+    def unpack_normal(self, data: bytes, threads=1) -> np.ndarray:
+        b = np.frombuffer(data, np.uint8).copy()
+        out, n = u16p(), sz()
+        self.oracle._check(self.lib.orc_unpack_normal(self.handle, ptr(b, C.c_uint8), len(data),
+                                                      threads, C.byref(out), C.byref(n)))
+        tokens = np.ctypeslib.as_array(out, shape=(n.value,)).copy() if n.value else np.zeros(0, np.uint16)
+        self.lib.orc_free(out)
+        return tokens
+
+    def distributions(self, h: Header, tokens, threads=1, max_symbols=None) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out = np.zeros((t.size, self.model.geometry.alphabet), np.uint16)
+        limit = C.c_size_t(-1).value if max_symbols is None else max_symbols
+        self.oracle._check(self.lib.orc_distributions_prefix(self.handle, C.byref(h), ptr(t, C.c_uint16),
+                                                             t.size, threads, limit, ptr(out, C.c_uint16)))
+        return out
+
+    # TransformerBackend surface
+    def reset(self, h: Header, lanes: int):
+        self.oracle._check(self.lib.orc_backend_reset(self.handle, C.byref(h), lanes))
+
+    def reset_temporal(self, lane):
+        self.oracle._check(self.lib.orc_backend_reset_temporal(self.handle, lane))
+
+    def temporal_step(self, lane, position, feedback, replay=False):
+        f = np.ascontiguousarray(feedback, np.uint16)
+        self.oracle._check(self.lib.orc_backend_temporal_step(self.handle, lane, position,
+                                                              ptr(f, C.c_uint16), f.size, int(replay)))
+
+    def reset_codebook(self, lane):
+        self.oracle._check(self.lib.orc_backend_reset_codebook(self.handle, lane))
+
+    def codebook_step(self, lane, book, prefix):
+        p = np.ascontiguousarray(prefix, np.uint16) if len(prefix) else np.zeros(1, np.uint16)
+        out = np.zeros(self.model.geometry.alphabet, np.uint16)
+        self.oracle._check(self.lib.orc_backend_codebook_step(self.handle, lane, book, ptr(p, C.c_uint16),
+                                                              len(prefix), ptr(out, C.c_uint16)))
+        return out
+
+
+class Reference(_Kernels):
+    """The reference's own scalar sources (compiled here from the reference tree)."""
+
+    def __init__(self):
+        lib = _load(REF_PATH)
+        super().__init__(lib, "ref_")
+        lib.ref_gelu_table.argtypes = [u16p, sz]
+        lib.ref_attention.argtypes = [u16p, u16p, u16p, sz, sz, sz, C.c_float, C.c_int, u16p]
+        lib.ref_range_encode.argtypes = [f32p, u16p, sz, sz, u8p, sz, C.POINTER(sz)]
+        lib.ref_pack_normal.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u8p, sz,
+                                        C.POINTER(sz)]
+        lib.ref_unpack_normal.argtypes = [C.POINTER(ModelDesc), u8p, sz, u16p, sz, C.POINTER(sz)]
+        lib.ref_distributions.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u16p]
+
+    @staticmethod
+    def available() -> bool:
+        return REF_PATH.exists()
+
+    def gelu_table(self, values):
+        v = np.ascontiguousarray(values, np.uint16).copy()
+        self.lib.ref_gelu_table(ptr(v, C.c_uint16), v.size)
+        return v
+
+    def attention(self, q, k, v, heads, head_width, scale, prefill=False):
+        q, k, v = (np.ascontiguousarray(a, np.uint16) for a in (q, k, v))
+        width = heads * head_width
+        out = np.zeros(width, np.uint16)
+        self._check(self.lib.ref_attention(ptr(q, C.c_uint16), ptr(k, C.c_uint16), ptr(v, C.c_uint16),
+                                           k.size // width, heads, head_width, scale, int(prefill),
+                                           ptr(out, C.c_uint16)))
+        return out
+
+    def range_encode(self, probabilities, symbols):
+        p = np.ascontiguousarray(probabilities, np.float32)
+        s = np.ascontiguousarray(symbols, np.uint16)
+        out = np.zeros(64 + 4 * p.size, np.uint8)
+        n = sz()
+        self._check(self.lib.ref_range_encode(ptr(p, C.c_float), ptr(s, C.c_uint16), s.size,
+                                              p.shape[-1], ptr(out, C.c_uint8), out.size, C.byref(n)))
+        return out[:n.value].tobytes()
+
+    def pack_normal(self, model, h: Header, tokens) -> bytes:
+        desc, keep = model_desc(model)
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out = np.zeros(1 << 22, np.uint8)
+        n = sz()
+        self._check(self.lib.ref_pack_normal(C.byref(desc), C.byref(h), ptr(t, C.c_uint16), t.size,
+                                             ptr(out, C.c_uint8), out.size, C.byref(n)))
+        return out[:n.value].tobytes()
+
+    def unpack_normal(self, model, data: bytes, capacity: int) -> np.ndarray:
+        desc, keep = model_desc(model)
+        b = np.frombuffer(data, np.uint8).copy()
+        out = np.zeros(max(capacity, 1), np.uint16)
+        n = sz()
+        self._check(self.lib.ref_unpack_normal(C.byref(desc), ptr(b, C.c_uint8), len(data),
+                                               ptr(out, C.c_uint16), out.size, C.byref(n)))
+        return out[:n.value]
+
+    def distributions(self, model, h: Header, tokens) -> np.ndarray:
+        desc, keep = model_desc(model)
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out = np.zeros((t.size, model.geometry.alphabet), np.uint16)
+        self._check(self.lib.ref_distributions(C.byref(desc), C.byref(h), ptr(t, C.c_uint16), t.size,
+                                               ptr(out, C.c_uint16)))
+        return out
+
+
+def host_threads() -> int:
+    return len(os.sched_getaffinity(0))
