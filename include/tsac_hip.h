@@ -1,0 +1,206 @@
+/*
+ * tsac_hip: the TSAC probability model on AMD Instinct MI355X (gfx950).
+ *
+ * A C ABI with plain pointers and sizes. Every function returns 0 on success or
+ * a nonzero status; tsac_hip_last_error() then names the failed requirement (a
+ * thread-local string). No C++ exception crosses this boundary. Sessions stay
+ * usable after any failure.
+ *
+ * Each entry point names the reference interface it replaces (paths relative to
+ * the skimmilk/tsac-metal tree).
+ */
+#ifndef TSAC_HIP_H
+#define TSAC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSAC_HIP_OK 0
+#define TSAC_HIP_ERROR 1
+
+/* Message of the calling thread's last failure ("" after success). */
+const char* tsac_hip_last_error(void);
+
+/* ---- model description (host memory, borrowed during creation) -------------
+ * Geometry of the two-stack model; the reference fixes width 512, 4x128 heads,
+ * FFN 2048, 12 temporal + 3 codebook layers, latent 1024, alphabet 1024,
+ * context 1024 (src/models/config.hpp:11-16). */
+typedef struct tsac_hip_geometry
+{
+    uint32_t width, heads, head_width, ffn;
+    uint32_t temporal_layers, codebook_layers;
+    uint32_t latent, alphabet, books, channels, context;
+    float attention_scale; /* 0.0883883461356163f for 128-wide heads */
+} tsac_hip_geometry;
+
+/* LinearWeights (src/models/types.hpp:44-48): int8 values [N][K] (input
+ * fastest), fp32 block scales [K/256][N], fp32 bias [N]. */
+typedef struct tsac_hip_linear
+{
+    const int8_t* values;
+    const float* scales;
+    const float* bias;
+} tsac_hip_linear;
+
+/* TransformerModel accessors (src/models/transformer_model.hpp:6-29).
+ * projections: temporal 4L+{qkv, attn_out, mlp_in, mlp_out}, codebook
+ * 4*Lt+4L+{...}, then temporal cb_proj, codebook cb_proj, proj_f
+ * (src/models/contract.cpp:88-110,195-199). norms: temporal 2L+{ln_1, ln_2},
+ * 2*Lt = ln_f, codebook 2*Lt+1+2L+{...}, 2*Lt+1+2*Lc = ln_f (contract.cpp:201-211). */
+typedef struct tsac_hip_model_desc
+{
+    tsac_hip_geometry geometry;
+    const tsac_hip_linear* projections;
+    const uint16_t* const* norm_gain; /* BF16 [width] each */
+    const uint16_t* const* norm_bias;
+    const uint16_t* positions;  /* BF16 [books][width] (codebook_decoder.wpe) */
+    const uint16_t* rotations;  /* BF16 [context][head_width] interleaved (cos, sin) */
+    const uint16_t* embeddings; /* BF16 [books][alphabet][latent] feedback embeddings */
+} tsac_hip_model_desc;
+
+/* Policy limits (include/tsac/types.hpp:21-31); a zero field takes the
+ * reference default. */
+typedef struct tsac_hip_limits
+{
+    uint64_t file_bytes, symbols, pcm_bytes, cache_bytes, tensor_elements;
+} tsac_hip_limits;
+
+/* Header (src/format/container.hpp:10-25). */
+typedef struct tsac_hip_header
+{
+    uint8_t method, groups, model_channels, codebooks;
+    uint64_t frames;
+    uint16_t batch;
+} tsac_hip_header;
+
+typedef struct tsac_hip_model tsac_hip_model;
+typedef struct tsac_hip_session tsac_hip_session;
+
+/* ---- model and sessions (src/metal/transformer.hpp:13-39) ------------------ */
+
+/* MetalTransformer::from_model (src/metal/transformer.hpp:16): validates the
+ * description, uploads and re-lays out the weights on the current HIP device.
+ * The description's host memory may be released after return. */
+int tsac_hip_model_create(const tsac_hip_model_desc* desc, const tsac_hip_limits* limits,
+                          tsac_hip_model** model);
+/* Destroys the model; every session created from it must be destroyed first. */
+void tsac_hip_model_destroy(tsac_hip_model* model);
+
+/* MetalTransformer::new_session (src/metal/transformer.hpp:24): independent
+ * mutable state (caches, scratch, stream) sharing the immutable model. One
+ * caller at a time per session; separate sessions may run concurrently. */
+int tsac_hip_session_create(tsac_hip_model* model, tsac_hip_session** session);
+void tsac_hip_session_destroy(tsac_hip_session* session);
+/* MetalTransformer::clear_session (src/metal/transformer.hpp:27): releases
+ * caches and scratch, keeps the model; the next call recreates them. */
+int tsac_hip_session_clear(tsac_hip_session* session);
+
+/* MetalTransformer::encode (src/metal/transformer.hpp:30): normal framing of
+ * `count` tokens laid out [frame][group][book] (count must equal
+ * frames*groups*codebooks). Writes a library-allocated FBAZ stream; release it
+ * with tsac_hip_free. Identical bytes to the reference's pack_normal. */
+int tsac_hip_encode(tsac_hip_session* session, const tsac_hip_header* header,
+                    const uint16_t* tokens, size_t count, uint8_t** stream, size_t* length);
+
+/* MetalTransformer::decode (src/metal/transformer.hpp:33): decodes an FBAZ
+ * normal stream to library-allocated tokens (release with tsac_hip_free);
+ * verifies the token CRC before returning (src/format/entropy.cpp:153). */
+int tsac_hip_decode(tsac_hip_session* session, const uint8_t* stream, size_t length,
+                    uint16_t** tokens, size_t* count);
+
+void tsac_hip_free(void* pointer);
+
+/* Teacher-forced probability-model outputs: the BF16 distribution the model
+ * assigns to every token position (out: host [count][alphabet]), i.e. what
+ * TransformerPredictor::predict returns (src/common/transformer.cpp:137-182).
+ * mode 0 = encode-side pass (all frames known; causal GEMM/prefill shapes),
+ * mode 1 = decode-side pass (frame by frame, book by book; GEMV shapes). The
+ * two modes return identical bits. */
+#define TSAC_HIP_PASS_ENCODE 0
+#define TSAC_HIP_PASS_DECODE 1
+int tsac_hip_distributions(tsac_hip_session* session, const tsac_hip_header* header,
+                           const uint16_t* tokens, size_t count, int mode, uint16_t* out);
+
+/* Wall-clock split of the session's last encode/decode/distributions call
+ * (seconds): [0] GPU model work, [1] host range coding, [2] total. */
+int tsac_hip_session_timing(const tsac_hip_session* session, double* seconds, size_t count);
+
+/* ---- operators on device memory (hipStream_t passed as void*) -------------- */
+
+typedef struct tsac_hip_device_linear tsac_hip_device_linear;
+
+/* PackedLinear::from_weights (src/common/packed_linear.tpp:216-253): copies one
+ * projection (host memory) to the current device. */
+int tsac_hip_linear_create(const tsac_hip_linear* weights, size_t K, size_t N,
+                           tsac_hip_device_linear** linear);
+void tsac_hip_linear_destroy(tsac_hip_device_linear* linear);
+
+/* path: 0 automatic (GEMV for M <= 8, else MFMA GEMM), 1 GEMV, 2 GEMM. */
+#define TSAC_HIP_PATH_AUTO 0
+#define TSAC_HIP_PATH_GEMV 1
+#define TSAC_HIP_PATH_GEMM 2
+
+/* PackedLinear::apply_into (src/common/packed_linear.tpp:264-302) on device
+ * memory: x [M][K] BF16 -> y [M][N] BF16. Quantisation scratch comes from the
+ * stream-ordered allocator on `stream`. */
+int tsac_hip_linear_apply(const tsac_hip_device_linear* linear, const uint16_t* x, size_t M,
+                          uint16_t* y, int path, void* stream);
+
+/* The same product on activations already in BF8L form (q [M][K] int8, scales
+ * [M][K/256] fp32 widened from BF16), with an optional BF16 residual [M][N]
+ * added after rounding (bf16(residual + y), src/scalar/probability.cpp:6-14);
+ * residual may alias y. Launches exactly one kernel and allocates nothing. */
+int tsac_hip_linear_apply_quantized(const tsac_hip_device_linear* linear, const int8_t* q,
+                                    const float* scales, size_t M, uint16_t* y,
+                                    const uint16_t* residual, int path, void* stream);
+
+/* scalar::bf8l (src/scalar/probability.cpp:16-40) on rows of K BF16 values,
+ * K in {256, 512, 1024, 2048, 4096}. Fails if any input is not finite. */
+int tsac_hip_bf8l(const uint16_t* x, size_t rows, size_t K, int8_t* q, float* scales,
+                  void* stream);
+
+/* probability_layer_norm_bf16_into (src/common/probability.cpp:138-169), rows
+ * of `width` in {256, 512, 1024, 2048}. */
+int tsac_hip_layer_norm(const uint16_t* x, size_t rows, size_t width, const uint16_t* gain,
+                        const uint16_t* bias, uint16_t* out, void* stream);
+
+/* probability_softmax_bf16_into (src/common/probability.cpp:96-122), rows of
+ * `width` in {256, 512, 1024, 2048}. Fails if any input is not finite. */
+int tsac_hip_softmax(const uint16_t* x, size_t rows, size_t width, uint16_t* out, void* stream);
+
+/* probability_gelu_bf16 (src/common/probability.cpp:45-85) elementwise. */
+int tsac_hip_gelu(const uint16_t* x, size_t count, uint16_t* out, void* stream);
+
+/* probability_rotary_bf16_into (src/common/probability.cpp:24-43). */
+int tsac_hip_rotary(const uint16_t* x, const uint16_t* coefficients, size_t count, uint16_t* out,
+                    void* stream);
+
+/* scalar::add_bf16 (src/scalar/probability.cpp:6-14): out = bf16(a + b[row % period]). */
+int tsac_hip_add(const uint16_t* a, const uint16_t* b, size_t rows, size_t width, size_t period,
+                 uint16_t* out, void* stream);
+
+/* scalar::attention_bf16_into (src/scalar/attention.cpp:117-131) for
+ * `sequences` independent queries: query [sequences][heads*head_width], keys and
+ * values of sequence s at + s*sequence_stride elements, rows of heads*head_width.
+ * head_width in {64, 128}. Scratch from the stream-ordered allocator. */
+int tsac_hip_attention(const uint16_t* query, const uint16_t* keys, const uint16_t* values,
+                       size_t sequence_stride, size_t sequences, size_t time, size_t heads,
+                       size_t head_width, float scale, int prefill, uint16_t* out, void* stream);
+
+/* Every query of causal sequences at once (the encode-side shape of the same
+ * arithmetic): qkv [rows][3*heads*head_width]; sequence s = rows start[s] ..
+ * start[s]+length[s]-1 (device int arrays), its first replay[s] positions use
+ * replay rounding; rotations [position][head_width] or NULL. */
+int tsac_hip_attention_causal(const uint16_t* qkv, size_t heads, size_t head_width,
+                              const int* start, const int* length, const int* replay,
+                              size_t sequences, size_t max_length, const uint16_t* rotations,
+                              float scale, uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

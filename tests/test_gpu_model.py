@@ -1,0 +1,164 @@
+"""Whole-model parity on the MI355X through the C ABI: the encode-side pass
+(GEMM/prefill shapes) and the decode-side pass (GEMV/step shapes) return the
+oracle's distributions bit for bit, encode writes the oracle's bytes, decode
+recovers the tokens."""
+import numpy as np
+import pytest
+
+from tsac_hip.synthetic import WIDE, Geometry, bf16_float, pattern_tokens, random_model, random_tokens
+
+pytestmark = pytest.mark.gpu
+
+SMALL = Geometry(width=256, heads=2, head_width=128, ffn=512, temporal_layers=2, codebook_layers=1,
+                 latent=256)
+TINY = Geometry(width=256, heads=2, head_width=128, ffn=256, temporal_layers=1, codebook_layers=1,
+                latent=256)
+
+
+@pytest.fixture(scope="module")
+def native():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    from tsac_hip import native
+
+    native.library()
+    return native
+
+
+@pytest.fixture(scope="module")
+def small(native):
+    model = random_model(SMALL, seed=3)
+    return model, native.HipModel(model)
+
+
+@pytest.fixture(scope="module")
+def reference_model(native):
+    model = random_model(seed=1)
+    return model, native.HipModel(model)
+
+
+def _both_passes(native, hip_model, h, tokens):
+    session = hip_model.session()
+    encode = session.distributions(h, tokens, native.PASS_ENCODE)
+    decode = session.distributions(h, tokens, native.PASS_DECODE)
+    return encode, decode
+
+
+@pytest.mark.parametrize("frames,batch,groups,books", [(17, 3, 1, 12), (35, 3, 2, 12), (17, 8, 16, 12),
+                                                       (3, 8, 2, 12), (5, 3, 1, 7), (17, 1, 1, 12)])
+def test_small_model_passes_match_oracle(native, oracle, small, frames, batch, groups, books):
+    model, hip_model = small
+    h = native.header(frames, batch, groups, books)
+    tokens = pattern_tokens(frames * groups * books)
+    encode, decode = _both_passes(native, hip_model, h, tokens)
+    from oracle import header
+
+    expected = oracle.model(model).distributions(header(frames, batch, groups, books), tokens, threads=4)
+    assert np.array_equal(encode, decode), "encode-side and decode-side passes differ"
+    assert np.array_equal(encode, expected)
+
+
+@pytest.mark.parametrize("frames,batch,groups", [(17, 3, 1), (101, 3, 1), (35, 3, 2), (3, 8, 2)])
+def test_stream_bytes_and_round_trip(native, oracle, small, frames, batch, groups):
+    """GPU encode == oracle pack_normal bytes; GPU decode recovers the tokens."""
+    model, hip_model = small
+    h = native.header(frames, batch, groups, 12)
+    tokens = random_tokens(frames, groups, 12, seed=frames)
+    session = hip_model.session()
+    stream = session.encode(h, tokens)
+    from oracle import header
+
+    assert stream == oracle.model(model).pack_normal(header(frames, batch, groups, 12), tokens, threads=4)
+    assert np.array_equal(session.decode(stream), tokens)
+
+
+def test_rollover_replay(native, oracle):
+    """1026 frames in one lane: context reset with the 256-frame replay."""
+    model = random_model(TINY, seed=5)
+    hip_model = native.HipModel(model)
+    h = native.header(1026, 1, 1, 1)
+    tokens = pattern_tokens(1026)
+    session = hip_model.session()
+    stream = session.encode(h, tokens)
+    from oracle import header
+
+    assert stream == oracle.model(model).pack_normal(header(1026, 1, 1, 1), tokens)
+    assert np.array_equal(session.decode(stream), tokens)
+    encode, decode = _both_passes(native, hip_model, h, tokens)
+    assert np.array_equal(encode, decode)
+
+
+def test_reference_geometry(native, oracle, reference_model):
+    """Full reference geometry: 12 + 3 layers, width 512, 4 x 128 heads."""
+    model, hip_model = reference_model
+    h = native.header(6, 3, 1, 12)
+    tokens = random_tokens(6, 1, 12, seed=9)
+    encode, decode = _both_passes(native, hip_model, h, tokens)
+    from oracle import header
+
+    oh = header(6, 3, 1, 12)
+    expected = oracle.model(model).distributions(oh, tokens, threads=3)
+    assert np.array_equal(encode, decode)
+    assert np.array_equal(encode, expected)
+    assert np.all(np.isfinite(bf16_float(encode)))
+    session = hip_model.session()
+    stream = session.encode(h, tokens)
+    assert stream == oracle.model(model).pack_normal(oh, tokens, threads=3)
+    assert np.array_equal(session.decode(stream), tokens)
+
+
+def test_wide_geometry(native, oracle):
+    """Width 1024, FFN 4096, 16 x 64 heads."""
+    model = random_model(WIDE, seed=2)
+    hip_model = native.HipModel(model)
+    h = native.header(2, 2, 1, 12)
+    tokens = random_tokens(2, 1, 12, seed=4)
+    encode, decode = _both_passes(native, hip_model, h, tokens)
+    from oracle import header
+
+    expected = oracle.model(model).distributions(header(2, 2, 1, 12), tokens, threads=2)
+    assert np.array_equal(encode, decode)
+    assert np.array_equal(encode, expected)
+
+
+def test_run_to_run_determinism(native, small):
+    _, hip_model = small
+    h = native.header(40, 3, 1, 12)
+    tokens = random_tokens(40, 1, 12, seed=1)
+    a, b = hip_model.session(), hip_model.session()
+    assert a.encode(h, tokens) == b.encode(h, tokens) == a.encode(h, tokens)
+    d1 = a.distributions(h, tokens, native.PASS_ENCODE)
+    assert np.array_equal(d1, b.distributions(h, tokens, native.PASS_ENCODE))
+
+
+def test_decode_rejects_corruption_and_session_recovers(native, small):
+    _, hip_model = small
+    h = native.header(9, 3, 1, 12)
+    tokens = pattern_tokens(9 * 12)
+    session = hip_model.session()
+    stream = bytearray(session.encode(h, tokens))
+    bad = bytearray(stream)
+    bad[-1] ^= 1
+    with pytest.raises(native.HipError, match="CRC"):
+        session.decode(bytes(bad))
+    bad = bytearray(stream)
+    bad[14] = 0xFF  # initial interval byte (tests/metal_optimized.cpp:607-630)
+    bad[15] = 0xFF
+    bad[16] = 0xFF
+    with pytest.raises(native.HipError):
+        session.decode(bytes(bad))
+    assert np.array_equal(session.decode(bytes(stream)), tokens)
+    session.clear()
+    assert np.array_equal(session.decode(bytes(stream)), tokens)
+
+
+def test_encode_validates_inputs(native, small):
+    _, hip_model = small
+    session = hip_model.session()
+    with pytest.raises(native.HipError, match="token count"):
+        session.encode(native.header(3, 1, 1, 12), np.zeros(5, np.uint16))
+    with pytest.raises(native.HipError, match="alphabet"):
+        session.encode(native.header(1, 1, 1, 1), np.array([1024], np.uint16))
+    with pytest.raises(native.HipError, match="codebook"):
+        session.encode(native.header(1, 1, 1, 13), np.zeros(13, np.uint16))

@@ -1,0 +1,393 @@
+// C ABI of the probability model (include/tsac_hip.h). Exceptions stop here and
+// become a nonzero status plus a thread-local message.
+#include "../../../include/tsac_hip.h"
+#include "runtime.hpp"
+
+#include <cstdlib>
+#include <cstring>
+#include <new>
+
+using namespace tsac_hip;
+
+struct tsac_hip_model
+{
+    std::shared_ptr<const Model> model;
+};
+
+struct tsac_hip_session
+{
+    std::unique_ptr<Session> session;
+};
+
+struct tsac_hip_device_linear
+{
+    DeviceBuffer values, constants;
+    DeviceLinear linear;
+};
+
+namespace
+{
+thread_local std::string last_error;
+
+template <class F> int guarded(F&& f)
+{
+    try
+    {
+        f();
+        last_error.clear();
+        return TSAC_HIP_OK;
+    }
+    catch (const std::bad_alloc&)
+    {
+        last_error = "out of host memory";
+    }
+    catch (const std::exception& e)
+    {
+        last_error = e.what();
+    }
+    return TSAC_HIP_ERROR;
+}
+
+hipStream_t as_stream(void* stream)
+{
+    return static_cast<hipStream_t>(stream);
+}
+
+Limits limits_of(const tsac_hip_limits* l)
+{
+    Limits r;
+    if (l)
+    {
+        r.file_bytes = l->file_bytes ? l->file_bytes : r.file_bytes;
+        r.symbols = l->symbols ? l->symbols : r.symbols;
+        r.pcm_bytes = l->pcm_bytes ? l->pcm_bytes : r.pcm_bytes;
+        r.cache_bytes = l->cache_bytes ? l->cache_bytes : r.cache_bytes;
+        r.tensor_elements = l->tensor_elements ? l->tensor_elements : r.tensor_elements;
+    }
+    return r;
+}
+
+Header header_of(const tsac_hip_header* h)
+{
+    require(h != nullptr, "missing header");
+    Header r;
+    r.method = h->method;
+    r.groups = h->groups;
+    r.model_channels = h->model_channels;
+    r.codebooks = h->codebooks;
+    r.frames = h->frames;
+    r.batch = h->batch;
+    return r;
+}
+
+template <class T> T* copy_out(const std::vector<T>& v)
+{
+    T* p = static_cast<T*>(std::malloc(v.empty() ? 1 : v.size() * sizeof(T)));
+    if (!p)
+    {
+        throw std::bad_alloc();
+    }
+    if (!v.empty())
+    {
+        std::memcpy(p, v.data(), v.size() * sizeof(T));
+    }
+    return p;
+}
+
+// Stream-ordered scratch for the operator entry points.
+struct AsyncScratch
+{
+    void* pointer = nullptr;
+    hipStream_t stream;
+    AsyncScratch(std::size_t bytes, hipStream_t s) : stream(s)
+    {
+        check_hip(hipMallocAsync(&pointer, bytes ? bytes : 256, s), "hipMallocAsync");
+    }
+    ~AsyncScratch()
+    {
+        (void)hipFreeAsync(pointer, stream);
+    }
+};
+
+LinearPath path_of(int path)
+{
+    require(path >= 0 && path <= 2, "invalid linear path");
+    return path == TSAC_HIP_PATH_GEMV ? LinearPath::gemv
+           : path == TSAC_HIP_PATH_GEMM ? LinearPath::gemm
+                                        : LinearPath::automatic;
+}
+} // namespace
+
+extern "C"
+{
+const char* tsac_hip_last_error(void)
+{
+    return last_error.c_str();
+}
+
+int tsac_hip_model_create(const tsac_hip_model_desc* desc, const tsac_hip_limits* limits,
+                          tsac_hip_model** model)
+{
+    return guarded(
+        [&]
+        {
+            require(desc && model, "missing argument");
+            const auto& d = desc->geometry;
+            Geometry g;
+            g.width = d.width;
+            g.heads = d.heads;
+            g.head_width = d.head_width;
+            g.ffn = d.ffn;
+            g.temporal_layers = d.temporal_layers;
+            g.codebook_layers = d.codebook_layers;
+            g.latent = d.latent;
+            g.alphabet = d.alphabet;
+            g.books = d.books;
+            g.channels = d.channels;
+            g.context = d.context;
+            g.attention_scale = d.attention_scale;
+            static_assert(sizeof(LinearHost) == sizeof(tsac_hip_linear));
+            auto m = std::make_shared<const Model>(
+                g, reinterpret_cast<const LinearHost*>(desc->projections), desc->norm_gain,
+                desc->norm_bias, desc->positions, desc->rotations, desc->embeddings, limits_of(limits));
+            *model = new tsac_hip_model{std::move(m)};
+        });
+}
+
+void tsac_hip_model_destroy(tsac_hip_model* model)
+{
+    delete model;
+}
+
+int tsac_hip_session_create(tsac_hip_model* model, tsac_hip_session** session)
+{
+    return guarded(
+        [&]
+        {
+            require(model && session, "missing argument");
+            *session = new tsac_hip_session{std::make_unique<Session>(model->model)};
+        });
+}
+
+void tsac_hip_session_destroy(tsac_hip_session* session)
+{
+    delete session;
+}
+
+int tsac_hip_session_clear(tsac_hip_session* session)
+{
+    return guarded(
+        [&]
+        {
+            require(session, "missing session");
+            session->session->clear();
+        });
+}
+
+int tsac_hip_encode(tsac_hip_session* session, const tsac_hip_header* header,
+                    const uint16_t* tokens, size_t count, uint8_t** stream, size_t* length)
+{
+    return guarded(
+        [&]
+        {
+            require(session && stream && length && (tokens || !count), "missing argument");
+            const auto bytes = session->session->encode(header_of(header), tokens, count);
+            *stream = copy_out(bytes);
+            *length = bytes.size();
+        });
+}
+
+int tsac_hip_decode(tsac_hip_session* session, const uint8_t* stream, size_t length,
+                    uint16_t** tokens, size_t* count)
+{
+    return guarded(
+        [&]
+        {
+            require(session && stream && tokens && count, "missing argument");
+            const auto t = session->session->decode(stream, length);
+            *tokens = copy_out(t);
+            *count = t.size();
+        });
+}
+
+void tsac_hip_free(void* pointer)
+{
+    std::free(pointer);
+}
+
+int tsac_hip_distributions(tsac_hip_session* session, const tsac_hip_header* header,
+                           const uint16_t* tokens, size_t count, int mode, uint16_t* out)
+{
+    return guarded(
+        [&]
+        {
+            require(session && out && (tokens || !count), "missing argument");
+            require(mode == TSAC_HIP_PASS_ENCODE || mode == TSAC_HIP_PASS_DECODE, "invalid pass");
+            session->session->distributions(header_of(header), tokens, count,
+                                            mode == TSAC_HIP_PASS_DECODE, out);
+        });
+}
+
+int tsac_hip_session_timing(const tsac_hip_session* session, double* seconds, size_t count)
+{
+    return guarded(
+        [&]
+        {
+            require(session && seconds, "missing argument");
+            const auto t = session->session->timing();
+            for (size_t i = 0; i < count && i < t.size(); ++i)
+            {
+                seconds[i] = t[i];
+            }
+        });
+}
+
+int tsac_hip_linear_create(const tsac_hip_linear* weights, size_t K, size_t N,
+                           tsac_hip_device_linear** linear)
+{
+    return guarded(
+        [&]
+        {
+            require(weights && linear && weights->values && weights->scales && weights->bias,
+                    "missing argument");
+            require(K >= 256 && K % 256 == 0 && N > 0, "invalid generated linear shape");
+            auto l = std::make_unique<tsac_hip_device_linear>();
+            l->values = DeviceBuffer(K * N);
+            const std::size_t scale_bytes = K / 256 * N * 4;
+            l->constants = DeviceBuffer((scale_bytes + 255) / 256 * 256 + N * 4);
+            auto* c = l->constants.as<uint8_t>();
+            check_hip(hipMemcpy(l->values.get(), weights->values, K * N, hipMemcpyHostToDevice), "upload");
+            check_hip(hipMemcpy(c, weights->scales, scale_bytes, hipMemcpyHostToDevice), "upload");
+            check_hip(hipMemcpy(c + (scale_bytes + 255) / 256 * 256, weights->bias, N * 4,
+                                hipMemcpyHostToDevice),
+                      "upload");
+            l->linear = {l->values.as<int8_t>(), reinterpret_cast<const float*>(c),
+                         reinterpret_cast<const float*>(c + (scale_bytes + 255) / 256 * 256), K, N};
+            *linear = l.release();
+        });
+}
+
+void tsac_hip_linear_destroy(tsac_hip_device_linear* linear)
+{
+    delete linear;
+}
+
+int tsac_hip_linear_apply(const tsac_hip_device_linear* linear, const uint16_t* x, size_t M,
+                          uint16_t* y, int path, void* stream)
+{
+    return guarded(
+        [&]
+        {
+            require(linear && (x || !M) && (y || !M), "missing argument");
+            const auto s = as_stream(stream);
+            const std::size_t K = linear->linear.K;
+            AsyncScratch scratch(M * K + M * (K / 256) * 4 + 256 + 8, s);
+            auto* q = static_cast<int8_t*>(scratch.pointer);
+            auto* scales = reinterpret_cast<float*>(static_cast<uint8_t*>(scratch.pointer) + (M * K + 255) / 256 * 256);
+            auto* error = reinterpret_cast<uint32_t*>(scales + M * (K / 256));
+            check_hip(hipMemsetAsync(error, 0, 8, s), "hipMemsetAsync");
+            quantize_rows(x, M, K, Prologue::none, nullptr, nullptr, q, scales, nullptr, error, s);
+            tsac_hip::linear(linear->linear, q, scales, M, y, nullptr, path_of(path), s);
+            uint32_t flags[2];
+            check_hip(hipMemcpyAsync(flags, error, 8, hipMemcpyDeviceToHost, s), "read error words");
+            check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+            require(!flags[0], "BF8L activations must be finite");
+        });
+}
+
+int tsac_hip_linear_apply_quantized(const tsac_hip_device_linear* linear, const int8_t* q,
+                                    const float* scales, size_t M, uint16_t* y,
+                                    const uint16_t* residual, int path, void* stream)
+{
+    return guarded(
+        [&]
+        {
+            require(linear && (q || !M) && (scales || !M) && (y || !M), "missing argument");
+            tsac_hip::linear(linear->linear, q, scales, M, y, residual, path_of(path), as_stream(stream));
+        });
+}
+
+int tsac_hip_bf8l(const uint16_t* x, size_t rows, size_t K, int8_t* q, float* scales, void* stream)
+{
+    return guarded(
+        [&]
+        {
+            const auto s = as_stream(stream);
+            AsyncScratch scratch(8, s);
+            auto* error = static_cast<uint32_t*>(scratch.pointer);
+            check_hip(hipMemsetAsync(error, 0, 8, s), "hipMemsetAsync");
+            quantize_rows(x, rows, K, Prologue::none, nullptr, nullptr, q, scales, nullptr, error, s);
+            uint32_t flags[2];
+            check_hip(hipMemcpyAsync(flags, error, 8, hipMemcpyDeviceToHost, s), "read error words");
+            check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+            require(!flags[0], "BF8L activations must be finite");
+        });
+}
+
+int tsac_hip_layer_norm(const uint16_t* x, size_t rows, size_t width, const uint16_t* gain,
+                        const uint16_t* bias, uint16_t* out, void* stream)
+{
+    return guarded([&] { layer_norm_rows(x, rows, width, gain, bias, out, as_stream(stream)); });
+}
+
+int tsac_hip_softmax(const uint16_t* x, size_t rows, size_t width, uint16_t* out, void* stream)
+{
+    return guarded(
+        [&]
+        {
+            const auto s = as_stream(stream);
+            AsyncScratch scratch(8, s);
+            auto* error = static_cast<uint32_t*>(scratch.pointer);
+            check_hip(hipMemsetAsync(error, 0, 8, s), "hipMemsetAsync");
+            softmax_rows(x, rows, width, out, error, s);
+            uint32_t flags[2];
+            check_hip(hipMemcpyAsync(flags, error, 8, hipMemcpyDeviceToHost, s), "read error words");
+            check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+            require(!flags[0], "softmax input must be finite");
+        });
+}
+
+int tsac_hip_gelu(const uint16_t* x, size_t count, uint16_t* out, void* stream)
+{
+    return guarded([&] { gelu_values(x, count, out, as_stream(stream)); });
+}
+
+int tsac_hip_rotary(const uint16_t* x, const uint16_t* coefficients, size_t count, uint16_t* out,
+                    void* stream)
+{
+    return guarded([&] { rotary_values(x, coefficients, count, out, as_stream(stream)); });
+}
+
+int tsac_hip_add(const uint16_t* a, const uint16_t* b, size_t rows, size_t width, size_t period,
+                 uint16_t* out, void* stream)
+{
+    return guarded([&] { add_rows(a, b, rows, width, period, out, as_stream(stream)); });
+}
+
+int tsac_hip_attention(const uint16_t* query, const uint16_t* keys, const uint16_t* values,
+                       size_t sequence_stride, size_t sequences, size_t time, size_t heads,
+                       size_t head_width, float scale, int prefill, uint16_t* out, void* stream)
+{
+    return guarded(
+        [&]
+        {
+            const auto s = as_stream(stream);
+            AsyncScratch scratch(decode_partial_floats(sequences, heads, head_width, time) * 4, s);
+            attention_decode(query, keys, values, sequence_stride, sequences, time, heads, head_width,
+                             scale, prefill != 0, static_cast<float*>(scratch.pointer), out, s);
+        });
+}
+
+int tsac_hip_attention_causal(const uint16_t* qkv, size_t heads, size_t head_width, const int* start,
+                              const int* length, const int* replay, size_t sequences,
+                              size_t max_length, const uint16_t* rotations, float scale,
+                              uint16_t* out, void* stream)
+{
+    return guarded(
+        [&]
+        {
+            attention_prefill(qkv, heads * head_width, heads, head_width, start, length, replay,
+                              sequences, max_length, rotations, scale, out, as_stream(stream));
+        });
+}
+}

@@ -1,0 +1,863 @@
+#include "runtime.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+
+namespace tsac_hip
+{
+namespace
+{
+constexpr std::size_t replay_frames = 256;
+// Rows processed per batched launch sequence; bounds scratch at roughly
+// rows * (3*width + ffn) * 2 bytes.
+constexpr std::size_t batch_rows = 65536;
+
+double now()
+{
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+std::size_t align_up(std::size_t n, std::size_t a)
+{
+    return (n + a - 1) / a * a;
+}
+
+bool supported_width(std::size_t k)
+{
+    return k == 256 || k == 512 || k == 1024 || k == 2048 || k == 4096;
+}
+} // namespace
+
+// ---------------------------------------------------------------- geometry
+
+std::pair<std::size_t, std::size_t> Geometry::projection_shape(std::size_t index) const
+{
+    const std::size_t stacked = 4 * std::size_t(temporal_layers + codebook_layers);
+    if (index == stacked || index == stacked + 1)
+    {
+        return {latent, width};
+    }
+    if (index == stacked + 2)
+    {
+        return {width, alphabet};
+    }
+    switch (index % 4)
+    {
+    case 0:
+        return {width, 3 * std::size_t(width)};
+    case 1:
+        return {width, width};
+    case 2:
+        return {width, ffn};
+    default:
+        return {ffn, width};
+    }
+}
+
+// ---------------------------------------------------------------- memory
+
+DeviceBuffer::DeviceBuffer(std::size_t bytes) : bytes_(bytes)
+{
+    if (bytes)
+    {
+        check_hip(hipMalloc(&data_, bytes), "hipMalloc");
+    }
+}
+
+DeviceBuffer::~DeviceBuffer()
+{
+    if (data_)
+    {
+        (void)hipFree(data_);
+    }
+}
+
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& other) noexcept : data_(other.data_), bytes_(other.bytes_)
+{
+    other.data_ = nullptr;
+    other.bytes_ = 0;
+}
+
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& other) noexcept
+{
+    if (this != &other)
+    {
+        if (data_)
+        {
+            (void)hipFree(data_);
+        }
+        data_ = other.data_;
+        bytes_ = other.bytes_;
+        other.data_ = nullptr;
+        other.bytes_ = 0;
+    }
+    return *this;
+}
+
+PinnedBuffer::~PinnedBuffer()
+{
+    if (data_)
+    {
+        (void)hipHostFree(data_);
+    }
+}
+
+void PinnedBuffer::reserve(std::size_t bytes)
+{
+    if (bytes <= bytes_)
+    {
+        return;
+    }
+    if (data_)
+    {
+        (void)hipHostFree(data_);
+        data_ = nullptr;
+    }
+    check_hip(hipHostMalloc(&data_, bytes, hipHostMallocDefault), "hipHostMalloc");
+    bytes_ = bytes;
+}
+
+void* Arena::get(const std::string& name, std::size_t bytes)
+{
+    auto& buffer = buffers_[name];
+    if (buffer.bytes() < bytes)
+    {
+        buffer = DeviceBuffer();
+        buffer = DeviceBuffer(align_up(std::max<std::size_t>(bytes, 256), 256));
+    }
+    return buffer.get();
+}
+
+// ---------------------------------------------------------------- model
+
+Model::Model(const Geometry& g, const LinearHost* projections, const uint16_t* const* gain,
+             const uint16_t* const* bias, const uint16_t* positions, const uint16_t* rotations,
+             const uint16_t* embeddings, const Limits& limits)
+    : g_(g), limits_(limits)
+{
+    require(g.width >= 256 && g.width <= 2048 && supported_width(g.width), "model width must be 256..2048, a power of two");
+    require(g.heads * g.head_width == g.width && (g.head_width == 64 || g.head_width == 128),
+            "heads x head width must equal width with 64- or 128-wide heads");
+    require(supported_width(g.ffn) && supported_width(g.latent), "ffn and latent widths must be 256..4096, powers of two");
+    require(g.alphabet == 1024, "the alphabet must hold 1024 symbols");
+    require(g.books >= 1 && g.books <= 12, "model codebooks must be 1..12");
+    require(g.channels == 1 || g.channels == 2, "model channels must be 1 or 2");
+    require(g.context >= replay_frames, "context must hold the 256-frame replay");
+    require(g.temporal_layers >= 1 && g.codebook_layers >= 1, "empty transformer stack");
+    require(projections && gain && bias && positions && rotations && embeddings, "missing model tensor");
+    check_hip(hipGetDevice(&device_), "hipGetDevice");
+
+    const std::size_t count = g.projections();
+    std::vector<std::size_t> value_offset(count), scale_offset(count), bias_offset(count);
+    std::size_t values_bytes = 0, constants_bytes = 0;
+    for (std::size_t i = 0; i < count; ++i)
+    {
+        const auto [k, n] = g.projection_shape(i);
+        require(projections[i].values && projections[i].scales && projections[i].bias,
+                "missing projection tensor");
+        value_offset[i] = values_bytes;
+        values_bytes += align_up(k * n, 256);
+        scale_offset[i] = constants_bytes;
+        constants_bytes += align_up(k / 256 * n * 4, 256);
+        bias_offset[i] = constants_bytes;
+        constants_bytes += align_up(n * 4, 256);
+    }
+    const std::size_t norm_bytes = align_up(std::size_t(g.width) * 2, 256);
+    const std::size_t norms_offset = constants_bytes;
+    constants_bytes += 2 * g.norms() * norm_bytes;
+    const std::size_t positions_offset = constants_bytes;
+    constants_bytes += align_up(std::size_t(g.books) * g.width * 2, 256);
+    const std::size_t rotations_offset = constants_bytes;
+    constants_bytes += align_up(std::size_t(g.context) * g.head_width * 2, 256);
+    const std::size_t embeddings_offset = constants_bytes;
+    constants_bytes += align_up(std::size_t(g.books) * g.alphabet * g.latent * 2, 256);
+
+    values_ = DeviceBuffer(values_bytes);
+    constants_ = DeviceBuffer(constants_bytes);
+    auto* values = values_.as<uint8_t>();
+    auto* constants = constants_.as<uint8_t>();
+    for (std::size_t i = 0; i < count; ++i)
+    {
+        const auto [k, n] = g.projection_shape(i);
+        check_hip(hipMemcpy(values + value_offset[i], projections[i].values, k * n, hipMemcpyHostToDevice),
+                  "upload weights");
+        check_hip(hipMemcpy(constants + scale_offset[i], projections[i].scales, k / 256 * n * 4,
+                            hipMemcpyHostToDevice),
+                  "upload scales");
+        check_hip(hipMemcpy(constants + bias_offset[i], projections[i].bias, n * 4, hipMemcpyHostToDevice),
+                  "upload bias");
+        projections_.push_back({reinterpret_cast<const int8_t*>(values + value_offset[i]),
+                                reinterpret_cast<const float*>(constants + scale_offset[i]),
+                                reinterpret_cast<const float*>(constants + bias_offset[i]), k, n});
+    }
+    for (std::size_t i = 0; i < g.norms(); ++i)
+    {
+        require(gain[i] && bias[i], "missing norm tensor");
+        uint8_t* gp = constants + norms_offset + 2 * i * norm_bytes;
+        uint8_t* bp = gp + norm_bytes;
+        check_hip(hipMemcpy(gp, gain[i], g.width * 2, hipMemcpyHostToDevice), "upload norm");
+        check_hip(hipMemcpy(bp, bias[i], g.width * 2, hipMemcpyHostToDevice), "upload norm");
+        gain_.push_back(reinterpret_cast<const uint16_t*>(gp));
+        bias_.push_back(reinterpret_cast<const uint16_t*>(bp));
+    }
+    check_hip(hipMemcpy(constants + positions_offset, positions, std::size_t(g.books) * g.width * 2,
+                        hipMemcpyHostToDevice),
+              "upload positions");
+    check_hip(hipMemcpy(constants + rotations_offset, rotations,
+                        std::size_t(g.context) * g.head_width * 2, hipMemcpyHostToDevice),
+              "upload rotations");
+    check_hip(hipMemcpy(constants + embeddings_offset, embeddings,
+                        std::size_t(g.books) * g.alphabet * g.latent * 2, hipMemcpyHostToDevice),
+              "upload embeddings");
+    positions_ = reinterpret_cast<const uint16_t*>(constants + positions_offset);
+    rotations_ = reinterpret_cast<const uint16_t*>(constants + rotations_offset);
+    embeddings_ = reinterpret_cast<const uint16_t*>(constants + embeddings_offset);
+}
+
+const DeviceLinear& Model::layer(bool temporal, std::size_t layer, int op) const
+{
+    return projections_.at((temporal ? 0 : 4 * std::size_t(g_.temporal_layers)) + 4 * layer + op);
+}
+
+const DeviceLinear& Model::temporal_projection() const
+{
+    return projections_.at(4 * std::size_t(g_.temporal_layers + g_.codebook_layers));
+}
+
+const DeviceLinear& Model::codebook_projection() const
+{
+    return projections_.at(4 * std::size_t(g_.temporal_layers + g_.codebook_layers) + 1);
+}
+
+const DeviceLinear& Model::output_projection() const
+{
+    return projections_.at(4 * std::size_t(g_.temporal_layers + g_.codebook_layers) + 2);
+}
+
+std::size_t Model::norm_index(bool temporal, std::size_t layer, bool mlp) const
+{
+    return (temporal ? 0 : 2 * std::size_t(g_.temporal_layers) + 1) + 2 * layer + (mlp ? 1 : 0);
+}
+
+std::size_t Model::final_norm_index(bool temporal) const
+{
+    return temporal ? 2 * std::size_t(g_.temporal_layers)
+                    : 2 * std::size_t(g_.temporal_layers) + 1 + 2 * std::size_t(g_.codebook_layers);
+}
+
+// ---------------------------------------------------------------- session
+
+Session::Session(std::shared_ptr<const Model> model) : model_(std::move(model))
+{
+    check_hip(hipSetDevice(model_->device()), "hipSetDevice");
+    check_hip(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    errors_ = DeviceBuffer(256);
+    pinned_errors_.reserve(256);
+}
+
+Session::~Session()
+{
+    if (stream_)
+    {
+        (void)hipStreamSynchronize(stream_);
+        (void)hipStreamDestroy(stream_);
+    }
+}
+
+void Session::clear()
+{
+    check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    arena_.clear();
+}
+
+void Session::reset_errors()
+{
+    check_hip(hipMemsetAsync(errors_.get(), 0, 8, stream_), "hipMemsetAsync");
+}
+
+void Session::check_errors()
+{
+    check_hip(hipMemcpyAsync(pinned_errors_.as<uint32_t>(), errors_.get(), 8, hipMemcpyDeviceToHost, stream_),
+              "read error words");
+    check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    const uint32_t* e = pinned_errors_.as<uint32_t>();
+    require(!(e[0] & error_nonfinite), "probability model activation is not finite");
+    require(!e[1], "invalid range decoder state");
+}
+
+// src/format/entropy.cpp:60-66, src/common/transformer.cpp:104-118 and
+// src/common/cpu_transformer.tpp:285-305.
+void Session::validate(const Header& h, const uint16_t* tokens, std::size_t count) const
+{
+    const Geometry& g = model_->geometry();
+    const Limits& limits = model_->limits();
+    validate_header(h, limits);
+    require(h.method == 1, "Transformer predictor requires normal framing");
+    require(h.frames <= 0xffffffffu, "normal frame count exceeds uint32");
+    require(count == h.symbols(), "normal token count does not match header");
+    require(h.model_channels == g.channels && h.codebooks <= g.books,
+            "Transformer stream/model mismatch");
+    if (tokens)
+    {
+        for (std::size_t i = 0; i < count; ++i)
+        {
+            require(tokens[i] < 1024, "index outside 10-bit alphabet");
+        }
+    }
+    const std::size_t independent = checked_mul(std::min<std::size_t>(h.batch, h.frames), h.groups);
+    require(independent <= limits.tensor_elements, "Transformer lane count exceeds limit");
+    const std::size_t base = h.frames / h.batch, extra = h.frames % h.batch;
+    const std::size_t contexts = checked_mul(
+        h.groups, checked_add(checked_mul(h.batch - extra, std::min<std::size_t>(base, g.context)),
+                              checked_mul(extra, std::min<std::size_t>(base + 1, g.context))));
+    const std::size_t temporal_bytes =
+        checked_mul(contexts, std::size_t(g.temporal_layers) * g.width * 2 * sizeof(uint16_t));
+    const std::size_t codebook_bytes = checked_mul(
+        checked_mul(independent, h.codebooks), std::size_t(g.codebook_layers) * g.width * 2 * sizeof(uint16_t));
+    require(checked_add(temporal_bytes, codebook_bytes) <= limits.cache_bytes,
+            "Transformer caches exceed byte limit; reduce the encoding batch size or channel count");
+}
+
+// One transformer stack over rows with causal prefill attention
+// (src/common/cpu_transformer.tpp:133-175, final norm left to the caller).
+void Session::stack_rows(bool temporal, uint16_t* x, std::size_t rows, const int* starts,
+                         const int* lengths, const int* replays, std::size_t sequences,
+                         std::size_t max_length, const std::string& tag)
+{
+    const Geometry& g = model_->geometry();
+    const Model& m = *model_;
+    const std::size_t w = g.width;
+    const std::size_t widest = std::max<std::size_t>({w, g.ffn, g.latent});
+    auto* q8 = arena_.get<int8_t>(tag + ".q8", rows * widest);
+    auto* s8 = arena_.get<float>(tag + ".s8", rows * widest / 256);
+    auto* qkv = arena_.get<uint16_t>(tag + ".qkv", rows * 3 * w);
+    auto* att = arena_.get<uint16_t>(tag + ".att", rows * w);
+    auto* hidden = arena_.get<uint16_t>(tag + ".hidden", rows * g.ffn);
+    auto* err = errors_.as<uint32_t>();
+    const std::size_t layers = temporal ? g.temporal_layers : g.codebook_layers;
+    for (std::size_t l = 0; l < layers; ++l)
+    {
+        const std::size_t n1 = m.norm_index(temporal, l, false), n2 = m.norm_index(temporal, l, true);
+        quantize_rows(x, rows, w, Prologue::layer_norm, m.norm_gain(n1), m.norm_bias(n1), q8, s8,
+                      nullptr, err, stream_);
+        linear(m.layer(temporal, l, 0), q8, s8, rows, qkv, nullptr, LinearPath::automatic, stream_);
+        attention_prefill(qkv, w, g.heads, g.head_width, starts, lengths, replays, sequences,
+                          max_length, temporal ? m.rotations() : nullptr, g.attention_scale, att,
+                          stream_);
+        quantize_rows(att, rows, w, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err, stream_);
+        linear(m.layer(temporal, l, 1), q8, s8, rows, x, x, LinearPath::automatic, stream_);
+        quantize_rows(x, rows, w, Prologue::layer_norm, m.norm_gain(n2), m.norm_bias(n2), q8, s8,
+                      nullptr, err, stream_);
+        linear(m.layer(temporal, l, 2), q8, s8, rows, hidden, nullptr, LinearPath::automatic, stream_);
+        quantize_rows(hidden, rows, g.ffn, Prologue::gelu, nullptr, nullptr, q8, s8, nullptr, err, stream_);
+        linear(m.layer(temporal, l, 3), q8, s8, rows, x, x, LinearPath::automatic, stream_);
+    }
+}
+
+// Temporal conditioning of every (frame, group) for known tokens: each lane's
+// context positions form causal sequences; a rollover starts a new sequence
+// with the last 256 complete frames replayed (src/common/transformer.cpp:184-211).
+void Session::temporal_rows(const Header& h, const uint16_t* tokens, uint16_t* conditioning)
+{
+    const Geometry& g = model_->geometry();
+    const Model& m = *model_;
+    const std::size_t C = h.codebooks, G = h.groups, w = g.width;
+    const Lanes lanes(h);
+    struct Sequence
+    {
+        std::size_t row, length, replay;
+    };
+    std::vector<uint16_t> feedback;
+    std::vector<Sequence> sequences;
+    std::vector<std::size_t> source_row(h.frames * G);
+    std::size_t rows = 0;
+    const auto add_row = [&](std::size_t frame_plus_one, std::size_t group)
+    {
+        // frame_plus_one == 0 feeds the all-zero indices of the first frame.
+        for (std::size_t b = 0; b < C; ++b)
+        {
+            feedback.push_back(frame_plus_one ? tokens[((frame_plus_one - 1) * G + group) * C + b] : 0);
+        }
+        return rows++;
+    };
+    for (std::size_t lane = 0; lane < lanes.count; ++lane)
+    {
+        for (std::size_t group = 0; group < G; ++group)
+        {
+            const std::size_t start = lanes.start(lane), length = lanes.length(lane);
+            Sequence current{rows, 0, 0};
+            std::size_t context_used = 0;
+            for (std::size_t s = 0; s < length; ++s)
+            {
+                if (context_used == g.context)
+                {
+                    sequences.push_back(current);
+                    current = {rows, 0, replay_frames};
+                    for (std::size_t k = 0; k < replay_frames; ++k)
+                    {
+                        add_row(start + s - replay_frames + k + 1, group);
+                    }
+                    current.length = replay_frames;
+                    context_used = replay_frames;
+                    source_row[(start + s) * G + group] = rows - 1;
+                }
+                else
+                {
+                    const std::size_t r = add_row(s == 0 ? 0 : start + s, group);
+                    ++current.length;
+                    ++context_used;
+                    source_row[(start + s) * G + group] = r;
+                }
+            }
+            sequences.push_back(current);
+        }
+    }
+    // Process whole sequences in batches of at most batch_rows rows.
+    auto* err = errors_.as<uint32_t>();
+    std::size_t first = 0;
+    while (first < sequences.size())
+    {
+        std::size_t last = first, batch = 0;
+        while (last < sequences.size() && (last == first || batch + sequences[last].length <= batch_rows))
+        {
+            batch += sequences[last].length;
+            ++last;
+        }
+        const std::size_t row0 = sequences[first].row;
+        const std::size_t count = last - first;
+        std::vector<int> info(3 * count);
+        std::size_t max_length = 0;
+        for (std::size_t i = 0; i < count; ++i)
+        {
+            info[i] = int(sequences[first + i].row - row0);
+            info[count + i] = int(sequences[first + i].length);
+            info[2 * count + i] = int(sequences[first + i].replay);
+            max_length = std::max(max_length, sequences[first + i].length);
+        }
+        std::vector<int> out_rows, out_index;
+        for (std::size_t step = 0; step < source_row.size(); ++step)
+        {
+            if (source_row[step] >= row0 && source_row[step] < row0 + batch)
+            {
+                out_rows.push_back(int(source_row[step] - row0));
+                out_index.push_back(int(step));
+            }
+        }
+        auto* d_feedback = arena_.get<uint16_t>("t.feedback", batch * C);
+        auto* d_info = arena_.get<int>("t.info", 3 * count);
+        auto* d_rows = arena_.get<int>("t.rows", std::max<std::size_t>(out_rows.size(), 1));
+        auto* d_index = arena_.get<int>("t.index", std::max<std::size_t>(out_index.size(), 1));
+        check_hip(hipMemcpyAsync(d_feedback, feedback.data() + row0 * C, batch * C * 2,
+                                 hipMemcpyHostToDevice, stream_),
+                  "upload feedback");
+        check_hip(hipMemcpyAsync(d_info, info.data(), info.size() * 4, hipMemcpyHostToDevice, stream_),
+                  "upload sequences");
+        check_hip(hipMemcpyAsync(d_rows, out_rows.data(), out_rows.size() * 4, hipMemcpyHostToDevice, stream_),
+                  "upload rows");
+        check_hip(hipMemcpyAsync(d_index, out_index.data(), out_index.size() * 4, hipMemcpyHostToDevice,
+                                 stream_),
+                  "upload rows");
+        auto* embedded = arena_.get<uint16_t>("t.embedded", batch * g.latent);
+        auto* x = arena_.get<uint16_t>("t.x", batch * w);
+        auto* q8 = arena_.get<int8_t>("t.q8", batch * std::max<std::size_t>({w, g.ffn, g.latent}));
+        auto* s8 = arena_.get<float>("t.s8", batch * std::max<std::size_t>({w, g.ffn, g.latent}) / 256);
+        embed_sum(m.embeddings(), g.alphabet, g.latent, d_feedback, C, batch, embedded, stream_);
+        quantize_rows(embedded, batch, g.latent, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err,
+                      stream_);
+        linear(m.temporal_projection(), q8, s8, batch, x, nullptr, LinearPath::automatic, stream_);
+        stack_rows(true, x, batch, d_info, d_info + count, d_info + 2 * count, count, max_length, "t");
+        const std::size_t f = m.final_norm_index(true);
+        layer_norm_rows(x, batch, w, m.norm_gain(f), m.norm_bias(f), x, stream_);
+        copy_rows(x, d_rows, conditioning, d_index, out_rows.size(), w, stream_);
+        // Host vectors above must outlive the asynchronous uploads.
+        check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+        first = last;
+    }
+}
+
+void Session::batched(const Header& h, const uint16_t* tokens, uint16_t* distributions,
+                      uint16_t* splits)
+{
+    const Geometry& g = model_->geometry();
+    const Model& m = *model_;
+    const std::size_t C = h.codebooks, w = g.width;
+    const std::size_t steps = h.frames * h.groups;
+    if (!steps)
+    {
+        return;
+    }
+    auto* err = errors_.as<uint32_t>();
+    auto* conditioning = arena_.get<uint16_t>("cond", steps * w);
+    temporal_rows(h, tokens, conditioning);
+    auto* d_tokens = arena_.get<uint16_t>("tokens", steps * C);
+    check_hip(hipMemcpyAsync(d_tokens, tokens, steps * C * 2, hipMemcpyHostToDevice, stream_),
+              "upload tokens");
+    const std::size_t chunk_steps = std::max<std::size_t>(1, batch_rows / C);
+    // Codebook sequences: step i of a chunk is rows i*C .. i*C+C-1.
+    {
+        std::vector<int> info(3 * chunk_steps);
+        for (std::size_t i = 0; i < chunk_steps; ++i)
+        {
+            info[i] = int(i * C);
+            info[chunk_steps + i] = int(C);
+            info[2 * chunk_steps + i] = 0;
+        }
+        auto* d_info = arena_.get<int>("c.info", info.size());
+        check_hip(hipMemcpyAsync(d_info, info.data(), info.size() * 4, hipMemcpyHostToDevice, stream_),
+                  "upload sequences");
+        check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    }
+    const int* d_info = arena_.get<int>("c.info", 3 * chunk_steps);
+    const std::size_t widest = std::max<std::size_t>({w, g.ffn, g.latent});
+    for (std::size_t s0 = 0; s0 < steps; s0 += chunk_steps)
+    {
+        const std::size_t n = std::min(chunk_steps, steps - s0), rows = n * C;
+        auto* prefix = arena_.get<uint16_t>("c.prefix", rows * g.latent);
+        auto* y = arena_.get<uint16_t>("c.y", rows * w);
+        auto* q8 = arena_.get<int8_t>("c.q8", rows * widest);
+        auto* s8 = arena_.get<float>("c.s8", rows * widest / 256);
+        auto* logits = arena_.get<uint16_t>("c.logits", rows * g.alphabet);
+        embed_prefixes(m.embeddings(), g.alphabet, g.latent, d_tokens + s0 * C, C, n, prefix, stream_);
+        quantize_rows(prefix, rows, g.latent, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err, stream_);
+        linear(m.codebook_projection(), q8, s8, rows, y, nullptr, LinearPath::automatic, stream_);
+        scatter_rows(conditioning + s0 * w, n, w, C, 0, y, stream_);
+        add_rows(y, m.positions(), rows, w, C, y, stream_);
+        stack_rows(false, y, rows, d_info, d_info + chunk_steps, d_info + 2 * chunk_steps, n, C, "c");
+        const std::size_t f = m.final_norm_index(false);
+        quantize_rows(y, rows, w, Prologue::layer_norm, m.norm_gain(f), m.norm_bias(f), q8, s8, nullptr,
+                      err, stream_);
+        linear(m.output_projection(), q8, s8, rows, logits, nullptr, LinearPath::automatic, stream_);
+        auto* probs = arena_.get<uint16_t>("c.probs", rows * g.alphabet);
+        softmax_rows(logits, rows, g.alphabet, probs, err, stream_);
+        if (distributions)
+        {
+            check_hip(hipMemcpyAsync(distributions + s0 * C * g.alphabet, probs, rows * g.alphabet * 2,
+                                     hipMemcpyDeviceToHost, stream_),
+                      "read distributions");
+        }
+        if (splits)
+        {
+            auto* d_splits = arena_.get<uint16_t>("c.splits", rows * 16);
+            categorical_paths(probs, rows, g.alphabet, d_tokens + s0 * C, d_splits, err, stream_);
+            check_hip(hipMemcpyAsync(splits + s0 * C * 16, d_splits, rows * 16 * 2, hipMemcpyDeviceToHost,
+                                     stream_),
+                      "read splits");
+        }
+        check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    }
+}
+
+// One decode-shaped layer over `rows` lanes at cache position `position`.
+void Session::layer_step(bool temporal, std::size_t layer, uint16_t* x, std::size_t rows,
+                         std::size_t position, bool replay, std::size_t extent)
+{
+    const Geometry& g = model_->geometry();
+    const Model& m = *model_;
+    const std::size_t w = g.width;
+    const std::size_t layers = temporal ? g.temporal_layers : g.codebook_layers;
+    const std::size_t widest = std::max<std::size_t>({w, g.ffn, g.latent});
+    auto* q8 = arena_.get<int8_t>("s.q8", rows * widest);
+    auto* s8 = arena_.get<float>("s.s8", rows * widest / 256);
+    auto* qkv = arena_.get<uint16_t>("s.qkv", rows * 3 * w);
+    auto* query = arena_.get<uint16_t>("s.query", rows * w);
+    auto* att = arena_.get<uint16_t>("s.att", rows * w);
+    auto* hidden = arena_.get<uint16_t>("s.hidden", rows * g.ffn);
+    auto* partial = arena_.get<float>("s.partial", decode_partial_floats(rows, g.heads, g.head_width, extent));
+    auto* keys = arena_.get<uint16_t>(temporal ? "s.tk" : "s.ck", 0);
+    auto* values = arena_.get<uint16_t>(temporal ? "s.tv" : "s.cv", 0);
+    auto* err = errors_.as<uint32_t>();
+    const std::size_t lane_stride = layers * extent * w;
+    uint16_t* layer_keys = keys + layer * extent * w;
+    uint16_t* layer_values = values + layer * extent * w;
+    const std::size_t n1 = m.norm_index(temporal, layer, false), n2 = m.norm_index(temporal, layer, true);
+    quantize_rows(x, rows, w, Prologue::layer_norm, m.norm_gain(n1), m.norm_bias(n1), q8, s8, nullptr,
+                  err, stream_);
+    linear(m.layer(temporal, layer, 0), q8, s8, rows, qkv, nullptr, LinearPath::automatic, stream_);
+    append_qkv(qkv, rows, w, g.head_width,
+               temporal ? m.rotations() + position * g.head_width : nullptr, query,
+               layer_keys + position * w, layer_values + position * w, lane_stride, stream_);
+    attention_decode(query, layer_keys, layer_values, lane_stride, rows, position + 1, g.heads,
+                     g.head_width, g.attention_scale, replay, partial, att, stream_);
+    quantize_rows(att, rows, w, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err, stream_);
+    linear(m.layer(temporal, layer, 1), q8, s8, rows, x, x, LinearPath::automatic, stream_);
+    quantize_rows(x, rows, w, Prologue::layer_norm, m.norm_gain(n2), m.norm_bias(n2), q8, s8, nullptr,
+                  err, stream_);
+    linear(m.layer(temporal, layer, 2), q8, s8, rows, hidden, nullptr, LinearPath::automatic, stream_);
+    quantize_rows(hidden, rows, g.ffn, Prologue::gelu, nullptr, nullptr, q8, s8, nullptr, err, stream_);
+    linear(m.layer(temporal, layer, 3), q8, s8, rows, x, x, LinearPath::automatic, stream_);
+}
+
+// Frame-by-frame, book-by-book pass with resident KV caches: the decode-side
+// shape (src/common/transformer.cpp:137-244 schedule, all ready lanes batched).
+void Session::stepwise(const Header& h, const uint16_t* known, RangeDecoder* decoder,
+                       uint16_t* tokens_out, uint16_t* distributions)
+{
+    const Geometry& g = model_->geometry();
+    const Model& m = *model_;
+    const std::size_t C = h.codebooks, G = h.groups, w = g.width;
+    const Lanes lanes(h);
+    const std::size_t independent = lanes.count * G;
+    if (!independent)
+    {
+        return;
+    }
+    const std::size_t longest = lanes.length(0);
+    const std::size_t extent = std::min<std::size_t>(longest, g.context);
+    arena_.get<uint16_t>("s.tk", independent * g.temporal_layers * extent * w);
+    arena_.get<uint16_t>("s.tv", independent * g.temporal_layers * extent * w);
+    arena_.get<uint16_t>("s.ck", independent * g.codebook_layers * C * w);
+    arena_.get<uint16_t>("s.cv", independent * g.codebook_layers * C * w);
+    auto* d_feedback = arena_.get<uint16_t>("s.feedback", independent * C);
+    auto* d_current = arena_.get<uint16_t>("s.current", independent * C);
+    auto* embedded = arena_.get<uint16_t>("s.embedded", independent * g.latent);
+    auto* prefix = arena_.get<uint16_t>("s.prefix", independent * g.latent);
+    auto* x = arena_.get<uint16_t>("s.x", independent * w);
+    auto* conditioning = arena_.get<uint16_t>("s.cond", independent * w);
+    auto* y = arena_.get<uint16_t>("s.y", independent * w);
+    auto* logits = arena_.get<uint16_t>("s.logits", independent * g.alphabet);
+    auto* probs = arena_.get<uint16_t>("s.probs", independent * g.alphabet);
+    auto* nodes = arena_.get<float>("s.nodes", independent * 1024);
+    const std::size_t widest = std::max<std::size_t>({w, g.ffn, g.latent});
+    auto* q8 = arena_.get<int8_t>("s.q8", independent * widest);
+    auto* s8 = arena_.get<float>("s.s8", independent * widest / 256);
+    auto* err = errors_.as<uint32_t>();
+    staging_.reserve(independent * g.alphabet * 2);
+    staging_nodes_.reserve(independent * 1024 * 4);
+    staging_tokens_.reserve(independent * C * 2 * 2);
+    auto* host_probs = staging_.as<uint16_t>();
+    auto* host_nodes = staging_nodes_.as<float>();
+    auto* host_feedback = staging_tokens_.as<uint16_t>();
+    auto* host_current = host_feedback + independent * C;
+
+    // Per-lane complete-frame history, newest last (src/common/transformer.cpp:222-244).
+    std::vector<std::vector<uint16_t>> history(independent);
+    std::size_t context_used = 0;
+    double host_seconds = 0;
+
+    const auto temporal_step = [&](std::size_t active, std::size_t position, bool replay)
+    {
+        check_hip(hipMemcpyAsync(d_feedback, host_feedback, active * C * 2, hipMemcpyHostToDevice, stream_),
+                  "upload feedback");
+        embed_sum(m.embeddings(), g.alphabet, g.latent, d_feedback, C, active, embedded, stream_);
+        quantize_rows(embedded, active, g.latent, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err,
+                      stream_);
+        linear(m.temporal_projection(), q8, s8, active, x, nullptr, LinearPath::automatic, stream_);
+        for (std::size_t l = 0; l < g.temporal_layers; ++l)
+        {
+            layer_step(true, l, x, active, position, replay, extent);
+        }
+        // The feedback staging is reused by the next step: wait for the upload.
+        check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    };
+
+    for (std::size_t step = 0; step < lanes.steps(); ++step)
+    {
+        const std::size_t active = step < lanes.base ? independent : lanes.extra * G;
+        if (context_used == g.context)
+        {
+            for (std::size_t i = 0; i < active; ++i)
+            {
+                require(history[i].size() == replay_frames * C, "incomplete Transformer replay history");
+            }
+            context_used = 0;
+            for (std::size_t k = 0; k < replay_frames; ++k)
+            {
+                for (std::size_t i = 0; i < active; ++i)
+                {
+                    std::memcpy(host_feedback + i * C, history[i].data() + k * C, C * 2);
+                }
+                temporal_step(active, context_used++, true);
+            }
+        }
+        else
+        {
+            for (std::size_t i = 0; i < active; ++i)
+            {
+                if (history[i].empty())
+                {
+                    std::memset(host_feedback + i * C, 0, C * 2);
+                }
+                else
+                {
+                    std::memcpy(host_feedback + i * C, history[i].data() + history[i].size() - C, C * 2);
+                }
+            }
+            temporal_step(active, context_used++, false);
+        }
+        const std::size_t f = m.final_norm_index(true);
+        layer_norm_rows(x, active, w, m.norm_gain(f), m.norm_bias(f), conditioning, stream_);
+
+        for (std::size_t book = 0; book < C; ++book)
+        {
+            if (book == 0)
+            {
+                check_hip(hipMemcpyAsync(y, conditioning, active * w * 2, hipMemcpyDeviceToDevice, stream_),
+                          "copy conditioning");
+            }
+            else
+            {
+                embed_accumulate(m.embeddings(), g.alphabet, g.latent, d_current + (book - 1), C, book - 1,
+                                 active, book == 1 ? nullptr : prefix, prefix, stream_);
+                quantize_rows(prefix, active, g.latent, Prologue::none, nullptr, nullptr, q8, s8, nullptr,
+                              err, stream_);
+                linear(m.codebook_projection(), q8, s8, active, y, nullptr, LinearPath::automatic, stream_);
+            }
+            add_rows(y, m.positions() + book * w, active, w, 1, y, stream_);
+            for (std::size_t l = 0; l < g.codebook_layers; ++l)
+            {
+                layer_step(false, l, y, active, book, false, C);
+            }
+            const std::size_t fc = m.final_norm_index(false);
+            quantize_rows(y, active, w, Prologue::layer_norm, m.norm_gain(fc), m.norm_bias(fc), q8, s8,
+                          nullptr, err, stream_);
+            linear(m.output_projection(), q8, s8, active, logits, nullptr, LinearPath::automatic, stream_);
+            softmax_rows(logits, active, g.alphabet, probs, err, stream_);
+            if (decoder)
+            {
+                categorical_trees(probs, active, nodes, stream_);
+                check_hip(hipMemcpyAsync(host_nodes, nodes, active * 1024 * 4, hipMemcpyDeviceToHost, stream_),
+                          "read masses");
+            }
+            check_hip(hipMemcpyAsync(host_probs, probs, active * g.alphabet * 2, hipMemcpyDeviceToHost,
+                                     stream_),
+                      "read distributions");
+            check_errors();
+            const double t0 = now();
+            for (std::size_t i = 0; i < active; ++i)
+            {
+                const std::size_t lane = i / G, group = i % G;
+                const std::size_t frame = lanes.start(lane) + step;
+                const std::size_t offset = (frame * G + group) * C + book;
+                uint16_t token;
+                if (decoder)
+                {
+                    token = uint16_t(decode_categorical(*decoder, host_nodes + i * 1024, host_probs + i * g.alphabet));
+                }
+                else
+                {
+                    token = known[offset];
+                }
+                if (tokens_out)
+                {
+                    tokens_out[offset] = token;
+                }
+                if (distributions)
+                {
+                    std::memcpy(distributions + offset * g.alphabet, host_probs + i * g.alphabet, g.alphabet * 2);
+                }
+                host_current[i * C + book] = token;
+            }
+            host_seconds += now() - t0;
+            check_hip(hipMemcpyAsync(d_current, host_current, active * C * 2, hipMemcpyHostToDevice, stream_),
+                      "upload tokens");
+            check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+        }
+        for (std::size_t i = 0; i < active; ++i)
+        {
+            auto& past = history[i];
+            past.insert(past.end(), host_current + i * C, host_current + (i + 1) * C);
+            if (past.size() > replay_frames * C)
+            {
+                past.erase(past.begin(), past.begin() + C);
+            }
+        }
+    }
+    timing_[1] = host_seconds;
+}
+
+std::vector<uint8_t> Session::encode(Header h, const uint16_t* tokens, std::size_t count)
+{
+    check_hip(hipSetDevice(model_->device()), "hipSetDevice");
+    const double t0 = now();
+    h.method = 1;
+    validate(h, tokens, count);
+    require(model_->limits().file_bytes >= 19, "normal framing exceeds file limit");
+    const uint32_t crc = token_crc32(tokens, count);
+    std::vector<uint16_t> splits(count * 16);
+    reset_errors();
+    batched(h, tokens, nullptr, splits.data());
+    check_errors();
+    const double t1 = now();
+    RangeEncoder encoder(model_->limits().file_bytes - 18);
+    const Lanes lanes(h);
+    for (std::size_t step = 0; step < lanes.steps(); ++step)
+    {
+        for (std::size_t book = 0; book < h.codebooks; ++book)
+        {
+            for (std::size_t lane = 0; lane < lanes.count; ++lane)
+            {
+                if (step >= lanes.length(lane))
+                {
+                    continue;
+                }
+                const std::size_t frame = lanes.start(lane) + step;
+                for (std::size_t group = 0; group < h.groups; ++group)
+                {
+                    const std::size_t offset = (frame * h.groups + group) * h.codebooks + book;
+                    const uint16_t symbol = tokens[offset];
+                    const uint16_t* s = splits.data() + offset * 16;
+                    std::size_t base = 0, n = 1024;
+                    for (int level = 0; n > 1; ++level)
+                    {
+                        const std::size_t half = n / 2;
+                        const bool bit = symbol >= base + half;
+                        encoder.put(s[level], bit);
+                        if (bit)
+                        {
+                            base += half;
+                            n -= half;
+                        }
+                        else
+                        {
+                            n = half;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    const auto bytes = frame_normal(h, crc, encoder.finish());
+    const double t2 = now();
+    timing_ = {t1 - t0, t2 - t1, t2 - t0};
+    return bytes;
+}
+
+std::vector<uint16_t> Session::decode(const uint8_t* stream, std::size_t length)
+{
+    check_hip(hipSetDevice(model_->device()), "hipSetDevice");
+    const double t0 = now();
+    const Header h = parse_header(stream, length, model_->limits());
+    require(h.method == 1, "unpack_normal requires method 1");
+    validate(h, nullptr, h.symbols());
+    std::vector<uint16_t> tokens(h.symbols());
+    RangeDecoder decoder(stream + h.payload_offset, h.payload_bytes);
+    reset_errors();
+    stepwise(h, nullptr, &decoder, tokens.data(), nullptr);
+    require(token_crc32(tokens.data(), tokens.size()) == h.token_crc, "invalid token CRC32");
+    const double t1 = now();
+    timing_ = {t1 - t0 - timing_[1], timing_[1], t1 - t0};
+    return tokens;
+}
+
+void Session::distributions(Header h, const uint16_t* tokens, std::size_t count, bool decode_pass,
+                            uint16_t* out)
+{
+    check_hip(hipSetDevice(model_->device()), "hipSetDevice");
+    const double t0 = now();
+    h.method = 1;
+    validate(h, tokens, count);
+    reset_errors();
+    if (decode_pass)
+    {
+        stepwise(h, tokens, nullptr, nullptr, out);
+    }
+    else
+    {
+        batched(h, tokens, out, nullptr);
+    }
+    check_errors();
+    const double t1 = now();
+    timing_ = {t1 - t0, 0.0, t1 - t0};
+}
+} // namespace tsac_hip

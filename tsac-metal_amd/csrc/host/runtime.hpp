@@ -1,0 +1,216 @@
+// Device model, sessions and the encode/decode drivers of the probability model.
+#pragma once
+
+#include "../kernels/attention.hpp"
+#include "../kernels/codec.hpp"
+#include "../kernels/kernels.hpp"
+#include "format.hpp"
+
+#include <array>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace tsac_hip
+{
+struct Geometry
+{
+    uint32_t width = 512, heads = 4, head_width = 128, ffn = 2048;
+    uint32_t temporal_layers = 12, codebook_layers = 3;
+    uint32_t latent = 1024, alphabet = 1024, books = 12, channels = 2, context = 1024;
+    float attention_scale = 0.0883883461356163f;
+
+    std::size_t projections() const
+    {
+        return 4 * std::size_t(temporal_layers + codebook_layers) + 3;
+    }
+    std::size_t norms() const
+    {
+        return 2 * std::size_t(temporal_layers + codebook_layers) + 2;
+    }
+    // (K, N) of projection `index` (src/models/contract.cpp:88-110).
+    std::pair<std::size_t, std::size_t> projection_shape(std::size_t index) const;
+};
+
+// Owning device allocation.
+class DeviceBuffer
+{
+public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(std::size_t bytes);
+    ~DeviceBuffer();
+    DeviceBuffer(DeviceBuffer&& other) noexcept;
+    DeviceBuffer& operator=(DeviceBuffer&& other) noexcept;
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+
+    void* get() const
+    {
+        return data_;
+    }
+    template <class T> T* as() const
+    {
+        return static_cast<T*>(data_);
+    }
+    std::size_t bytes() const
+    {
+        return bytes_;
+    }
+
+private:
+    void* data_ = nullptr;
+    std::size_t bytes_ = 0;
+};
+
+// Page-locked host staging.
+class PinnedBuffer
+{
+public:
+    PinnedBuffer() = default;
+    ~PinnedBuffer();
+    void reserve(std::size_t bytes);
+    template <class T> T* as() const
+    {
+        return static_cast<T*>(data_);
+    }
+
+private:
+    void* data_ = nullptr;
+    std::size_t bytes_ = 0;
+};
+
+// Named scratch that grows on demand and is released by clear().
+class Arena
+{
+public:
+    void* get(const std::string& name, std::size_t bytes);
+    template <class T> T* get(const std::string& name, std::size_t count)
+    {
+        return static_cast<T*>(get(name, count * sizeof(T)));
+    }
+    void clear()
+    {
+        buffers_.clear();
+    }
+
+private:
+    std::map<std::string, DeviceBuffer> buffers_;
+};
+
+struct LinearHost
+{
+    const int8_t* values;
+    const float* scales;
+    const float* bias;
+};
+
+class Model
+{
+public:
+    Model(const Geometry& g, const LinearHost* projections, const uint16_t* const* gain,
+          const uint16_t* const* bias, const uint16_t* positions, const uint16_t* rotations,
+          const uint16_t* embeddings, const Limits& limits);
+
+    const Geometry& geometry() const
+    {
+        return g_;
+    }
+    const Limits& limits() const
+    {
+        return limits_;
+    }
+    int device() const
+    {
+        return device_;
+    }
+    const DeviceLinear& projection(std::size_t index) const
+    {
+        return projections_.at(index);
+    }
+    // Stack projections: op 0 qkv, 1 attn_out, 2 mlp_in, 3 mlp_out.
+    const DeviceLinear& layer(bool temporal, std::size_t layer, int op) const;
+    const DeviceLinear& temporal_projection() const;
+    const DeviceLinear& codebook_projection() const;
+    const DeviceLinear& output_projection() const;
+    const uint16_t* norm_gain(std::size_t index) const
+    {
+        return gain_.at(index);
+    }
+    const uint16_t* norm_bias(std::size_t index) const
+    {
+        return bias_.at(index);
+    }
+    std::size_t norm_index(bool temporal, std::size_t layer, bool mlp) const;
+    std::size_t final_norm_index(bool temporal) const;
+    const uint16_t* positions() const
+    {
+        return positions_;
+    }
+    const uint16_t* rotations() const
+    {
+        return rotations_;
+    }
+    const uint16_t* embeddings() const
+    {
+        return embeddings_;
+    }
+
+private:
+    Geometry g_;
+    Limits limits_;
+    int device_ = 0;
+    DeviceBuffer values_, constants_;
+    std::vector<DeviceLinear> projections_;
+    std::vector<const uint16_t*> gain_, bias_;
+    const uint16_t *positions_ = nullptr, *rotations_ = nullptr, *embeddings_ = nullptr;
+};
+
+class Session
+{
+public:
+    explicit Session(std::shared_ptr<const Model> model);
+    ~Session();
+    Session(const Session&) = delete;
+    Session& operator=(const Session&) = delete;
+
+    void clear();
+    std::vector<uint8_t> encode(Header header, const uint16_t* tokens, std::size_t count);
+    std::vector<uint16_t> decode(const uint8_t* stream, std::size_t length);
+    // Teacher-forced distributions [count][alphabet]; decode_pass selects the
+    // stepwise (GEMV) driver instead of the batched (GEMM) one.
+    void distributions(Header header, const uint16_t* tokens, std::size_t count, bool decode_pass,
+                       uint16_t* out);
+    std::array<double, 3> timing() const
+    {
+        return timing_;
+    }
+
+private:
+    struct Stepwise;
+    void check_errors();
+    void reset_errors();
+    void validate(const Header& h, const uint16_t* tokens, std::size_t count) const;
+    // Batched known-token pass. Writes either the BF16 distributions of every
+    // token (distributions != null) or its ten Q15 splits (splits != null).
+    void batched(const Header& h, const uint16_t* tokens, uint16_t* distributions,
+                 uint16_t* splits);
+    void temporal_rows(const Header& h, const uint16_t* tokens, uint16_t* conditioning);
+    void stack_rows(bool temporal, uint16_t* x, std::size_t rows, const int* starts,
+                    const int* lengths, const int* replays, std::size_t sequences,
+                    std::size_t max_length, const std::string& tag);
+    // Stepwise pass. `known` tokens are teacher-forced when non-null; otherwise
+    // symbols are range-decoded from `decoder`.
+    void stepwise(const Header& h, const uint16_t* known, RangeDecoder* decoder,
+                  uint16_t* tokens_out, uint16_t* distributions);
+    void layer_step(bool temporal, std::size_t layer, uint16_t* x, std::size_t rows,
+                    std::size_t position, bool replay, std::size_t extent);
+
+    std::shared_ptr<const Model> model_;
+    hipStream_t stream_ = nullptr;
+    Arena arena_;
+    DeviceBuffer errors_;
+    PinnedBuffer pinned_errors_, staging_, staging_nodes_, staging_tokens_;
+    std::array<double, 3> timing_{};
+};
+} // namespace tsac_hip

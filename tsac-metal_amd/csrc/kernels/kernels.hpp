@@ -1,0 +1,88 @@
+// Host-side launchers for the probability-model kernels. Every launcher checks
+// the shapes its kernel's indexing assumes and throws tsac_hip::Error before
+// launching anything that would not fit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace tsac_hip
+{
+struct Error : std::runtime_error
+{
+    using std::runtime_error::runtime_error;
+};
+
+inline void require(bool condition, const char* message)
+{
+    if (!condition)
+    {
+        throw Error(message);
+    }
+}
+
+inline void check_hip(hipError_t status, const char* what)
+{
+    if (status != hipSuccess)
+    {
+        throw Error(std::string(what) + ": " + hipGetErrorString(status));
+    }
+}
+
+// Error words written by kernels (plain stores of fixed values, no atomics):
+// word 0 = a BF8L, softmax or categorical input was not finite; word 1 is reserved
+// for range-decoder state.
+constexpr uint32_t error_nonfinite = 1u;
+
+// ---- quantisation (BF8L, src/scalar/probability.cpp:16-40) ------------------
+enum class Prologue
+{
+    none,       // quantise the BF16 rows as they are
+    layer_norm, // LayerNorm (gain, bias) first (src/common/probability.cpp:138-169)
+    gelu,       // GELU first (src/common/probability.cpp:45-63)
+};
+
+// x: [rows][K] BF16. q: [rows][K] int8. scales: [rows][K/256] fp32 (widened BF16).
+// normalized (optional, layer_norm only): [rows][K] BF16 of the normalised values.
+void quantize_rows(const uint16_t* x, std::size_t rows, std::size_t K, Prologue prologue,
+                   const uint16_t* gain, const uint16_t* bias, int8_t* q, float* scales,
+                   uint16_t* normalized, uint32_t* error, hipStream_t stream);
+
+// ---- quantised linear (src/scalar/packed_linear.cpp:8-30) ---------------------
+struct DeviceLinear
+{
+    const int8_t* values = nullptr; // [N][K] canonical
+    const float* scales = nullptr;  // [K/256][N]
+    const float* bias = nullptr;    // [N]
+    std::size_t K = 0, N = 0;
+};
+
+enum class LinearPath
+{
+    automatic,
+    gemv,
+    gemm
+};
+
+// y[m][n] = bf16(chain_b fma(dot_b, ws[b][n]*as[m][b]) + bias[n]); with a residual,
+// y[m][n] = bf16(float(residual[m][n]) + float(that)). residual may alias y.
+void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M,
+            uint16_t* y, const uint16_t* residual, LinearPath path, hipStream_t stream);
+std::size_t gemv_max_rows();
+
+// ---- row-wise elementwise kernels --------------------------------------------
+void layer_norm_rows(const uint16_t* x, std::size_t rows, std::size_t width, const uint16_t* gain,
+                     const uint16_t* bias, uint16_t* out, hipStream_t stream);
+// out[r][i] = bf16(float(a[r][i]) + float(b[(r % b_period)][i])); out may alias a.
+void add_rows(const uint16_t* a, const uint16_t* b, std::size_t rows, std::size_t width,
+              std::size_t b_period, uint16_t* out, hipStream_t stream);
+void softmax_rows(const uint16_t* x, std::size_t rows, std::size_t width, uint16_t* out,
+                  uint32_t* error, hipStream_t stream);
+void gelu_values(const uint16_t* x, std::size_t count, uint16_t* out, hipStream_t stream);
+void rotary_values(const uint16_t* x, const uint16_t* coefficients, std::size_t count,
+                   uint16_t* out, hipStream_t stream);
+} // namespace tsac_hip

@@ -1,0 +1,155 @@
+// BF8L activation quantisation with optional LayerNorm or GELU prologue.
+//
+// One 64-lane wavefront owns one row of K BF16 values; lane l holds the V = K/64
+// consecutive values [l*V, l*V+V). That placement makes the cross-lane
+// adjacent-pair tree (strides 1, 2, 4, ...) identical to the reference's pair
+// tree over the whole row, and puts each 256-value BF8L block on 256/V aligned
+// neighbouring lanes.
+#include "kernels.hpp"
+#include "row_ops.hpp"
+
+namespace tsac_hip
+{
+namespace
+{
+constexpr int rows_per_block = 4;
+
+template <int V, Prologue prologue>
+__global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restrict__ x, int rows,
+                                                       const uint16_t* __restrict__ gain,
+                                                       const uint16_t* __restrict__ bias,
+                                                       int8_t* __restrict__ q,
+                                                       float* __restrict__ scales,
+                                                       uint16_t* __restrict__ normalized,
+                                                       uint32_t* __restrict__ error)
+{
+    constexpr int K = 64 * V, lanes_per_block = 256 / V;
+    const int lane = threadIdx.x % wave;
+    const int row = blockIdx.x * rows_per_block + threadIdx.x / wave;
+    if (row >= rows)
+    {
+        return;
+    }
+    uint16_t v[V];
+    load_row<V>(x + size_t(row) * K + lane * V, v);
+    if constexpr (prologue == Prologue::layer_norm)
+    {
+        layer_norm_lane<V>(v, gain, bias, lane);
+        if (normalized)
+        {
+            store_row<V>(normalized + size_t(row) * K + lane * V, v);
+        }
+    }
+    else if constexpr (prologue == Prologue::gelu)
+    {
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+        {
+            v[i] = gelu_bf16(v[i]);
+        }
+    }
+    // src/scalar/probability.cpp:20-38
+    float values[V];
+    float maximum = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+    {
+        values[i] = bf16_to_float(v[i]);
+        finite = finite && is_finite(values[i]);
+        const float a = __builtin_fabsf(flush(values[i]));
+        maximum = maximum < a ? a : maximum;
+    }
+    if (!finite)
+    {
+        error[0] = error_nonfinite;
+    }
+    maximum = group_max<lanes_per_block>(maximum);
+    float s = ftz_divide(maximum, 127.0f);
+    s = s < 1e-35f ? 1e-35f : s;
+    const uint16_t scale = float_to_bf16(s);
+    const float reciprocal = ftz_divide(1.0f, bf16_to_float(scale));
+    int8_t out[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+    {
+        float r = __builtin_rintf(ftz_multiply(values[i], reciprocal));
+        r = r < -128.0f ? -128.0f : (127.0f < r ? 127.0f : r);
+        out[i] = int8_t(r);
+    }
+    int8_t* qrow = q + size_t(row) * K + lane * V;
+    if constexpr (V == 4)
+    {
+        *reinterpret_cast<uint32_t*>(qrow) = *reinterpret_cast<const uint32_t*>(out);
+    }
+    else
+    {
+#pragma unroll
+        for (int c = 0; c < V / 8; ++c)
+        {
+            reinterpret_cast<uint2*>(qrow)[c] = reinterpret_cast<const uint2*>(out)[c];
+        }
+    }
+    if (lane % lanes_per_block == 0)
+    {
+        scales[size_t(row) * (K / 256) + lane / lanes_per_block] = bf16_to_float(scale);
+    }
+}
+
+template <int V>
+void launch_quantize(const uint16_t* x, std::size_t rows, Prologue prologue, const uint16_t* gain,
+                     const uint16_t* bias, int8_t* q, float* scales, uint16_t* normalized,
+                     uint32_t* error, hipStream_t stream)
+{
+    const dim3 grid(unsigned((rows + rows_per_block - 1) / rows_per_block)), block(256);
+    switch (prologue)
+    {
+    case Prologue::none:
+        quantize_kernel<V, Prologue::none><<<grid, block, 0, stream>>>(
+            x, int(rows), gain, bias, q, scales, normalized, error);
+        break;
+    case Prologue::layer_norm:
+        quantize_kernel<V, Prologue::layer_norm><<<grid, block, 0, stream>>>(
+            x, int(rows), gain, bias, q, scales, normalized, error);
+        break;
+    case Prologue::gelu:
+        quantize_kernel<V, Prologue::gelu><<<grid, block, 0, stream>>>(
+            x, int(rows), gain, bias, q, scales, normalized, error);
+        break;
+    }
+}
+} // namespace
+
+void quantize_rows(const uint16_t* x, std::size_t rows, std::size_t K, Prologue prologue,
+                   const uint16_t* gain, const uint16_t* bias, int8_t* q, float* scales,
+                   uint16_t* normalized, uint32_t* error, hipStream_t stream)
+{
+    require(rows < (std::size_t(1) << 31), "too many rows");
+    require(prologue != Prologue::layer_norm || (gain && bias), "layer norm needs gain and bias");
+    if (rows == 0)
+    {
+        return;
+    }
+    switch (K)
+    {
+    case 256:
+        launch_quantize<4>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        break;
+    case 512:
+        launch_quantize<8>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        break;
+    case 1024:
+        launch_quantize<16>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        break;
+    case 2048:
+        launch_quantize<32>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        break;
+    case 4096:
+        launch_quantize<64>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        break;
+    default:
+        throw Error("quantize: K must be one of 256, 512, 1024, 2048, 4096");
+    }
+    check_hip(hipGetLastError(), "quantize launch");
+}
+} // namespace tsac_hip

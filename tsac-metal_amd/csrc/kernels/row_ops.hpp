@@ -1,0 +1,115 @@
+// Row helpers for kernels where one 64-lane wavefront owns one row and lane l
+// holds the V consecutive BF16 values [l*V, l*V+V).
+#pragma once
+
+#include "device_numeric.hpp"
+
+namespace tsac_hip
+{
+template <int V> __device__ __forceinline__ void load_row(const uint16_t* p, uint16_t (&v)[V])
+{
+    if constexpr (V == 1)
+    {
+        v[0] = p[0];
+    }
+    else if constexpr (V == 2)
+    {
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+        v[0] = u & 0xffff, v[1] = u >> 16;
+    }
+    else if constexpr (V == 4)
+    {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
+        v[0] = u.x & 0xffff, v[1] = u.x >> 16, v[2] = u.y & 0xffff, v[3] = u.y >> 16;
+    }
+    else
+    {
+#pragma unroll
+        for (int c = 0; c < V / 8; ++c)
+        {
+            const uint4 u = reinterpret_cast<const uint4*>(p)[c];
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                v[8 * c + 2 * i] = w[i] & 0xffff;
+                v[8 * c + 2 * i + 1] = w[i] >> 16;
+            }
+        }
+    }
+}
+
+template <int V> __device__ __forceinline__ void store_row(uint16_t* p, const uint16_t (&v)[V])
+{
+    if constexpr (V == 1)
+    {
+        p[0] = v[0];
+    }
+    else if constexpr (V == 2)
+    {
+        *reinterpret_cast<uint32_t*>(p) = v[0] | (uint32_t(v[1]) << 16);
+    }
+    else if constexpr (V == 4)
+    {
+        *reinterpret_cast<uint2*>(p) =
+            make_uint2(v[0] | (uint32_t(v[1]) << 16), v[2] | (uint32_t(v[3]) << 16));
+    }
+    else
+    {
+#pragma unroll
+        for (int c = 0; c < V / 8; ++c)
+        {
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                w[i] = v[8 * c + 2 * i] | (uint32_t(v[8 * c + 2 * i + 1]) << 16);
+            }
+            reinterpret_cast<uint4*>(p)[c] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+}
+
+// The reference's probability_sum over a full row of 64*V leaves (V >= 2):
+// the balanced pair tree equals its 64-block binary-carry merge, which ends
+// with add(+0, S) (src/format/categorical.cpp:44-74).
+template <int V> __device__ __forceinline__ float row_sum(float (&v)[V])
+{
+    static_assert(V >= 2, "rows of 64 or fewer values use the single-block tree");
+    return ftz_add(0.0f, tree_sum<wave>(register_tree(v)));
+}
+
+// LayerNorm of one row (src/common/probability.cpp:138-169), in place.
+template <int V>
+__device__ __forceinline__ void layer_norm_lane(uint16_t (&v)[V], const uint16_t* gain,
+                                                const uint16_t* bias, int lane)
+{
+    float values[V], squares[V], x[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+    {
+        x[i] = bf16_to_float(v[i]);
+        values[i] = x[i];
+        squares[i] = x[i] * x[i];
+    }
+    constexpr int width = wave * V;
+    const float sum = row_sum<V>(values);
+    const float sum_squares = row_sum<V>(squares);
+    const float reciprocal = 1.0f / float(width);
+    const float mean = sum * reciprocal;
+    float variance = __builtin_fmaf(sum_squares, reciprocal, 0.0f);
+    variance = __builtin_fmaf(mean, -mean, variance);
+    variance += 1e-5f;
+    const float inverse = 1.0f / __builtin_sqrtf(variance);
+    const float offset = -mean * inverse;
+    uint16_t g[V], b[V];
+    load_row<V>(gain + lane * V, g);
+    load_row<V>(bias + lane * V, b);
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+    {
+        const float normalized = __builtin_fmaf(x[i], inverse, offset);
+        v[i] = float_to_bf16(__builtin_fmaf(normalized, bf16_to_float(g[i]), bf16_to_float(b[i])));
+    }
+}
+} // namespace tsac_hip

@@ -1,0 +1,295 @@
+"""ctypes bindings of libtsac_hip.so (include/tsac_hip.h).
+
+The library is the product: every call here runs the hand-written gfx950
+kernels. Loading fails loudly when the library has not been built; there is no
+fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+import numpy as np
+
+PACKAGE = pathlib.Path(__file__).resolve().parent.parent
+LIBRARY = PACKAGE / "libtsac_hip.so"
+
+u8p = C.POINTER(C.c_uint8)
+u16p = C.POINTER(C.c_uint16)
+i8p = C.POINTER(C.c_int8)
+f32p = C.POINTER(C.c_float)
+i32p = C.POINTER(C.c_int)
+sz = C.c_size_t
+vp = C.c_void_p
+
+#: Exported entry points declared by include/tsac_hip.h.
+EXPORTS = (
+    "tsac_hip_last_error", "tsac_hip_model_create", "tsac_hip_model_destroy",
+    "tsac_hip_session_create", "tsac_hip_session_destroy", "tsac_hip_session_clear",
+    "tsac_hip_encode", "tsac_hip_decode", "tsac_hip_free", "tsac_hip_distributions",
+    "tsac_hip_session_timing", "tsac_hip_linear_create", "tsac_hip_linear_destroy",
+    "tsac_hip_linear_apply", "tsac_hip_linear_apply_quantized", "tsac_hip_bf8l",
+    "tsac_hip_layer_norm", "tsac_hip_softmax", "tsac_hip_gelu", "tsac_hip_rotary", "tsac_hip_add",
+    "tsac_hip_attention", "tsac_hip_attention_causal",
+)
+
+PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
+PASS_ENCODE, PASS_DECODE = 0, 1
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class Geometry(C.Structure):
+    _fields_ = [(name, C.c_uint32) for name in (
+        "width", "heads", "head_width", "ffn", "temporal_layers", "codebook_layers", "latent",
+        "alphabet", "books", "channels", "context")] + [("attention_scale", C.c_float)]
+
+
+class Linear(C.Structure):
+    _fields_ = [("values", i8p), ("scales", f32p), ("bias", f32p)]
+
+
+class ModelDesc(C.Structure):
+    _fields_ = [("geometry", Geometry), ("projections", C.POINTER(Linear)),
+                ("norm_gain", C.POINTER(u16p)), ("norm_bias", C.POINTER(u16p)),
+                ("positions", u16p), ("rotations", u16p), ("embeddings", u16p)]
+
+
+class Limits(C.Structure):
+    _fields_ = [(name, C.c_uint64) for name in (
+        "file_bytes", "symbols", "pcm_bytes", "cache_bytes", "tensor_elements")]
+
+
+class Header(C.Structure):
+    _fields_ = [("method", C.c_uint8), ("groups", C.c_uint8), ("model_channels", C.c_uint8),
+                ("codebooks", C.c_uint8), ("frames", C.c_uint64), ("batch", C.c_uint16)]
+
+
+def header(frames, batch, groups, codebooks, model_channels=2, method=1) -> Header:
+    return Header(method, groups, model_channels, codebooks, frames, batch)
+
+
+_lib = None
+
+
+def library() -> C.CDLL:
+    """Loads libtsac_hip.so once; raises if it is missing."""
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            raise HipError(f"{LIBRARY} is not built: run `make -C {PACKAGE}` "
+                           "(or __graft_entry__.build())")
+        lib = C.CDLL(str(LIBRARY))
+        lib.tsac_hip_last_error.restype = C.c_char_p
+        lib.tsac_hip_model_create.argtypes = [C.POINTER(ModelDesc), C.POINTER(Limits), C.POINTER(vp)]
+        lib.tsac_hip_model_destroy.argtypes = [vp]
+        lib.tsac_hip_session_create.argtypes = [vp, C.POINTER(vp)]
+        lib.tsac_hip_session_destroy.argtypes = [vp]
+        lib.tsac_hip_session_clear.argtypes = [vp]
+        lib.tsac_hip_encode.argtypes = [vp, C.POINTER(Header), u16p, sz, C.POINTER(u8p), C.POINTER(sz)]
+        lib.tsac_hip_decode.argtypes = [vp, u8p, sz, C.POINTER(u16p), C.POINTER(sz)]
+        lib.tsac_hip_free.argtypes = [vp]
+        lib.tsac_hip_distributions.argtypes = [vp, C.POINTER(Header), u16p, sz, C.c_int, u16p]
+        lib.tsac_hip_session_timing.argtypes = [vp, C.POINTER(C.c_double), sz]
+        lib.tsac_hip_linear_create.argtypes = [C.POINTER(Linear), sz, sz, C.POINTER(vp)]
+        lib.tsac_hip_linear_destroy.argtypes = [vp]
+        lib.tsac_hip_linear_apply.argtypes = [vp, vp, sz, vp, C.c_int, vp]
+        lib.tsac_hip_linear_apply_quantized.argtypes = [vp, vp, vp, sz, vp, vp, C.c_int, vp]
+        lib.tsac_hip_bf8l.argtypes = [vp, sz, sz, vp, vp, vp]
+        lib.tsac_hip_layer_norm.argtypes = [vp, sz, sz, vp, vp, vp, vp]
+        lib.tsac_hip_softmax.argtypes = [vp, sz, sz, vp, vp]
+        lib.tsac_hip_gelu.argtypes = [vp, sz, vp, vp]
+        lib.tsac_hip_rotary.argtypes = [vp, vp, sz, vp, vp]
+        lib.tsac_hip_add.argtypes = [vp, vp, sz, sz, sz, vp, vp]
+        lib.tsac_hip_attention.argtypes = [vp, vp, vp, sz, sz, sz, sz, sz, C.c_float, C.c_int, vp, vp]
+        lib.tsac_hip_attention_causal.argtypes = [vp, sz, sz, vp, vp, vp, sz, sz, vp, C.c_float, vp, vp]
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    if status:
+        raise HipError(library().tsac_hip_last_error().decode())
+
+
+def _ptr(array: np.ndarray, ctype):
+    assert array.flags["C_CONTIGUOUS"]
+    return array.ctypes.data_as(C.POINTER(ctype))
+
+
+def model_desc(model):
+    """ModelDesc over a tsac_hip.synthetic.Model; returns (desc, keepalive)."""
+    g = model.geometry
+    geometry = Geometry(g.width, g.heads, g.head_width, g.ffn, g.temporal_layers, g.codebook_layers,
+                        g.latent, g.alphabet, g.books, g.channels, g.context, g.attention_scale)
+    keep = []
+    linears = (Linear * len(model.projections))()
+    for i, (values, scales, bias) in enumerate(model.projections):
+        values, scales, bias = (np.ascontiguousarray(a) for a in (values, scales, bias))
+        keep += [values, scales, bias]
+        linears[i] = Linear(_ptr(values, C.c_int8), _ptr(scales, C.c_float), _ptr(bias, C.c_float))
+    gains = [np.ascontiguousarray(a) for a in model.norm_gain]
+    biases = [np.ascontiguousarray(a) for a in model.norm_bias]
+    gain_ptrs = (u16p * len(gains))(*[_ptr(a, C.c_uint16) for a in gains])
+    bias_ptrs = (u16p * len(biases))(*[_ptr(a, C.c_uint16) for a in biases])
+    arrays = [np.ascontiguousarray(model.positions), np.ascontiguousarray(model.rotations),
+              np.ascontiguousarray(model.embeddings)]
+    keep += [linears, gains, biases, gain_ptrs, bias_ptrs, arrays]
+    desc = ModelDesc(geometry, linears, gain_ptrs, bias_ptrs, _ptr(arrays[0], C.c_uint16),
+                     _ptr(arrays[1], C.c_uint16), _ptr(arrays[2], C.c_uint16))
+    return desc, keep
+
+
+class HipModel:
+    """Immutable device model (MetalTransformer::from_model, src/metal/transformer.hpp:16)."""
+
+    def __init__(self, model, limits: Limits | None = None):
+        self.geometry = model.geometry
+        lib = library()
+        desc, keep = model_desc(model)
+        handle = vp()
+        check(lib.tsac_hip_model_create(C.byref(desc), C.byref(limits) if limits else None,
+                                        C.byref(handle)))
+        self.handle = handle
+        del keep
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            library().tsac_hip_model_destroy(self.handle)
+            self.handle = None
+
+    def session(self) -> "HipSession":
+        return HipSession(self)
+
+
+class HipSession:
+    """Mutable session (MetalTransformer::new_session / encode / decode)."""
+
+    def __init__(self, model: HipModel):
+        self.model = model
+        handle = vp()
+        check(library().tsac_hip_session_create(model.handle, C.byref(handle)))
+        self.handle = handle
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            library().tsac_hip_session_destroy(self.handle)
+            self.handle = None
+
+    def clear(self):
+        check(library().tsac_hip_session_clear(self.handle))
+
+    def encode(self, h: Header, tokens) -> bytes:
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out, n = u8p(), sz()
+        check(library().tsac_hip_encode(self.handle, C.byref(h), _ptr(t, C.c_uint16), t.size,
+                                        C.byref(out), C.byref(n)))
+        data = C.string_at(out, n.value)
+        library().tsac_hip_free(out)
+        return data
+
+    def decode(self, data: bytes) -> np.ndarray:
+        b = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+        out, n = u16p(), sz()
+        check(library().tsac_hip_decode(self.handle, _ptr(b, C.c_uint8), len(data), C.byref(out),
+                                        C.byref(n)))
+        tokens = np.ctypeslib.as_array(out, shape=(n.value,)).copy() if n.value else np.zeros(0, np.uint16)
+        library().tsac_hip_free(out)
+        return tokens
+
+    def distributions(self, h: Header, tokens, mode: int = PASS_ENCODE) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out = np.zeros((t.size, self.model.geometry.alphabet), np.uint16)
+        check(library().tsac_hip_distributions(self.handle, C.byref(h), _ptr(t, C.c_uint16), t.size,
+                                               mode, _ptr(out, C.c_uint16)))
+        return out
+
+    def timing(self):
+        t = (C.c_double * 3)()
+        check(library().tsac_hip_session_timing(self.handle, t, 3))
+        return {"model": t[0], "range_coding": t[1], "total": t[2]}
+
+
+# ---------------------------------------------------------------- operators on torch tensors
+
+def _stream(stream=None):
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return vp(s.cuda_stream)
+
+
+def _dp(tensor):
+    assert tensor.is_cuda and tensor.is_contiguous()
+    return vp(tensor.data_ptr())
+
+
+class DeviceLinear:
+    """PackedLinear on the GPU (src/common/packed_linear.tpp:216-302)."""
+
+    def __init__(self, values: np.ndarray, scales: np.ndarray, bias: np.ndarray):
+        n, k = values.shape
+        self.K, self.N = k, n
+        values = np.ascontiguousarray(values, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        bias = np.ascontiguousarray(bias, np.float32)
+        desc = Linear(_ptr(values, C.c_int8), _ptr(scales, C.c_float), _ptr(bias, C.c_float))
+        handle = vp()
+        check(library().tsac_hip_linear_create(C.byref(desc), k, n, C.byref(handle)))
+        self.handle = handle
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            library().tsac_hip_linear_destroy(self.handle)
+            self.handle = None
+
+    def apply(self, x, y, path=PATH_AUTO, stream=None):
+        """x: int16/uint16 cuda tensor [M][K] of BF16 bits -> y [M][N]."""
+        m = x.numel() // self.K
+        check(library().tsac_hip_linear_apply(self.handle, _dp(x), m, _dp(y), path, _stream(stream)))
+
+    def apply_quantized(self, q, scales, m, y, residual=None, path=PATH_AUTO, stream=None):
+        check(library().tsac_hip_linear_apply_quantized(
+            self.handle, _dp(q), _dp(scales), m, _dp(y), _dp(residual) if residual is not None else None,
+            path, _stream(stream)))
+
+
+def bf8l(x, rows, k, q, scales, stream=None):
+    check(library().tsac_hip_bf8l(_dp(x), rows, k, _dp(q), _dp(scales), _stream(stream)))
+
+
+def layer_norm(x, rows, width, gain, bias, out, stream=None):
+    check(library().tsac_hip_layer_norm(_dp(x), rows, width, _dp(gain), _dp(bias), _dp(out),
+                                        _stream(stream)))
+
+
+def softmax(x, rows, width, out, stream=None):
+    check(library().tsac_hip_softmax(_dp(x), rows, width, _dp(out), _stream(stream)))
+
+
+def gelu(x, out, stream=None):
+    check(library().tsac_hip_gelu(_dp(x), x.numel(), _dp(out), _stream(stream)))
+
+
+def rotary(x, coefficients, out, stream=None):
+    check(library().tsac_hip_rotary(_dp(x), _dp(coefficients), x.numel(), _dp(out), _stream(stream)))
+
+
+def add(a, b, rows, width, period, out, stream=None):
+    check(library().tsac_hip_add(_dp(a), _dp(b), rows, width, period, _dp(out), _stream(stream)))
+
+
+def attention(query, keys, values, sequence_stride, sequences, time, heads, head_width, scale,
+              prefill, out, stream=None):
+    check(library().tsac_hip_attention(_dp(query), _dp(keys), _dp(values), sequence_stride, sequences,
+                                       time, heads, head_width, scale, int(prefill), _dp(out),
+                                       _stream(stream)))
+
+
+def attention_causal(qkv, heads, head_width, start, length, replay, sequences, max_length, rotations,
+                     scale, out, stream=None):
+    check(library().tsac_hip_attention_causal(
+        _dp(qkv), heads, head_width, _dp(start), _dp(length), _dp(replay), sequences, max_length,
+        _dp(rotations) if rotations is not None else None, scale, _dp(out), _stream(stream)))
