@@ -1,0 +1,268 @@
+"""Benchmark of the TSAC probability model on one MI355X.
+
+Step = one GPU encode (pack_normal-equivalent: model + range coder -> FBAZ
+bytes) plus one GPU decode (unpack_normal-equivalent: model + range decoder ->
+tokens, CRC checked) of a 30 s joint-stereo token stream: 2580 frames x 12
+codebooks, entropy batch 3 (three lanes of 860 frames), one channel group, on
+the reference geometry (12 temporal + 3 codebook layers, width 512, 4 x 128
+heads, FFN 2048) with seeded random-init weights in the reference's packed
+layout. Tokens are synthetic (uniform over the 1024-symbol alphabet).
+
+value = tokens / (encode seconds + decode seconds) of one step.
+
+Also measured in the same run:
+  * roofline: the decode GEMV (the qlinear kernel decode runs) streaming
+    int8 weights from HBM: K=1024, M=3 columns, 4 distinct 256 MiB weight
+    matrices (N = 262,144 rows each, 1 GiB total, larger than the 256 MB
+    MALL) rotated across launches; HIP events on the launch stream.
+  * roofline_gemm: the encode MFMA GEMM on the codebook-stack qkv shape
+    (M = 30,960 rows, K = 512, N = 1536).
+  * qlinear: per-launch GB/s on the K=1024, N in {1024, 4096} shapes.
+  * cpu_baseline: the C oracle (bit-exact restatement of the reference CPU
+    path, lane-parallel like the reference's executor) on a bounded sample.
+"""
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for path in (ROOT, ROOT / "tsac-metal_amd"):
+    if str(path) not in sys.path:
+        sys.path.insert(0, str(path))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--frames", type=int, default=2580)
+    p.add_argument("--batch", type=int, default=3)
+    p.add_argument("--geometry", choices=["reference", "wide"], default="reference")
+    p.add_argument("--only", choices=["all", "model", "gemv", "gemm"], default="all")
+    p.add_argument("--gemv-launches", type=int, default=64)
+    p.add_argument("--cpu-frames", type=int, default=660, help="CPU baseline sample (frames)")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def gemv_roofline(torch, native, launches):
+    """Decode GEMV streaming 1 GiB of distinct int8 weights (K=1024, M=3)."""
+    K, M, rows, mats = 1024, 3, 262144, 4
+    rng = np.random.default_rng(17)
+    linears = []
+    for i in range(mats):
+        values = np.frombuffer(rng.bytes(rows * K), np.int8).reshape(rows, K)
+        values = np.where(values == -128, np.int8(-127), values)  # int8 in [-127, 127]
+        scales = np.full((K // 256, rows), 0.0078125, np.float32)
+        bias = np.zeros(rows, np.float32)
+        linears.append(native.DeviceLinear(values, scales, bias))
+        del values
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    xb = (x.view(torch.int32) >> 16).to(torch.int16).contiguous()
+    q = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    s = torch.empty((M, K // 256), dtype=torch.float32, device="cuda")
+    native.bf8l(xb, M, K, q, s)
+    y = torch.empty((M, rows), dtype=torch.int16, device="cuda")
+    for i in range(8):
+        linears[i % mats].apply_quantized(q, s, M, y, path=native.PATH_GEMV)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(launches):
+        linears[i % mats].apply_quantized(q, s, M, y, path=native.PATH_GEMV)
+    stop.record()
+    torch.cuda.synchronize()
+    seconds = start.elapsed_time(stop) / 1000 / launches
+    traffic = K * rows + 16 * rows + 4 * rows + M * K + M * (K // 256) * 4 + 2 * M * rows
+    achieved = traffic / seconds / 1e9
+    del linears
+    torch.cuda.empty_cache()
+    return {"kernel": "gemv_kernel<1024,3>", "bound": "hbm", "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None, "bytes_per_launch": traffic, "avg_launch_us": round(seconds * 1e6, 2),
+            "shape": {"K": K, "N": rows, "M": M, "distinct_weight_bytes": mats * rows * K}}
+
+
+def gemm_roofline(torch, native, launches=20):
+    """Encode MFMA GEMM on the codebook qkv shape (M = 2580*12 rows)."""
+    M, K, N = 30960, 512, 1536
+    rng = np.random.default_rng(23)
+    from tsac_hip.synthetic import random_linear
+
+    linear = native.DeviceLinear(*random_linear(rng, K, N))
+    q = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda")
+    s = torch.full((M, K // 256), 0.01, dtype=torch.float32, device="cuda")
+    y = torch.empty((M, N), dtype=torch.int16, device="cuda")
+    for _ in range(3):
+        linear.apply_quantized(q, s, M, y, path=native.PATH_GEMM)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(launches):
+        linear.apply_quantized(q, s, M, y, path=native.PATH_GEMM)
+    stop.record()
+    torch.cuda.synchronize()
+    seconds = start.elapsed_time(stop) / 1000 / launches
+    tops = 2 * M * N * K / seconds / 1e12
+    return {"kernel": "gemm_kernel", "bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
+            "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
+            "avg_launch_us": round(seconds * 1e6, 2), "shape": {"M": M, "K": K, "N": N}}
+
+
+def qlinear_table(torch, native):
+    """Per-launch GEMV/GEMM rates on the isolated K=1024 configuration."""
+    rng = np.random.default_rng(29)
+    from tsac_hip.synthetic import random_linear
+
+    table = []
+    for n in (1024, 4096):
+        linear = native.DeviceLinear(*random_linear(rng, 1024, n, row_scales=True))
+        for m in (1, 3, 64, 1024, 4096):
+            q = torch.randint(-127, 128, (m, 1024), dtype=torch.int8, device="cuda")
+            s = torch.full((m, 4), 0.01, dtype=torch.float32, device="cuda")
+            y = torch.empty((m, n), dtype=torch.int16, device="cuda")
+            for _ in range(3):
+                linear.apply_quantized(q, s, m, y)
+            torch.cuda.synchronize()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 50
+            start.record()
+            for _ in range(reps):
+                linear.apply_quantized(q, s, m, y)
+            stop.record()
+            torch.cuda.synchronize()
+            seconds = start.elapsed_time(stop) / 1000 / reps
+            traffic = 1024 * n + 20 * n + m * 1024 + 16 * m + 2 * m * n
+            table.append({"N": n, "M": m, "path": "gemv" if m <= 8 else "gemm",
+                          "us": round(seconds * 1e6, 2), "GB/s": round(traffic / seconds / 1e9, 1),
+                          "TOP/s": round(2 * m * n * 1024 / seconds / 1e12, 2)})
+    return table
+
+
+def cpu_baseline(model, frames, batch):
+    """The C oracle on a bounded sample: pack_normal of `frames` frames (same
+    geometry, batch, books), lanes prepared concurrently like the reference's
+    executor (src/common/transformer.cpp:70-90)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    from oracle import Oracle, header
+    from tsac_hip.synthetic import random_tokens
+
+    threads = min(len(os.sched_getaffinity(0)), batch)
+    tokens = random_tokens(frames, 1, 12, seed=99)
+    om = Oracle().model(model)
+    t0 = time.perf_counter()
+    om.pack_normal(header(frames, batch, 1, 12), tokens, threads=threads)
+    seconds = time.perf_counter() - t0
+    return {"value": round(tokens.size / seconds, 1), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle pack_normal of {frames} frames x 12 codebooks (batch {batch}, "
+                      f"{tokens.size} tokens) in {seconds:.1f} s; host has "
+                      f"{len(os.sched_getaffinity(0))} cores, lane parallelism caps threads at {threads}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the probability model runs on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs an MI355X"
+    from tsac_hip import native
+    from tsac_hip.synthetic import REFERENCE, WIDE, random_model, random_tokens
+
+    geometry = REFERENCE if args.geometry == "reference" else WIDE
+    result = {}
+    if args.only in ("all", "model"):
+        model = random_model(geometry, seed=1)
+        hip_model = native.HipModel(model)
+        session = hip_model.session()
+        h = native.header(args.frames, args.batch, 1, 12)
+        tokens = random_tokens(args.frames, 1, 12, seed=5)
+        for _ in range(args.warmup):
+            stream = session.encode(h, tokens)
+            assert np.array_equal(session.decode(stream), tokens)
+        torch.cuda.synchronize()
+        encode_s = decode_s = 0.0
+        encode_split = [0.0, 0.0]
+        decode_split = [0.0, 0.0]
+        for _ in range(args.steps):
+            t0 = time.perf_counter()
+            stream = session.encode(h, tokens)
+            t1 = time.perf_counter()
+            e = session.timing()
+            decoded = session.decode(stream)
+            t2 = time.perf_counter()
+            d = session.timing()
+            encode_s += t1 - t0
+            decode_s += t2 - t1
+            encode_split[0] += e["model"]
+            encode_split[1] += e["range_coding"]
+            decode_split[0] += d["model"]
+            decode_split[1] += d["range_coding"]
+        torch.cuda.synchronize()
+        assert np.array_equal(decoded, tokens), "round trip failed"
+        encode_s /= args.steps
+        decode_s /= args.steps
+        count = tokens.size
+        result.update({
+            "value": round(count / (encode_s + decode_s), 1),
+            "ms_per_step": round(1000 * (encode_s + decode_s), 2),
+            "encode_tokens_per_s": round(count / encode_s, 1),
+            "decode_tokens_per_s": round(count / decode_s, 1),
+            "encode_decode_s_per_30s_stereo": round(encode_s + decode_s, 4),
+            "stream_bytes": len(stream),
+            "split_s": {"encode_model": round(encode_split[0] / args.steps, 4),
+                        "encode_range_coding": round(encode_split[1] / args.steps, 4),
+                        "decode_model": round(decode_split[0] / args.steps, 4),
+                        "decode_range_coding": round(decode_split[1] / args.steps, 4)},
+        })
+        del session, hip_model
+        torch.cuda.synchronize()
+    if args.only in ("all", "gemv"):
+        result["roofline"] = gemv_roofline(torch, native, args.gemv_launches)
+    if args.only in ("all", "gemm"):
+        result["roofline_gemm"] = gemm_roofline(torch, native)
+    if args.only == "all":
+        result["qlinear"] = qlinear_table(torch, native)
+        if not args.no_cpu:
+            result["cpu_baseline"] = cpu_baseline(random_model(geometry, seed=1), args.cpu_frames,
+                                                  args.batch)
+    line = {
+        "metric": "prob-model tokens/s",
+        "value": result.pop("value", None),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": result.pop("ms_per_step", None),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 (W8A8 int32-exact dots) + fp32/bf16",
+        "data": "synthetic tokens, seeded random-init weights in the reference packed layout",
+        "config": {"workload": f"encode+decode of a 30 s joint-stereo token stream: {args.frames} frames x "
+                               f"12 codebooks, entropy batch {args.batch}, {args.geometry} geometry",
+                   "frames": args.frames, "codebooks": 12, "batch": args.batch, "groups": 1,
+                   "geometry": {"width": geometry.width, "heads": geometry.heads,
+                                "head_width": geometry.head_width, "ffn": geometry.ffn,
+                                "layers": [geometry.temporal_layers, geometry.codebook_layers]},
+                   "parallelism": "single GPU"},
+        "baseline_metrics": "prob-model tokens/s; qlinear HBM GB/s; encode+decode s per 30 s stereo",
+    }
+    line.update(result)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
