@@ -256,7 +256,9 @@ int tsac_hip_linear_create(const tsac_hip_linear* weights, size_t K, size_t N,
             const std::size_t scale_bytes = K / 256 * N * 4;
             l->constants = DeviceBuffer((scale_bytes + 255) / 256 * 256 + N * 4);
             auto* c = l->constants.as<uint8_t>();
-            check_hip(hipMemcpy(l->values.get(), weights->values, K * N, hipMemcpyHostToDevice), "upload");
+            std::vector<int8_t> tiled(K * N);
+            tile_weights(weights->values, K, N, tiled.data());
+            check_hip(hipMemcpy(l->values.get(), tiled.data(), K * N, hipMemcpyHostToDevice), "upload");
             check_hip(hipMemcpy(c, weights->scales, scale_bytes, hipMemcpyHostToDevice), "upload");
             check_hip(hipMemcpy(c + (scale_bytes + 255) / 256 * 256, weights->bias, N * 4,
                                 hipMemcpyHostToDevice),

@@ -180,7 +180,9 @@ Model::Model(const Geometry& g, const LinearHost* projections, const uint16_t* c
     for (std::size_t i = 0; i < count; ++i)
     {
         const auto [k, n] = g.projection_shape(i);
-        check_hip(hipMemcpy(values + value_offset[i], projections[i].values, k * n, hipMemcpyHostToDevice),
+        std::vector<int8_t> tiled(k * n);
+        tile_weights(projections[i].values, k, n, tiled.data());
+        check_hip(hipMemcpy(values + value_offset[i], tiled.data(), k * n, hipMemcpyHostToDevice),
                   "upload weights");
         check_hip(hipMemcpy(constants + scale_offset[i], projections[i].scales, k / 256 * n * 4,
                             hipMemcpyHostToDevice),
@@ -548,224 +550,6 @@ void Session::batched(const Header& h, const uint16_t* tokens, uint16_t* distrib
     }
 }
 
-// One decode-shaped layer over `rows` lanes at cache position `position`.
-void Session::layer_step(bool temporal, std::size_t layer, uint16_t* x, std::size_t rows,
-                         std::size_t position, bool replay, std::size_t extent)
-{
-    const Geometry& g = model_->geometry();
-    const Model& m = *model_;
-    const std::size_t w = g.width;
-    const std::size_t layers = temporal ? g.temporal_layers : g.codebook_layers;
-    const std::size_t widest = std::max<std::size_t>({w, g.ffn, g.latent});
-    auto* q8 = arena_.get<int8_t>("s.q8", rows * widest);
-    auto* s8 = arena_.get<float>("s.s8", rows * widest / 256);
-    auto* qkv = arena_.get<uint16_t>("s.qkv", rows * 3 * w);
-    auto* query = arena_.get<uint16_t>("s.query", rows * w);
-    auto* att = arena_.get<uint16_t>("s.att", rows * w);
-    auto* hidden = arena_.get<uint16_t>("s.hidden", rows * g.ffn);
-    auto* partial = arena_.get<float>("s.partial", decode_partial_floats(rows, g.heads, g.head_width, extent));
-    auto* keys = arena_.get<uint16_t>(temporal ? "s.tk" : "s.ck", 0);
-    auto* values = arena_.get<uint16_t>(temporal ? "s.tv" : "s.cv", 0);
-    auto* err = errors_.as<uint32_t>();
-    const std::size_t lane_stride = layers * extent * w;
-    uint16_t* layer_keys = keys + layer * extent * w;
-    uint16_t* layer_values = values + layer * extent * w;
-    const std::size_t n1 = m.norm_index(temporal, layer, false), n2 = m.norm_index(temporal, layer, true);
-    quantize_rows(x, rows, w, Prologue::layer_norm, m.norm_gain(n1), m.norm_bias(n1), q8, s8, nullptr,
-                  err, stream_);
-    linear(m.layer(temporal, layer, 0), q8, s8, rows, qkv, nullptr, LinearPath::automatic, stream_);
-    append_qkv(qkv, rows, w, g.head_width,
-               temporal ? m.rotations() + position * g.head_width : nullptr, query,
-               layer_keys + position * w, layer_values + position * w, lane_stride, stream_);
-    attention_decode(query, layer_keys, layer_values, lane_stride, rows, position + 1, g.heads,
-                     g.head_width, g.attention_scale, replay, partial, att, stream_);
-    quantize_rows(att, rows, w, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err, stream_);
-    linear(m.layer(temporal, layer, 1), q8, s8, rows, x, x, LinearPath::automatic, stream_);
-    quantize_rows(x, rows, w, Prologue::layer_norm, m.norm_gain(n2), m.norm_bias(n2), q8, s8, nullptr,
-                  err, stream_);
-    linear(m.layer(temporal, layer, 2), q8, s8, rows, hidden, nullptr, LinearPath::automatic, stream_);
-    quantize_rows(hidden, rows, g.ffn, Prologue::gelu, nullptr, nullptr, q8, s8, nullptr, err, stream_);
-    linear(m.layer(temporal, layer, 3), q8, s8, rows, x, x, LinearPath::automatic, stream_);
-}
-
-// Frame-by-frame, book-by-book pass with resident KV caches: the decode-side
-// shape (src/common/transformer.cpp:137-244 schedule, all ready lanes batched).
-void Session::stepwise(const Header& h, const uint16_t* known, RangeDecoder* decoder,
-                       uint16_t* tokens_out, uint16_t* distributions)
-{
-    const Geometry& g = model_->geometry();
-    const Model& m = *model_;
-    const std::size_t C = h.codebooks, G = h.groups, w = g.width;
-    const Lanes lanes(h);
-    const std::size_t independent = lanes.count * G;
-    if (!independent)
-    {
-        return;
-    }
-    const std::size_t longest = lanes.length(0);
-    const std::size_t extent = std::min<std::size_t>(longest, g.context);
-    arena_.get<uint16_t>("s.tk", independent * g.temporal_layers * extent * w);
-    arena_.get<uint16_t>("s.tv", independent * g.temporal_layers * extent * w);
-    arena_.get<uint16_t>("s.ck", independent * g.codebook_layers * C * w);
-    arena_.get<uint16_t>("s.cv", independent * g.codebook_layers * C * w);
-    auto* d_feedback = arena_.get<uint16_t>("s.feedback", independent * C);
-    auto* d_current = arena_.get<uint16_t>("s.current", independent * C);
-    auto* embedded = arena_.get<uint16_t>("s.embedded", independent * g.latent);
-    auto* prefix = arena_.get<uint16_t>("s.prefix", independent * g.latent);
-    auto* x = arena_.get<uint16_t>("s.x", independent * w);
-    auto* conditioning = arena_.get<uint16_t>("s.cond", independent * w);
-    auto* y = arena_.get<uint16_t>("s.y", independent * w);
-    auto* logits = arena_.get<uint16_t>("s.logits", independent * g.alphabet);
-    auto* probs = arena_.get<uint16_t>("s.probs", independent * g.alphabet);
-    auto* nodes = arena_.get<float>("s.nodes", independent * 1024);
-    const std::size_t widest = std::max<std::size_t>({w, g.ffn, g.latent});
-    auto* q8 = arena_.get<int8_t>("s.q8", independent * widest);
-    auto* s8 = arena_.get<float>("s.s8", independent * widest / 256);
-    auto* err = errors_.as<uint32_t>();
-    staging_.reserve(independent * g.alphabet * 2);
-    staging_nodes_.reserve(independent * 1024 * 4);
-    staging_tokens_.reserve(independent * C * 2 * 2);
-    auto* host_probs = staging_.as<uint16_t>();
-    auto* host_nodes = staging_nodes_.as<float>();
-    auto* host_feedback = staging_tokens_.as<uint16_t>();
-    auto* host_current = host_feedback + independent * C;
-
-    // Per-lane complete-frame history, newest last (src/common/transformer.cpp:222-244).
-    std::vector<std::vector<uint16_t>> history(independent);
-    std::size_t context_used = 0;
-    double host_seconds = 0;
-
-    const auto temporal_step = [&](std::size_t active, std::size_t position, bool replay)
-    {
-        check_hip(hipMemcpyAsync(d_feedback, host_feedback, active * C * 2, hipMemcpyHostToDevice, stream_),
-                  "upload feedback");
-        embed_sum(m.embeddings(), g.alphabet, g.latent, d_feedback, C, active, embedded, stream_);
-        quantize_rows(embedded, active, g.latent, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err,
-                      stream_);
-        linear(m.temporal_projection(), q8, s8, active, x, nullptr, LinearPath::automatic, stream_);
-        for (std::size_t l = 0; l < g.temporal_layers; ++l)
-        {
-            layer_step(true, l, x, active, position, replay, extent);
-        }
-        // The feedback staging is reused by the next step: wait for the upload.
-        check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
-    };
-
-    for (std::size_t step = 0; step < lanes.steps(); ++step)
-    {
-        const std::size_t active = step < lanes.base ? independent : lanes.extra * G;
-        if (context_used == g.context)
-        {
-            for (std::size_t i = 0; i < active; ++i)
-            {
-                require(history[i].size() == replay_frames * C, "incomplete Transformer replay history");
-            }
-            context_used = 0;
-            for (std::size_t k = 0; k < replay_frames; ++k)
-            {
-                for (std::size_t i = 0; i < active; ++i)
-                {
-                    std::memcpy(host_feedback + i * C, history[i].data() + k * C, C * 2);
-                }
-                temporal_step(active, context_used++, true);
-            }
-        }
-        else
-        {
-            for (std::size_t i = 0; i < active; ++i)
-            {
-                if (history[i].empty())
-                {
-                    std::memset(host_feedback + i * C, 0, C * 2);
-                }
-                else
-                {
-                    std::memcpy(host_feedback + i * C, history[i].data() + history[i].size() - C, C * 2);
-                }
-            }
-            temporal_step(active, context_used++, false);
-        }
-        const std::size_t f = m.final_norm_index(true);
-        layer_norm_rows(x, active, w, m.norm_gain(f), m.norm_bias(f), conditioning, stream_);
-
-        for (std::size_t book = 0; book < C; ++book)
-        {
-            if (book == 0)
-            {
-                check_hip(hipMemcpyAsync(y, conditioning, active * w * 2, hipMemcpyDeviceToDevice, stream_),
-                          "copy conditioning");
-            }
-            else
-            {
-                embed_accumulate(m.embeddings(), g.alphabet, g.latent, d_current + (book - 1), C, book - 1,
-                                 active, book == 1 ? nullptr : prefix, prefix, stream_);
-                quantize_rows(prefix, active, g.latent, Prologue::none, nullptr, nullptr, q8, s8, nullptr,
-                              err, stream_);
-                linear(m.codebook_projection(), q8, s8, active, y, nullptr, LinearPath::automatic, stream_);
-            }
-            add_rows(y, m.positions() + book * w, active, w, 1, y, stream_);
-            for (std::size_t l = 0; l < g.codebook_layers; ++l)
-            {
-                layer_step(false, l, y, active, book, false, C);
-            }
-            const std::size_t fc = m.final_norm_index(false);
-            quantize_rows(y, active, w, Prologue::layer_norm, m.norm_gain(fc), m.norm_bias(fc), q8, s8,
-                          nullptr, err, stream_);
-            linear(m.output_projection(), q8, s8, active, logits, nullptr, LinearPath::automatic, stream_);
-            softmax_rows(logits, active, g.alphabet, probs, err, stream_);
-            if (decoder)
-            {
-                categorical_trees(probs, active, nodes, stream_);
-                check_hip(hipMemcpyAsync(host_nodes, nodes, active * 1024 * 4, hipMemcpyDeviceToHost, stream_),
-                          "read masses");
-            }
-            check_hip(hipMemcpyAsync(host_probs, probs, active * g.alphabet * 2, hipMemcpyDeviceToHost,
-                                     stream_),
-                      "read distributions");
-            check_errors();
-            const double t0 = now();
-            for (std::size_t i = 0; i < active; ++i)
-            {
-                const std::size_t lane = i / G, group = i % G;
-                const std::size_t frame = lanes.start(lane) + step;
-                const std::size_t offset = (frame * G + group) * C + book;
-                uint16_t token;
-                if (decoder)
-                {
-                    token = uint16_t(decode_categorical(*decoder, host_nodes + i * 1024, host_probs + i * g.alphabet));
-                }
-                else
-                {
-                    token = known[offset];
-                }
-                if (tokens_out)
-                {
-                    tokens_out[offset] = token;
-                }
-                if (distributions)
-                {
-                    std::memcpy(distributions + offset * g.alphabet, host_probs + i * g.alphabet, g.alphabet * 2);
-                }
-                host_current[i * C + book] = token;
-            }
-            host_seconds += now() - t0;
-            check_hip(hipMemcpyAsync(d_current, host_current, active * C * 2, hipMemcpyHostToDevice, stream_),
-                      "upload tokens");
-            check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
-        }
-        for (std::size_t i = 0; i < active; ++i)
-        {
-            auto& past = history[i];
-            past.insert(past.end(), host_current + i * C, host_current + (i + 1) * C);
-            if (past.size() > replay_frames * C)
-            {
-                past.erase(past.begin(), past.begin() + C);
-            }
-        }
-    }
-    timing_[1] = host_seconds;
-}
-
 std::vector<uint8_t> Session::encode(Header h, const uint16_t* tokens, std::size_t count)
 {
     check_hip(hipSetDevice(model_->device()), "hipSetDevice");
@@ -831,12 +615,14 @@ std::vector<uint16_t> Session::decode(const uint8_t* stream, std::size_t length)
     require(h.method == 1, "unpack_normal requires method 1");
     validate(h, nullptr, h.symbols());
     std::vector<uint16_t> tokens(h.symbols());
-    RangeDecoder decoder(stream + h.payload_offset, h.payload_bytes);
+    // The initial interval is validated on the host (src/format/range.cpp:122-129).
+    RangeDecoder initial(stream + h.payload_offset, h.payload_bytes);
     reset_errors();
-    stepwise(h, nullptr, &decoder, tokens.data(), nullptr);
+    stepwise(h, nullptr, stream + h.payload_offset, h.payload_bytes, tokens.data(), nullptr);
+    check_errors();
     require(token_crc32(tokens.data(), tokens.size()) == h.token_crc, "invalid token CRC32");
     const double t1 = now();
-    timing_ = {t1 - t0 - timing_[1], timing_[1], t1 - t0};
+    timing_ = {t1 - t0, 0.0, t1 - t0};
     return tokens;
 }
 
@@ -850,7 +636,7 @@ void Session::distributions(Header h, const uint16_t* tokens, std::size_t count,
     reset_errors();
     if (decode_pass)
     {
-        stepwise(h, tokens, nullptr, nullptr, out);
+        stepwise(h, tokens, nullptr, 0, nullptr, out);
     }
     else
     {

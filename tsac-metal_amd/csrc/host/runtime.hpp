@@ -199,12 +199,14 @@ private:
     void stack_rows(bool temporal, uint16_t* x, std::size_t rows, const int* starts,
                     const int* lengths, const int* replays, std::size_t sequences,
                     std::size_t max_length, const std::string& tag);
-    // Stepwise pass. `known` tokens are teacher-forced when non-null; otherwise
-    // symbols are range-decoded from `decoder`.
-    void stepwise(const Header& h, const uint16_t* known, RangeDecoder* decoder,
-                  uint16_t* tokens_out, uint16_t* distributions);
+    // Stepwise pass, enqueued without host round trips. `known` tokens are
+    // teacher-forced when non-null; otherwise symbols are range-decoded on the
+    // GPU from `payload`. Writes tokens (and, if requested, the BF16
+    // distributions) in token order.
+    void stepwise(const Header& h, const uint16_t* known, const uint8_t* payload,
+                  std::size_t payload_bytes, uint16_t* tokens_out, uint16_t* distributions);
     void layer_step(bool temporal, std::size_t layer, uint16_t* x, std::size_t rows,
-                    std::size_t position, bool replay, std::size_t extent);
+                    std::size_t first_lane, std::size_t position, bool replay, std::size_t extent);
 
     std::shared_ptr<const Model> model_;
     hipStream_t stream_ = nullptr;

@@ -1,0 +1,693 @@
+// Decode-side kernels (see decode.hpp). Arithmetic is shared with the batched
+// path through row_ops.hpp / device_numeric.hpp, so both passes produce the same
+// bits: the same BF8L quantiser, LayerNorm, embedding sums, exact int8 block
+// dots and ordered per-block fma chain (src/scalar/packed_linear.cpp:16-27),
+// attention recurrence (src/scalar/attention.cpp:62-101), softmax
+// (src/common/probability.cpp:96-122) and categorical bisection
+// (src/format/categorical.cpp:119-142) with the range decoder
+// (src/format/range.cpp:131-151).
+#include "decode.hpp"
+#include "row_ops.hpp"
+
+namespace tsac_hip
+{
+namespace
+{
+constexpr int tile_rows = 64;
+constexpr int segments = 16;
+constexpr int max_columns = 8;
+
+__device__ __forceinline__ std::size_t tile_offset(int t, int b, int s, int blocks)
+{
+    return ((std::size_t(t) * blocks + b) * segments + s) * (tile_rows * 16);
+}
+
+__device__ __forceinline__ void rotate(float& re, float& im, const uint16_t* c)
+{
+    const float cosine = bf16_to_float(c[0]), sine = bf16_to_float(c[1]);
+    const float im_sine = im * sine;
+    const float re_sine = re * sine;
+    const float r = __builtin_fmaf(re, cosine, -im_sine);
+    const float i = __builtin_fmaf(im, cosine, re_sine);
+    re = bf16_to_float(float_to_bf16(r));
+    im = bf16_to_float(float_to_bf16(i));
+}
+
+// ------------------------------------------------------------------ fused projection
+
+template <int V, Input I>
+__device__ __forceinline__ void input_row(const FusedLinear& a, int m, int lane, int8_t* q_row,
+                                          float* s_row, bool write_prefix)
+{
+    constexpr int K = wave * V;
+    uint16_t v[V];
+    if constexpr (I == Input::bf16 || I == Input::layer_norm)
+    {
+        load_row<V>(a.x + std::size_t(m) * a.x_stride + lane * V, v);
+        if constexpr (I == Input::layer_norm)
+        {
+            layer_norm_lane<V>(v, a.gain, a.beta, lane);
+        }
+    }
+    else if constexpr (I == Input::embed_sum)
+    {
+        // src/common/cpu_transformer.tpp:205-224: copy book 0, add later books in order.
+        const uint16_t* t = a.tokens + std::size_t(m) * a.token_stride;
+        load_row<V>(a.embeddings + std::size_t(t[0]) * K + lane * V, v);
+        for (int b = 1; b < a.books; ++b)
+        {
+            uint16_t e[V];
+            load_row<V>(a.embeddings + (std::size_t(b) * a.alphabet + t[b]) * K + lane * V, e);
+#pragma unroll
+            for (int i = 0; i < V; ++i)
+            {
+                v[i] = float_to_bf16(bf16_to_float(v[i]) + bf16_to_float(e[i]));
+            }
+        }
+    }
+    else
+    {
+        const int token = a.tokens[std::size_t(m) * a.token_stride + a.token_offset];
+        load_row<V>(a.embeddings + (std::size_t(a.book) * a.alphabet + token) * K + lane * V, v);
+        if (a.x)
+        {
+            uint16_t p[V];
+            load_row<V>(a.x + std::size_t(m) * K + lane * V, p);
+#pragma unroll
+            for (int i = 0; i < V; ++i)
+            {
+                v[i] = float_to_bf16(bf16_to_float(p[i]) + bf16_to_float(v[i]));
+            }
+        }
+        if (write_prefix)
+        {
+            store_row<V>(a.prefix_out + std::size_t(m) * K + lane * V, v);
+        }
+    }
+    bf8l_lane<V>(v, lane, q_row, s_row, a.error);
+}
+
+template <int V, Input I>
+__global__ __launch_bounds__(256) void fused_linear_kernel(const FusedLinear a)
+{
+    constexpr int K = wave * V, blocks = K / 256;
+    __shared__ __attribute__((aligned(16))) int8_t q[max_columns * K];
+    __shared__ float scales[max_columns * blocks];
+    __shared__ int dots[blocks * max_columns * tile_rows];
+    const int lane = threadIdx.x % wave;
+    const int warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
+    const int tile = blockIdx.x;
+    const int M = a.M, N = int(a.w.N);
+    for (int m = warp; m < M; m += 4)
+    {
+        input_row<V, I>(a, m, lane, q + m * K, scales + m * blocks, tile == 0);
+    }
+    __syncthreads();
+    for (int b = warp; b < blocks; b += 4)
+    {
+        uint4 w[segments];
+        const int8_t* base = a.w.values + tile_offset(tile, b, 0, blocks) + lane * 16;
+#pragma unroll
+        for (int s = 0; s < segments; ++s)
+        {
+            w[s] = *reinterpret_cast<const uint4*>(base + s * tile_rows * 16);
+        }
+        for (int m = 0; m < M; ++m)
+        {
+            const uint4* x = reinterpret_cast<const uint4*>(q + m * K + b * 256);
+            int dot = 0;
+#pragma unroll
+            for (int s = 0; s < segments; ++s)
+            {
+                const uint4 u = x[s];
+                dot = __builtin_amdgcn_sdot4(int(w[s].x), int(u.x), dot, false);
+                dot = __builtin_amdgcn_sdot4(int(w[s].y), int(u.y), dot, false);
+                dot = __builtin_amdgcn_sdot4(int(w[s].z), int(u.z), dot, false);
+                dot = __builtin_amdgcn_sdot4(int(w[s].w), int(u.w), dot, false);
+            }
+            dots[(b * max_columns + m) * tile_rows + lane] = dot;
+        }
+    }
+    __syncthreads();
+    // Two adjacent rows per thread (rotary pairs), one column.
+    const int pair = threadIdx.x % 32, m = threadIdx.x / 32;
+    if (m >= M)
+    {
+        return;
+    }
+    const int r0 = 2 * pair, n0 = tile * tile_rows + r0;
+    float sum0 = 0.0f, sum1 = 0.0f;
+    for (int b = 0; b < blocks; ++b)
+    {
+        const float as = scales[m * blocks + b];
+        const float scale0 = a.w.scales[std::size_t(b) * N + n0] * as;
+        const float scale1 = a.w.scales[std::size_t(b) * N + n0 + 1] * as;
+        sum0 = __builtin_fmaf(float(dots[(b * max_columns + m) * tile_rows + r0]), scale0, sum0);
+        sum1 = __builtin_fmaf(float(dots[(b * max_columns + m) * tile_rows + r0 + 1]), scale1, sum1);
+    }
+    uint16_t y0 = float_to_bf16(sum0 + a.w.bias[n0]);
+    uint16_t y1 = float_to_bf16(sum1 + a.w.bias[n0 + 1]);
+    switch (a.output)
+    {
+    case Output::plain:
+        break;
+    case Output::residual:
+    {
+        const uint16_t* r = a.residual + std::size_t(m) * a.residual_stride + n0;
+        y0 = float_to_bf16(bf16_to_float(r[0]) + bf16_to_float(y0));
+        y1 = float_to_bf16(bf16_to_float(r[1]) + bf16_to_float(y1));
+        break;
+    }
+    case Output::gelu:
+        y0 = gelu_bf16(y0);
+        y1 = gelu_bf16(y1);
+        break;
+    case Output::qkv:
+    {
+        const int position = a.position ? *a.position : a.fixed_position;
+        const int w = a.width;
+        float re = bf16_to_float(y0), im = bf16_to_float(y1);
+        if (n0 < 2 * w && a.rotations)
+        {
+            rotate(re, im, a.rotations + std::size_t(position) * a.head_width + n0 % a.head_width);
+        }
+        const uint32_t packed = float_to_bf16(re) | (uint32_t(float_to_bf16(im)) << 16);
+        uint16_t* dst;
+        if (n0 < w)
+        {
+            dst = a.query + std::size_t(m) * w + n0;
+        }
+        else if (n0 < 2 * w)
+        {
+            dst = a.keys + std::size_t(m) * a.lane_stride + std::size_t(position) * w + (n0 - w);
+        }
+        else
+        {
+            dst = a.values + std::size_t(m) * a.lane_stride + std::size_t(position) * w + (n0 - 2 * w);
+        }
+        *reinterpret_cast<uint32_t*>(dst) = packed;
+        return;
+    }
+    }
+    *reinterpret_cast<uint32_t*>(a.y + std::size_t(m) * a.y_stride + n0) = y0 | (uint32_t(y1) << 16);
+}
+
+template <int V> void launch_fused(const FusedLinear& a, hipStream_t stream)
+{
+    const dim3 grid(unsigned(a.w.N / tile_rows));
+    switch (a.input)
+    {
+    case Input::bf16:
+        fused_linear_kernel<V, Input::bf16><<<grid, 256, 0, stream>>>(a);
+        break;
+    case Input::layer_norm:
+        fused_linear_kernel<V, Input::layer_norm><<<grid, 256, 0, stream>>>(a);
+        break;
+    case Input::embed_sum:
+        fused_linear_kernel<V, Input::embed_sum><<<grid, 256, 0, stream>>>(a);
+        break;
+    case Input::embed_accumulate:
+        fused_linear_kernel<V, Input::embed_accumulate><<<grid, 256, 0, stream>>>(a);
+        break;
+    }
+}
+
+// ------------------------------------------------------------------ attention
+
+constexpr int step_waves = 16;
+
+template <int HW>
+__global__ __launch_bounds__(step_waves * wave) void attention_step_kernel(
+    const uint16_t* __restrict__ query, const uint16_t* __restrict__ keys,
+    const uint16_t* __restrict__ values, long long lane_stride, int width, int heads, float scale,
+    const int* position_ptr, int fixed_position, int replay, uint16_t* __restrict__ out)
+{
+    extern __shared__ float partial[]; // [blocks][2 + HW]
+    __shared__ float qf[HW];
+    __shared__ float weights[step_waves][64];
+    const int lane_index = blockIdx.x / heads, head = blockIdx.x % heads;
+    const int lane = threadIdx.x % wave;
+    const int warp = threadIdx.x / wave;
+    const int time = (position_ptr ? *position_ptr : fixed_position) + 1;
+    const int blocks = (time + 63) / 64;
+    const bool round_values = time > 64 || replay;
+    const uint16_t* k = keys + std::size_t(lane_index) * lane_stride + head * HW;
+    const uint16_t* v = values + std::size_t(lane_index) * lane_stride + head * HW;
+    for (int j = threadIdx.x; j < HW; j += blockDim.x)
+    {
+        qf[j] = bf16_to_float(query[std::size_t(lane_index) * width + head * HW + j]);
+    }
+    __syncthreads();
+    for (int block = warp; block < blocks; block += step_waves)
+    {
+        const int start = block * 64;
+        const int count = time - start < 64 ? time - start : 64;
+        float score = -__builtin_inff();
+        if (lane < count)
+        {
+            const uint16_t* row = k + std::size_t(start + lane) * width;
+            float dot = 0.0f;
+#pragma unroll
+            for (int c = 0; c < HW / 8; ++c)
+            {
+                const uint4 u = reinterpret_cast<const uint4*>(row)[c];
+                const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    dot = __builtin_fmaf(qf[8 * c + 2 * i], bf16_to_float(uint16_t(w4[i] & 0xffff)), dot);
+                    dot = __builtin_fmaf(qf[8 * c + 2 * i + 1], bf16_to_float(uint16_t(w4[i] >> 16)), dot);
+                }
+            }
+            score = dot * scale;
+        }
+        const float maximum = group_max<wave>(score);
+        float e = 0.0f;
+        if (lane < count)
+        {
+            const float shifted = score - maximum;
+            e = original_exp(shifted);
+        }
+        const float sum = tree_sum<wave>(e);
+        weights[warp][lane] = e;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        float* record = partial + std::size_t(block) * (2 + HW);
+        if (lane == 0)
+        {
+            record[0] = maximum;
+            record[1] = sum;
+        }
+        for (int j = lane; j < HW; j += 64)
+        {
+            float s = 0.0f;
+            for (int t = 0; t < count; ++t)
+            {
+                s = __builtin_fmaf(bf16_to_float(v[std::size_t(start + t) * width + j]), weights[warp][t], s);
+            }
+            record[2 + j] = round_values ? round_bf16(s) : s;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    if (warp != 0)
+    {
+        return;
+    }
+    constexpr int per_lane = (HW + 63) / 64;
+    float numerator[per_lane];
+#pragma unroll
+    for (int i = 0; i < per_lane; ++i)
+    {
+        numerator[i] = 0.0f;
+    }
+    float running_maximum = -__builtin_inff(), total = 0.0f;
+    for (int b = 0; b < blocks; ++b)
+    {
+        const float* record = partial + std::size_t(b) * (2 + HW);
+        const float maximum = record[0];
+        const float difference = maximum - running_maximum;
+        const float factor = original_exp(-__builtin_fabsf(difference));
+        const float old_scale = running_maximum > maximum ? 1.0f : factor;
+        const float new_scale = running_maximum > maximum ? factor : 1.0f;
+        const float old_total = total * old_scale;
+        total = __builtin_fmaf(record[1], new_scale, old_total);
+#pragma unroll
+        for (int i = 0; i < per_lane; ++i)
+        {
+            const int j = lane + 64 * i;
+            if (j < HW)
+            {
+                const float old = numerator[i] * old_scale;
+                numerator[i] = __builtin_fmaf(record[2 + j], new_scale, old);
+            }
+        }
+        running_maximum = running_maximum < maximum ? maximum : running_maximum;
+    }
+    const float reciprocal = 1.0f / total;
+#pragma unroll
+    for (int i = 0; i < per_lane; ++i)
+    {
+        const int j = lane + 64 * i;
+        if (j < HW)
+        {
+            out[std::size_t(lane_index) * width + head * HW + j] = float_to_bf16(numerator[i] * reciprocal);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ norms
+
+template <int V>
+__global__ __launch_bounds__(256) void layer_norm_add_kernel(const uint16_t* x, int rows,
+                                                             const uint16_t* __restrict__ gain,
+                                                             const uint16_t* __restrict__ bias,
+                                                             const uint16_t* __restrict__ add_row,
+                                                             uint16_t* out)
+{
+    constexpr int width = wave * V;
+    const int lane = threadIdx.x % wave;
+    const int row = blockIdx.x * 4 + threadIdx.x / wave;
+    if (row >= rows)
+    {
+        return;
+    }
+    uint16_t v[V];
+    load_row<V>(x + std::size_t(row) * width + lane * V, v);
+    layer_norm_lane<V>(v, gain, bias, lane);
+    if (add_row)
+    {
+        uint16_t p[V];
+        load_row<V>(add_row + lane * V, p);
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+        {
+            v[i] = float_to_bf16(bf16_to_float(v[i]) + bf16_to_float(p[i]));
+        }
+    }
+    store_row<V>(out + std::size_t(row) * width + lane * V, v);
+}
+
+// ------------------------------------------------------------------ sampling
+
+// conditional_q15 (src/format/categorical.cpp:76-89).
+__device__ __forceinline__ uint16_t q15(float left, float mass)
+{
+    const float value = ftz_divide(ftz_multiply(left, 32768.0f), mass);
+    if (!is_finite(value) || value >= 0x1p63f || value < -0x1p63f)
+    {
+        return 1;
+    }
+    const long long integer = static_cast<long long>(__builtin_rintf(value));
+    const int low = int(uint32_t(uint64_t(integer)));
+    return uint16_t(low < 1 ? 1 : (low > 32767 ? 32767 : low));
+}
+
+constexpr int sample_waves = 8;
+
+// Heap-ordered subtree masses of one 1024-symbol row held 16 per lane, into
+// nodes[1..1023] (shared memory).
+__device__ __forceinline__ bool build_masses(const float (&leaf)[16], int lane, float* nodes)
+{
+    bool valid = true;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+    {
+        valid = valid && is_finite(leaf[i]) && leaf[i] >= 0.0f;
+    }
+    float level[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+    {
+        level[i] = ftz_add(leaf[2 * i], leaf[2 * i + 1]);
+        nodes[512 + lane * 8 + i] = level[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        level[i] = ftz_add(level[2 * i], level[2 * i + 1]);
+        nodes[256 + lane * 4 + i] = level[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+    {
+        level[i] = ftz_add(level[2 * i], level[2 * i + 1]);
+        nodes[128 + lane * 2 + i] = level[i];
+    }
+    float v = ftz_add(level[0], level[1]);
+    nodes[64 + lane] = v;
+#pragma unroll
+    for (int l = 0; l < 6; ++l)
+    {
+        v = ftz_add(v, lane_xor(v, 1 << l));
+        const int size = 32 << l;
+        if ((lane * 16) % size == 0)
+        {
+            nodes[1024 / size + lane * 16 / size] = v;
+        }
+    }
+    return __all(valid);
+}
+
+__global__ __launch_bounds__(sample_waves * wave) void sample_kernel(const Sample a)
+{
+    __shared__ float nodes[sample_waves][1024];
+    __shared__ uint16_t leaves[sample_waves][1024];
+    __shared__ int valid[sample_waves];
+    const int lane = threadIdx.x % wave, warp = threadIdx.x / wave;
+    const int step = a.step ? *a.step : a.fixed_step;
+    for (int first = 0; first < a.lanes; first += sample_waves)
+    {
+        const int i = first + warp;
+        if (i < a.lanes)
+        {
+            // Softmax (src/common/probability.cpp:96-122), 16 values per lane.
+            uint16_t v[16];
+            load_row<16>(a.logits + std::size_t(i) * 1024 + lane * 16, v);
+            float maximum = -__builtin_inff();
+            bool finite = true;
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+            {
+                const float value = bf16_to_float(v[k]);
+                finite = finite && is_finite(value);
+                maximum = maximum < value ? value : maximum;
+            }
+            if (!finite)
+            {
+                a.error[0] = 1u;
+            }
+            maximum = group_max<wave>(maximum);
+            float e[16], leaves_sum[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+            {
+                const float shifted = bf16_to_float(v[k]) - maximum;
+                e[k] = original_exp(shifted);
+                leaves_sum[k] = e[k];
+            }
+            const float total = row_sum<16>(leaves_sum);
+            const float reciprocal = 1.0f / total;
+            float p[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+            {
+                v[k] = float_to_bf16(e[k] * reciprocal);
+                p[k] = bf16_to_float(v[k]);
+            }
+            store_row<16>(&leaves[warp][lane * 16], v);
+            const std::size_t row = std::size_t(a.row_base[i]) + std::size_t(step) * a.step_stride + a.book;
+            if (a.distributions)
+            {
+                store_row<16>(a.distributions + row * 1024 + lane * 16, v);
+            }
+            if (a.state)
+            {
+                const bool ok = build_masses(p, lane, nodes[warp]);
+                if (lane == 0)
+                {
+                    valid[warp] = ok;
+                }
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0)
+        {
+            const int count = a.lanes - first < sample_waves ? a.lanes - first : sample_waves;
+            for (int w = 0; w < count; ++w)
+            {
+                const int lane_index = first + w;
+                const std::size_t row =
+                    std::size_t(a.row_base[lane_index]) + std::size_t(step) * a.step_stride + a.book;
+                int token;
+                if (a.known)
+                {
+                    token = a.known[row];
+                }
+                else
+                {
+                    // decode_categorical + RangeDecoder::get.
+                    DecoderState s = *a.state;
+                    if (!valid[w])
+                    {
+                        s.failed = 1;
+                    }
+                    int base = 0, count_left = 1024;
+                    float mass = 1.0f;
+                    while (count_left > 1 && !s.failed)
+                    {
+                        const int half = count_left / 2;
+                        const float left = half == 1 ? flush(bf16_to_float(leaves[w][base]))
+                                                     : nodes[w][1024 / half + base / half];
+                        const uint16_t p0 = q15(left, mass);
+                        const uint32_t range0 = uint32_t((uint64_t(s.range) * p0) >> 15);
+                        const bool bit = s.code >= range0;
+                        if (bit)
+                        {
+                            s.code -= range0;
+                            s.range -= range0;
+                            base += half;
+                            count_left -= half;
+                            mass = flush(flush(mass) - flush(left));
+                        }
+                        else
+                        {
+                            s.range = range0;
+                            count_left = half;
+                            mass = left;
+                        }
+                        while (s.range < 0xff01u)
+                        {
+                            s.range <<= 8;
+                            const uint32_t byte = s.offset < a.payload_bytes ? a.payload[s.offset] : 0u;
+                            s.offset += s.offset < a.payload_bytes ? 1 : 0;
+                            s.code = (s.code << 8) + byte;
+                        }
+                        if (!(s.code < s.range))
+                        {
+                            s.failed = 1;
+                        }
+                    }
+                    *a.state = s;
+                    if (s.failed)
+                    {
+                        a.error[1] = 1u;
+                    }
+                    token = base;
+                }
+                a.current[std::size_t(lane_index) * a.books + a.book] = uint16_t(token);
+                a.tokens[row] = uint16_t(token);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+__global__ void gather_frame_kernel(const uint16_t* tokens, const int* row_base, int frame,
+                                    int step_stride, int books, int lanes, uint16_t* dst)
+{
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < lanes * books; i += gridDim.x * blockDim.x)
+    {
+        const int lane = i / books, b = i % books;
+        dst[i] = tokens[std::size_t(row_base[lane]) + std::size_t(frame) * step_stride + b];
+    }
+}
+
+__global__ void advance_kernel(int* counter, int amount)
+{
+    *counter += amount;
+}
+} // namespace
+
+void fused_linear(const FusedLinear& a, hipStream_t stream)
+{
+    require(a.M >= 1 && a.M <= max_columns, "fused linear: 1..8 columns");
+    require(a.w.N % tile_rows == 0 && a.w.K % 256 == 0, "fused linear: shape");
+    require(a.error != nullptr, "fused linear: error word");
+    switch (a.w.K)
+    {
+    case 256:
+        launch_fused<4>(a, stream);
+        break;
+    case 512:
+        launch_fused<8>(a, stream);
+        break;
+    case 1024:
+        launch_fused<16>(a, stream);
+        break;
+    case 2048:
+        launch_fused<32>(a, stream);
+        break;
+    case 4096:
+        launch_fused<64>(a, stream);
+        break;
+    default:
+        throw Error("fused linear: K must be one of 256, 512, 1024, 2048, 4096");
+    }
+    check_hip(hipGetLastError(), "fused linear launch");
+}
+
+void attention_step(const uint16_t* query, const uint16_t* keys, const uint16_t* values,
+                    long long lane_stride, std::size_t lanes, std::size_t width,
+                    std::size_t heads, std::size_t head_width, float scale, const int* position,
+                    int fixed_position, std::size_t max_time, bool replay, uint16_t* out,
+                    hipStream_t stream)
+{
+    require(lanes > 0 && max_time > 0 && width == heads * head_width, "attention step: shape");
+    const std::size_t lds = (max_time + 63) / 64 * (2 + head_width) * sizeof(float);
+    require(lds <= 64 * 1024, "attention step: history too long");
+    const unsigned grid = unsigned(lanes * heads);
+    switch (head_width)
+    {
+    case 64:
+        attention_step_kernel<64><<<grid, step_waves * wave, lds, stream>>>(
+            query, keys, values, lane_stride, int(width), int(heads), scale, position, fixed_position,
+            replay ? 1 : 0, out);
+        break;
+    case 128:
+        attention_step_kernel<128><<<grid, step_waves * wave, lds, stream>>>(
+            query, keys, values, lane_stride, int(width), int(heads), scale, position, fixed_position,
+            replay ? 1 : 0, out);
+        break;
+    default:
+        throw Error("attention: head width must be 64 or 128");
+    }
+    check_hip(hipGetLastError(), "attention step launch");
+}
+
+void layer_norm_add(const uint16_t* x, std::size_t rows, std::size_t width, const uint16_t* gain,
+                    const uint16_t* bias, const uint16_t* add_row, uint16_t* out, hipStream_t stream)
+{
+    if (!rows)
+    {
+        return;
+    }
+    const unsigned grid = unsigned((rows + 3) / 4);
+    switch (width)
+    {
+    case 256:
+        layer_norm_add_kernel<4><<<grid, 256, 0, stream>>>(x, int(rows), gain, bias, add_row, out);
+        break;
+    case 512:
+        layer_norm_add_kernel<8><<<grid, 256, 0, stream>>>(x, int(rows), gain, bias, add_row, out);
+        break;
+    case 1024:
+        layer_norm_add_kernel<16><<<grid, 256, 0, stream>>>(x, int(rows), gain, bias, add_row, out);
+        break;
+    case 2048:
+        layer_norm_add_kernel<32><<<grid, 256, 0, stream>>>(x, int(rows), gain, bias, add_row, out);
+        break;
+    default:
+        throw Error("layer norm: width must be one of 256, 512, 1024, 2048");
+    }
+    check_hip(hipGetLastError(), "layer norm launch");
+}
+
+void sample_step(const Sample& a, hipStream_t stream)
+{
+    require(a.lanes > 0 && a.current && a.tokens && a.row_base && a.error, "sample: arguments");
+    require(a.known || a.state, "sample: needs known tokens or a decoder");
+    sample_kernel<<<1, sample_waves * wave, 0, stream>>>(a);
+    check_hip(hipGetLastError(), "sample launch");
+}
+
+void gather_frame(const uint16_t* tokens, const int* row_base, int frame, int step_stride, int books,
+                  int lanes, uint16_t* dst, hipStream_t stream)
+{
+    if (lanes <= 0)
+    {
+        return;
+    }
+    const int n = lanes * books;
+    gather_frame_kernel<<<(n + 255) / 256, 256, 0, stream>>>(tokens, row_base, frame, step_stride, books,
+                                                             lanes, dst);
+    check_hip(hipGetLastError(), "gather launch");
+}
+
+void advance(int* counter, int amount, hipStream_t stream)
+{
+    advance_kernel<<<1, 1, 0, stream>>>(counter, amount);
+    check_hip(hipGetLastError(), "advance launch");
+}
+} // namespace tsac_hip

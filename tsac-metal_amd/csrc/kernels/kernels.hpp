@@ -55,11 +55,17 @@ void quantize_rows(const uint16_t* x, std::size_t rows, std::size_t K, Prologue 
 // ---- quantised linear (src/scalar/packed_linear.cpp:8-30) ---------------------
 struct DeviceLinear
 {
-    const int8_t* values = nullptr; // [N][K] canonical
+    const int8_t* values = nullptr; // row tiles, see tile_weights
     const float* scales = nullptr;  // [K/256][N]
     const float* bias = nullptr;    // [N]
     std::size_t K = 0, N = 0;
 };
+
+// One-time host re-layout of canonical int8 weights [N][K] (input fastest) into
+// row tiles: tile (t, b) holds rows 64t..64t+63 of block b as
+// [segment 0..15][row 0..63][16 bytes], tiles ordered [N/64][K/256]. Requires
+// K % 256 == 0 and N % 64 == 0. `tiled` holds K*N bytes.
+void tile_weights(const int8_t* canonical, std::size_t K, std::size_t N, int8_t* tiled);
 
 enum class LinearPath
 {

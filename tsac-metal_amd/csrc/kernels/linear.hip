@@ -7,20 +7,30 @@
 // block dots and then run that same chain, so GEMV and GEMM agree bit for bit
 // with each other and with the reference.
 //
-//  * GEMV (decode, M <= 8 columns): one wavefront streams a group of weight rows
-//    as contiguous 1 KiB loads, v_dot4 against activations staged in LDS, exact
-//    16-lane integer reductions, then the ordered chain.
-//  * GEMM (encode, large M): 128x128 tiles per 256-thread workgroup, int8 MFMA
-//    32x32x32 into int32 accumulators per 256-wide K block, LDS-staged operand
-//    tiles, and the per-block fp32 fma epilogue into a second accumulator set.
+// Weights live in HBM in "row tiles", laid out once at load time: 64 output rows
+// x one 256-value block form a 16 KiB tile stored as [segment 0..15][row 0..63]
+// [16 bytes], tiles ordered [N/64][K/256]. A wavefront load of one segment is
+// then 1 KiB contiguous with lane l holding row l.
+//
+//  * GEMV (decode, M <= 8 columns): one workgroup per 64-row tile, one
+//    wavefront per block; every lane accumulates its row's whole block dot with
+//    v_dot4 against wave-uniform activations (no cross-lane reduction), then the
+//    ordered chain runs per (row, column) from LDS.
+//  * GEMM (encode, large M): 128x128 output tiles per 256-thread workgroup,
+//    int8 MFMA 32x32x32 into int32 accumulators per 256-wide K block, LDS-staged
+//    operand tiles, and the per-block fp32 fma epilogue into a second
+//    accumulator set.
 #include "device_numeric.hpp"
 #include "kernels.hpp"
+
+#include <cstring>
 
 namespace tsac_hip
 {
 namespace
 {
-// ------------------------------------------------------------------ epilogue
+constexpr int tile_rows = 64;
+constexpr int segments = 16; // 16-byte segments per 256-value block
 
 __device__ __forceinline__ uint16_t finish(float sum, float bias, const uint16_t* residual,
                                            std::size_t index)
@@ -33,126 +43,82 @@ __device__ __forceinline__ uint16_t finish(float sum, float bias, const uint16_t
     return y;
 }
 
+// Byte offset of segment `s` of block `b` in row tile `t` (row 0 of the tile).
+__device__ __forceinline__ std::size_t tile_offset(int t, int b, int s, int blocks)
+{
+    return ((std::size_t(t) * blocks + b) * segments + s) * (tile_rows * 16);
+}
+
 // ------------------------------------------------------------------ GEMV
 
 constexpr int gemv_waves = 4;
-constexpr int gemv_unroll = 4;
 constexpr int gemv_max_columns = 8;
 
-__device__ __forceinline__ int dot16(uint4 w, uint4 a, int acc)
-{
-    acc = __builtin_amdgcn_sdot4(int(w.x), int(a.x), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.y), int(a.y), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.z), int(a.z), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.w), int(a.w), acc, false);
-    return acc;
-}
-
-// K: input width. G = rows per wave group (1 KiB of weights for K <= 1024).
-// J = 16-byte segments per lane per group. M = activation columns.
-template <int K, int M>
+template <int M>
 __global__ __launch_bounds__(gemv_waves * wave) void gemv_kernel(
     const int8_t* __restrict__ weights, const float* __restrict__ weight_scales,
-    const float* __restrict__ bias, int N, const int8_t* __restrict__ q,
+    const float* __restrict__ bias, int N, int K, const int8_t* __restrict__ q,
     const float* __restrict__ activation_scales, uint16_t* y, const uint16_t* residual)
 {
-    constexpr int G = K >= 1024 ? 1 : 1024 / K;
-    constexpr int J = G * K / 1024;
-    constexpr int blocks = K / 256;
-    constexpr int segments_per_row = K / 16;
-    __shared__ uint4 staged[M * K / 16];
-    for (int i = threadIdx.x; i < M * K / 16; i += blockDim.x)
+    extern __shared__ int block_dots[]; // [blocks][M][64]
+    const int blocks = K / 256;
+    const int tile = blockIdx.x;
+    const int lane = threadIdx.x % wave;
+    const int warp = __builtin_amdgcn_readfirstlane(threadIdx.x / wave);
+    for (int b = warp; b < blocks; b += gemv_waves)
     {
-        staged[i] = reinterpret_cast<const uint4*>(q)[i];
+        uint4 w[segments];
+        const int8_t* base = weights + tile_offset(tile, b, 0, blocks) + lane * 16;
+#pragma unroll
+        for (int s = 0; s < segments; ++s)
+        {
+            w[s] = *reinterpret_cast<const uint4*>(base + s * tile_rows * 16);
+        }
+        int dot[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+        {
+            dot[m] = 0;
+            const uint4* a = reinterpret_cast<const uint4*>(q + std::size_t(m) * K + b * 256);
+#pragma unroll
+            for (int s = 0; s < segments; ++s)
+            {
+                const uint4 x = a[s];
+                dot[m] = __builtin_amdgcn_sdot4(int(w[s].x), int(x.x), dot[m], false);
+                dot[m] = __builtin_amdgcn_sdot4(int(w[s].y), int(x.y), dot[m], false);
+                dot[m] = __builtin_amdgcn_sdot4(int(w[s].z), int(x.z), dot[m], false);
+                dot[m] = __builtin_amdgcn_sdot4(int(w[s].w), int(x.w), dot[m], false);
+            }
+            block_dots[(b * M + m) * tile_rows + lane] = dot[m];
+        }
     }
     __syncthreads();
-
-    const int lane = threadIdx.x % wave;
-    const int groups = N / G;
-    const int total_waves = gridDim.x * gemv_waves;
-    for (int first = blockIdx.x * gemv_waves + threadIdx.x / wave; first < groups;
-         first += total_waves * gemv_unroll)
+    // Ordered chain per (row, column): ascending blocks, one fma each.
+    for (int pair = threadIdx.x; pair < M * tile_rows; pair += blockDim.x)
     {
-        // Issue every weight load of this iteration before any arithmetic.
-        uint4 w[gemv_unroll][J];
-#pragma unroll
-        for (int u = 0; u < gemv_unroll; ++u)
+        const int m = pair / tile_rows, row = pair % tile_rows;
+        const int n = tile * tile_rows + row;
+        float sum = 0.0f;
+        for (int b = 0; b < blocks; ++b)
         {
-            const int group = first + u * total_waves;
-            const int g = group < groups ? group : groups - 1;
-#pragma unroll
-            for (int j = 0; j < J; ++j)
-            {
-                w[u][j] = reinterpret_cast<const uint4*>(weights + std::size_t(g) * G * K +
-                                                         j * 1024)[lane];
-            }
+            const float scale = weight_scales[std::size_t(b) * N + n] * activation_scales[m * blocks + b];
+            sum = __builtin_fmaf(float(block_dots[(b * M + m) * tile_rows + row]), scale, sum);
         }
-#pragma unroll
-        for (int u = 0; u < gemv_unroll; ++u)
-        {
-            const int group = first + u * total_waves;
-            if (group >= groups)
-            {
-                break;
-            }
-            int dots[J][M];
-#pragma unroll
-            for (int j = 0; j < J; ++j)
-            {
-                const int segment = j * wave + lane;
-                const int k16 = segment % segments_per_row;
-#pragma unroll
-                for (int m = 0; m < M; ++m)
-                {
-                    dots[j][m] = group_isum<16>(dot16(w[u][j], staged[m * segments_per_row + k16], 0));
-                }
-            }
-            // Ordered per-block chain; every lane computes it, lane r*M+m stores.
-            uint16_t out = 0;
-#pragma unroll
-            for (int r = 0; r < G; ++r)
-            {
-                const int n = group * G + r;
-#pragma unroll
-                for (int m = 0; m < M; ++m)
-                {
-                    float sum = 0.0f;
-#pragma unroll
-                    for (int b = 0; b < blocks; ++b)
-                    {
-                        const int segment = r * segments_per_row + 16 * b;
-                        const int dot = __shfl(dots[segment / wave][m], segment % wave, wave);
-                        const float scale = weight_scales[b * N + n] * activation_scales[m * blocks + b];
-                        sum = __builtin_fmaf(float(dot), scale, sum);
-                    }
-                    if (lane == r * M + m)
-                    {
-                        out = finish(sum, bias[n], residual, std::size_t(m) * N + n);
-                    }
-                }
-            }
-            if (lane < G * M)
-            {
-                const int r = lane / M, m = lane % M;
-                y[std::size_t(m) * N + group * G + r] = out;
-            }
-        }
+        const std::size_t index = std::size_t(m) * N + n;
+        y[index] = finish(sum, bias[n], residual, index);
     }
 }
 
-template <int K>
-void launch_gemv_k(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M,
-                   uint16_t* y, const uint16_t* residual, hipStream_t stream)
+void launch_gemv(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M,
+                 uint16_t* y, const uint16_t* residual, hipStream_t stream)
 {
-    constexpr int G = K >= 1024 ? 1 : 1024 / K;
-    const std::size_t groups = w.N / G;
-    const std::size_t wanted = (groups + gemv_waves - 1) / gemv_waves;
-    const unsigned grid = unsigned(wanted < 2048 ? wanted : 2048);
-    const int N = int(w.N);
+    const unsigned grid = unsigned(w.N / tile_rows);
+    const std::size_t lds = (w.K / 256) * M * tile_rows * sizeof(int);
+    const int N = int(w.N), K = int(w.K);
 #define TSAC_GEMV(MM)                                                                              \
     case MM:                                                                                       \
-        gemv_kernel<K, MM><<<grid, gemv_waves * wave, 0, stream>>>(w.values, w.scales, w.bias, N,  \
-                                                                   q, scales, y, residual);       \
+        gemv_kernel<MM><<<grid, gemv_waves * wave, lds, stream>>>(w.values, w.scales, w.bias, N, K, \
+                                                                  q, scales, y, residual);        \
         break;
     switch (M)
     {
@@ -168,31 +134,6 @@ void launch_gemv_k(const DeviceLinear& w, const int8_t* q, const float* scales, 
         throw Error("gemv: column count out of range");
     }
 #undef TSAC_GEMV
-}
-
-void launch_gemv(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M,
-                 uint16_t* y, const uint16_t* residual, hipStream_t stream)
-{
-    switch (w.K)
-    {
-    case 256:
-        launch_gemv_k<256>(w, q, scales, M, y, residual, stream);
-        break;
-    case 512:
-        launch_gemv_k<512>(w, q, scales, M, y, residual, stream);
-        break;
-    case 1024:
-        launch_gemv_k<1024>(w, q, scales, M, y, residual, stream);
-        break;
-    case 2048:
-        launch_gemv_k<2048>(w, q, scales, M, y, residual, stream);
-        break;
-    case 4096:
-        launch_gemv_k<4096>(w, q, scales, M, y, residual, stream);
-        break;
-    default:
-        throw Error("gemv: K must be one of 256, 512, 1024, 2048, 4096");
-    }
 }
 
 // ------------------------------------------------------------------ GEMM (MFMA)
@@ -216,6 +157,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     const int wm = warp / 2, wn = warp % 2;
     const int n0 = blockIdx.x * tile_n, m0 = blockIdx.y * tile_m;
     const int blocks = K / 256;
+    const int row_tiles = N / tile_rows;
 
     v16i acc[2][2];
     float sum[2][2][16];
@@ -234,6 +176,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 
     for (int k0 = 0; k0 < K; k0 += stage_k)
     {
+        const int block = k0 / 256, first_segment = (k0 % 256) / 16;
         // Global -> registers: 128 rows x 128 bytes per operand, 4 x 16 B per thread.
         uint4 ra[4], rb[4];
 #pragma unroll
@@ -243,12 +186,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             const int m = m0 + row;
             ra[it] = m < M ? *reinterpret_cast<const uint4*>(q + std::size_t(m) * K + k0 + chunk * 16)
                            : make_uint4(0, 0, 0, 0);
-            const int n = n0 + row;
-            rb[it] = n < N ? *reinterpret_cast<const uint4*>(weights + std::size_t(n) * K + k0 +
-                                                            chunk * 16)
-                           : make_uint4(0, 0, 0, 0);
+            // Weights: 2 row tiles x 8 segments, each a contiguous 1 KiB.
+            const int c = index / 64, t = n0 / tile_rows + c / 8;
+            rb[it] = t < row_tiles
+                         ? *reinterpret_cast<const uint4*>(
+                               weights + tile_offset(t, block, first_segment + c % 8, blocks) + (index % 64) * 16)
+                         : make_uint4(0, 0, 0, 0);
         }
-        const int block = k0 / 256;
         const bool block_start = k0 % 256 == 0;
         float scale_value = 0.0f;
         if (block_start)
@@ -270,7 +214,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(
         {
             const int index = it * 256 + tid, row = index / 8, chunk = index % 8;
             *reinterpret_cast<uint4*>(a_tile + row * lds_stride + chunk * 16) = ra[it];
-            *reinterpret_cast<uint4*>(b_tile + row * lds_stride + chunk * 16) = rb[it];
+            const int c = index / 64;
+            *reinterpret_cast<uint4*>(b_tile + ((c / 8) * tile_rows + index % 64) * lds_stride + (c % 8) * 16) =
+                rb[it];
         }
         if (block_start)
         {
@@ -364,11 +310,30 @@ std::size_t gemv_max_rows()
     return gemv_max_columns;
 }
 
+void tile_weights(const int8_t* canonical, std::size_t K, std::size_t N, int8_t* tiled)
+{
+    require(K % 256 == 0 && N % tile_rows == 0, "weights: K must be a multiple of 256, N of 64");
+    const std::size_t blocks = K / 256;
+    for (std::size_t n = 0; n < N; ++n)
+    {
+        const std::size_t t = n / tile_rows, lane = n % tile_rows;
+        for (std::size_t b = 0; b < blocks; ++b)
+        {
+            for (std::size_t s = 0; s < segments; ++s)
+            {
+                std::memcpy(tiled + ((t * blocks + b) * segments + s) * tile_rows * 16 + lane * 16,
+                            canonical + n * K + b * 256 + s * 16, 16);
+            }
+        }
+    }
+}
+
 void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M,
             uint16_t* y, const uint16_t* residual, LinearPath path, hipStream_t stream)
 {
     require(w.K >= 256 && w.K % 256 == 0 && w.K <= 4096, "linear: K must be a multiple of 256 <= 4096");
-    require(w.N > 0 && w.N % 16 == 0 && w.N < (std::size_t(1) << 30), "linear: N must be a multiple of 16");
+    require(w.N > 0 && w.N % tile_rows == 0 && w.N < (std::size_t(1) << 30),
+            "linear: N must be a multiple of 64");
     if (M == 0)
     {
         return;
@@ -380,8 +345,6 @@ void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::si
     if (path == LinearPath::gemv)
     {
         require(M <= gemv_max_columns, "gemv: at most 8 columns");
-        const std::size_t G = w.K >= 1024 ? 1 : 1024 / w.K;
-        require(w.N % G == 0, "gemv: N must be a multiple of the row group");
         launch_gemv(w, q, scales, M, y, residual, stream);
     }
     else

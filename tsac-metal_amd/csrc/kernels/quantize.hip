@@ -23,7 +23,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restric
                                                        uint16_t* __restrict__ normalized,
                                                        uint32_t* __restrict__ error)
 {
-    constexpr int K = 64 * V, lanes_per_block = 256 / V;
+    constexpr int K = 64 * V;
     const int lane = threadIdx.x % wave;
     const int row = blockIdx.x * rows_per_block + threadIdx.x / wave;
     if (row >= rows)
@@ -48,52 +48,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restric
             v[i] = gelu_bf16(v[i]);
         }
     }
-    // src/scalar/probability.cpp:20-38
-    float values[V];
-    float maximum = 0.0f;
-    bool finite = true;
-#pragma unroll
-    for (int i = 0; i < V; ++i)
-    {
-        values[i] = bf16_to_float(v[i]);
-        finite = finite && is_finite(values[i]);
-        const float a = __builtin_fabsf(flush(values[i]));
-        maximum = maximum < a ? a : maximum;
-    }
-    if (!finite)
-    {
-        error[0] = error_nonfinite;
-    }
-    maximum = group_max<lanes_per_block>(maximum);
-    float s = ftz_divide(maximum, 127.0f);
-    s = s < 1e-35f ? 1e-35f : s;
-    const uint16_t scale = float_to_bf16(s);
-    const float reciprocal = ftz_divide(1.0f, bf16_to_float(scale));
-    int8_t out[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i)
-    {
-        float r = __builtin_rintf(ftz_multiply(values[i], reciprocal));
-        r = r < -128.0f ? -128.0f : (127.0f < r ? 127.0f : r);
-        out[i] = int8_t(r);
-    }
-    int8_t* qrow = q + size_t(row) * K + lane * V;
-    if constexpr (V == 4)
-    {
-        *reinterpret_cast<uint32_t*>(qrow) = *reinterpret_cast<const uint32_t*>(out);
-    }
-    else
-    {
-#pragma unroll
-        for (int c = 0; c < V / 8; ++c)
-        {
-            reinterpret_cast<uint2*>(qrow)[c] = reinterpret_cast<const uint2*>(out)[c];
-        }
-    }
-    if (lane % lanes_per_block == 0)
-    {
-        scales[size_t(row) * (K / 256) + lane / lanes_per_block] = bf16_to_float(scale);
-    }
+    bf8l_lane<V>(v, lane, q + size_t(row) * K, scales + size_t(row) * (K / 256), error);
 }
 
 template <int V>

@@ -79,6 +79,66 @@ template <int V> __device__ __forceinline__ float row_sum(float (&v)[V])
     return ftz_add(0.0f, tree_sum<wave>(register_tree(v)));
 }
 
+// BF8L quantisation of one row held V-per-lane (src/scalar/probability.cpp:20-38):
+// q_row/s_row are the row's int8 values and block scales (fp32, widened BF16).
+// Sets error[0] when a value is not finite.
+template <int V>
+__device__ __forceinline__ void bf8l_lane(const uint16_t (&v)[V], int lane, int8_t* q_row,
+                                          float* s_row, uint32_t* error)
+{
+    constexpr int lanes_per_block = 256 / V;
+    float values[V];
+    float maximum = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+    {
+        values[i] = bf16_to_float(v[i]);
+        finite = finite && is_finite(values[i]);
+        const float a = __builtin_fabsf(flush(values[i]));
+        maximum = maximum < a ? a : maximum;
+    }
+    if (!finite)
+    {
+        error[0] = 1u;
+    }
+    maximum = group_max<lanes_per_block>(maximum);
+    float s = ftz_divide(maximum, 127.0f);
+    s = s < 1e-35f ? 1e-35f : s;
+    const uint16_t scale = float_to_bf16(s);
+    const float reciprocal = ftz_divide(1.0f, bf16_to_float(scale));
+    uint32_t packed[(V + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (V + 3) / 4; ++i)
+    {
+        packed[i] = 0;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+    {
+        float r = __builtin_rintf(ftz_multiply(values[i], reciprocal));
+        r = r < -128.0f ? -128.0f : (127.0f < r ? 127.0f : r);
+        packed[i / 4] |= (uint32_t(int(r)) & 0xffu) << (8 * (i % 4));
+    }
+    int8_t* q = q_row + lane * V;
+    if constexpr (V == 4)
+    {
+        *reinterpret_cast<uint32_t*>(q) = packed[0];
+    }
+    else
+    {
+#pragma unroll
+        for (int c = 0; c < V / 8; ++c)
+        {
+            *reinterpret_cast<uint2*>(q + 8 * c) = make_uint2(packed[2 * c], packed[2 * c + 1]);
+        }
+    }
+    if (lane % lanes_per_block == 0)
+    {
+        s_row[lane / lanes_per_block] = bf16_to_float(scale);
+    }
+}
+
 // LayerNorm of one row (src/common/probability.cpp:138-169), in place.
 template <int V>
 __device__ __forceinline__ void layer_norm_lane(uint16_t (&v)[V], const uint16_t* gain,
