@@ -86,9 +86,22 @@ def gemv_roofline(torch, native, launches):
     achieved = traffic / seconds / 1e9
     del linears
     torch.cuda.empty_cache()
-    return {"kernel": "gemv_kernel<1024,3>", "bound": "hbm", "achieved": round(achieved, 1),
+    # Calibration for hardware byte counters: a plain 256 MiB device copy.
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    # HBM bytes per launch from the two calibrated PMC runs of this same command
+    # (FETCH_SIZE, WRITE_SIZE), recorded in profiles/.
+    measured = None
+    record = ROOT / "profiles" / "gemv_rotating_1GiB_K1024_M3.traffic.txt"
+    if record.exists():
+        fields = dict(line.split("=", 1) for line in record.read_text().split() if "=" in line)
+        measured = int(float(fields["bytes_per_launch"]))
+    return {"kernel": "gemv_kernel<3>", "bound": "hbm", "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None, "bytes_per_launch": traffic, "avg_launch_us": round(seconds * 1e6, 2),
+            "traffic": measured, "bytes_per_launch": traffic, "avg_launch_us": round(seconds * 1e6, 2),
             "shape": {"K": K, "N": rows, "M": M, "distinct_weight_bytes": mats * rows * K}}
 
 

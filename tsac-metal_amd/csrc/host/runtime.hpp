@@ -205,8 +205,10 @@ private:
     // distributions) in token order.
     void stepwise(const Header& h, const uint16_t* known, const uint8_t* payload,
                   std::size_t payload_bytes, uint16_t* tokens_out, uint16_t* distributions);
+    // position: host value, or read from device_position when that is non-null.
     void layer_step(bool temporal, std::size_t layer, uint16_t* x, std::size_t rows,
-                    std::size_t first_lane, std::size_t position, bool replay, std::size_t extent);
+                    std::size_t first_lane, std::size_t position, const int* device_position,
+                    bool replay, std::size_t extent);
 
     std::shared_ptr<const Model> model_;
     hipStream_t stream_ = nullptr;

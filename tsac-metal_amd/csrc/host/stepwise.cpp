@@ -2,6 +2,9 @@
 // the columns of each projection (src/common/transformer.cpp:137-244 schedule).
 // Every kernel of the pass is enqueued up front on the session's stream; the
 // range decoder runs on the GPU, so nothing returns to the host until the end.
+// Ordinary frame steps (every lane active, no context rollover) replay one
+// captured HIP graph whose kernels read the context position and step index
+// from device counters.
 #include "../kernels/decode.hpp"
 #include "runtime.hpp"
 
@@ -13,20 +16,41 @@ namespace tsac_hip
 namespace
 {
 constexpr std::size_t replay_frames = 256;
-}
+// Projections batch up to `chunk` lanes as their columns; larger lane sets run
+// chunk by chunk, which keeps each (step, book)'s lanes in stream order.
+constexpr std::size_t chunk = 8;
+
+struct Graph
+{
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    ~Graph()
+    {
+        if (exec)
+        {
+            (void)hipGraphExecDestroy(exec);
+        }
+        if (graph)
+        {
+            (void)hipGraphDestroy(graph);
+        }
+    }
+};
+} // namespace
 
 // One decode-shaped layer (src/common/cpu_transformer.tpp:139-173) over lanes
-// first_lane .. first_lane + rows - 1 at cache position `position`: five launches.
+// first_lane .. first_lane + rows - 1: five launches.
 void Session::layer_step(bool temporal, std::size_t layer, uint16_t* x, std::size_t rows,
-                         std::size_t first_lane, std::size_t position, bool replay, std::size_t extent)
+                         std::size_t first_lane, std::size_t position, const int* device_position,
+                         bool replay, std::size_t extent)
 {
     const Geometry& g = model_->geometry();
     const Model& m = *model_;
     const std::size_t w = g.width;
     const std::size_t layers = temporal ? g.temporal_layers : g.codebook_layers;
-    auto* query = arena_.get<uint16_t>("s.query", rows * w);
-    auto* att = arena_.get<uint16_t>("s.att", rows * w);
-    auto* hidden = arena_.get<uint16_t>("s.hidden", rows * g.ffn);
+    auto* query = arena_.get<uint16_t>("s.query", chunk * w);
+    auto* att = arena_.get<uint16_t>("s.att", chunk * w);
+    auto* hidden = arena_.get<uint16_t>("s.hidden", chunk * g.ffn);
     auto* keys = arena_.get<uint16_t>(temporal ? "s.tk" : "s.ck", 0);
     auto* values = arena_.get<uint16_t>(temporal ? "s.tv" : "s.cv", 0);
     auto* err = errors_.as<uint32_t>();
@@ -52,11 +76,12 @@ void Session::layer_step(bool temporal, std::size_t layer, uint16_t* x, std::siz
     qkv.width = int(w);
     qkv.head_width = int(g.head_width);
     qkv.rotations = temporal ? m.rotations() : nullptr;
+    qkv.position = device_position;
     qkv.fixed_position = int(position);
     fused_linear(qkv, stream_);
 
     attention_step(query, layer_keys, layer_values, lane_stride, rows, w, g.heads, g.head_width,
-                   g.attention_scale, nullptr, int(position), extent, replay, att, stream_);
+                   g.attention_scale, device_position, int(position), extent, replay, att, stream_);
 
     FusedLinear out;
     out.w = m.layer(temporal, layer, 1);
@@ -119,6 +144,9 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
     arena_.get<uint16_t>("s.tv", independent * g.temporal_layers * extent * w);
     arena_.get<uint16_t>("s.ck", independent * g.codebook_layers * C * w);
     arena_.get<uint16_t>("s.cv", independent * g.codebook_layers * C * w);
+    arena_.get<uint16_t>("s.query", chunk * w);
+    arena_.get<uint16_t>("s.att", chunk * w);
+    arena_.get<uint16_t>("s.hidden", chunk * g.ffn);
     auto* current = arena_.get<uint16_t>("s.current", independent * C);
     auto* feedback = arena_.get<uint16_t>("s.feedback", independent * C);
     auto* tokens = arena_.get<uint16_t>("s.tokens", symbols);
@@ -129,6 +157,7 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
     auto* y = arena_.get<uint16_t>("s.y", independent * w);
     auto* logits = arena_.get<uint16_t>("s.logits", independent * g.alphabet);
     auto* row_base = arena_.get<int>("s.row_base", independent);
+    auto* counters = arena_.get<int>("s.counters", 2);
     auto* state = arena_.get<DecoderState>("s.state", 1);
     uint16_t* d_known = nullptr;
     uint16_t* d_distributions = nullptr;
@@ -174,11 +203,9 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
     // Host data above must reach the device before the host buffers go away.
     check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
 
-    // Projections batch up to `chunk` lanes as their columns; larger lane sets
-    // run chunk by chunk, which keeps each (step, book)'s lanes in stream order.
-    constexpr std::size_t chunk = 8;
+    // Temporal stack for lanes [first, first + count) fed by `fed` token rows.
     const auto temporal_step = [&](std::size_t first, std::size_t count, std::size_t position,
-                                   bool replay, const uint16_t* fed)
+                                   const int* device_position, bool replay, const uint16_t* fed)
     {
         FusedLinear project;
         project.w = m.temporal_projection();
@@ -196,39 +223,13 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
         fused_linear(project, stream_);
         for (std::size_t l = 0; l < g.temporal_layers; ++l)
         {
-            layer_step(true, l, x + first * w, count, first, position, replay, extent);
+            layer_step(true, l, x + first * w, count, first, position, device_position, replay, extent);
         }
     };
 
-    std::size_t context_used = 0;
-    for (std::size_t step = 0; step < lanes.steps(); ++step)
+    // Conditioning + every codebook of one frame step for `active` lanes.
+    const auto codebooks = [&](std::size_t active, std::size_t step, const int* device_step)
     {
-        const std::size_t active = step < lanes.base ? independent : lanes.extra * G;
-        if (context_used == g.context)
-        {
-            // Context rollover: reset and replay the last 256 complete frames
-            // (src/common/transformer.cpp:187-203).
-            context_used = 0;
-            for (std::size_t k = 0; k < replay_frames; ++k)
-            {
-                gather_frame(tokens, row_base, int(step - replay_frames + k), int(G * C), int(C), int(active),
-                             feedback, stream_);
-                for (std::size_t first = 0; first < active; first += chunk)
-                {
-                    temporal_step(first, std::min(chunk, active - first), context_used, true, feedback);
-                }
-                ++context_used;
-            }
-        }
-        else
-        {
-            // Feedback = the previous complete frame (all-zero indices first).
-            for (std::size_t first = 0; first < active; first += chunk)
-            {
-                temporal_step(first, std::min(chunk, active - first), context_used, false, current);
-            }
-            ++context_used;
-        }
         layer_norm_add(x, active, w, m.norm_gain(m.final_norm_index(true)),
                        m.norm_bias(m.final_norm_index(true)), m.positions(), book0, stream_);
         uint16_t* prefix_in = nullptr;
@@ -264,7 +265,7 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
                 }
                 for (std::size_t l = 0; l < g.codebook_layers; ++l)
                 {
-                    layer_step(false, l, input, count, first, book, false, C);
+                    layer_step(false, l, input, count, first, book, nullptr, false, C);
                 }
                 FusedLinear head;
                 head.w = m.output_projection();
@@ -288,6 +289,7 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
                 sample.current = current + first * C;
                 sample.tokens = tokens;
                 sample.row_base = row_base + first;
+                sample.step = device_step;
                 sample.fixed_step = int(step);
                 sample.step_stride = int(G * C);
                 sample.known = d_known;
@@ -303,6 +305,80 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
                 prefix_in = prefix_out;
                 prefix_out = prefix_out == prefix_a ? prefix_b : prefix_a;
             }
+        }
+    };
+
+    // An ordinary step: feedback = the previous complete frame (all-zero
+    // indices first), context position from counters[0], step from counters[1].
+    const auto ordinary_step = [&](std::size_t active, std::size_t position, std::size_t step,
+                                   bool device)
+    {
+        for (std::size_t first = 0; first < active; first += chunk)
+        {
+            temporal_step(first, std::min(chunk, active - first), position, device ? counters : nullptr,
+                          false, current);
+        }
+        codebooks(active, step, device ? counters + 1 : nullptr);
+    };
+
+    Graph graph;
+    std::size_t context_used = 0;
+    for (std::size_t step = 0; step < lanes.steps(); ++step)
+    {
+        const std::size_t active = step < lanes.base ? independent : lanes.extra * G;
+        if (context_used == g.context)
+        {
+            // Context rollover: reset and replay the last 256 complete frames
+            // (src/common/transformer.cpp:187-203).
+            context_used = 0;
+            for (std::size_t k = 0; k < replay_frames; ++k)
+            {
+                gather_frame(tokens, row_base, int(step - replay_frames + k), int(G * C), int(C), int(active),
+                             feedback, stream_);
+                for (std::size_t first = 0; first < active; first += chunk)
+                {
+                    temporal_step(first, std::min(chunk, active - first), context_used, nullptr, true, feedback);
+                }
+                ++context_used;
+            }
+            codebooks(active, step, nullptr);
+        }
+        else if (active == independent && step > 0)
+        {
+            if (!graph.exec)
+            {
+                set_counters(counters, int(context_used), int(step), stream_);
+                check_hip(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+                try
+                {
+                    ordinary_step(active, 0, 0, true);
+                    advance_counters(counters, stream_);
+                }
+                catch (...)
+                {
+                    hipGraph_t broken = nullptr;
+                    (void)hipStreamEndCapture(stream_, &broken);
+                    if (broken)
+                    {
+                        (void)hipGraphDestroy(broken);
+                    }
+                    throw;
+                }
+                check_hip(hipStreamEndCapture(stream_, &graph.graph), "end capture");
+                check_hip(hipGraphInstantiate(&graph.exec, graph.graph, nullptr, nullptr, 0),
+                          "instantiate graph");
+            }
+            else
+            {
+                set_counters(counters, int(context_used), int(step), stream_);
+            }
+            check_hip(hipGraphLaunch(graph.exec, stream_), "launch graph");
+            ++context_used;
+        }
+        else
+        {
+            ordinary_step(active, context_used, step, false);
+            ++context_used;
         }
     }
     if (tokens_out)

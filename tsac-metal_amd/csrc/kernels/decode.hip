@@ -6,6 +6,10 @@
 // (src/common/probability.cpp:96-122) and categorical bisection
 // (src/format/categorical.cpp:119-142) with the range decoder
 // (src/format/range.cpp:131-151).
+//
+// These launches are latency-bound (a few lanes per step), so every kernel
+// issues its independent global loads first and overlaps them with its
+// prologue arithmetic.
 #include "decode.hpp"
 #include "row_ops.hpp"
 
@@ -87,37 +91,80 @@ __device__ __forceinline__ void input_row(const FusedLinear& a, int m, int lane,
     bf8l_lane<V>(v, lane, q_row, s_row, a.error);
 }
 
+constexpr int fused_waves = 8;
+
+// One workgroup per 64-row weight tile. Waves split the tile's K/16 segments
+// (blocks x 16) evenly; exact int32 partial dots meet in LDS and the ordered
+// fma chain runs per (row pair, column).
 template <int V, Input I>
-__global__ __launch_bounds__(256) void fused_linear_kernel(const FusedLinear a)
+__global__ __launch_bounds__(fused_waves * wave) void fused_linear_kernel(const FusedLinear a)
 {
     constexpr int K = wave * V, blocks = K / 256;
+    constexpr int waves_per_block = blocks >= fused_waves ? 1 : fused_waves / blocks;
+    constexpr int wave_segments = segments / waves_per_block;
+    constexpr int rounds = blocks > fused_waves ? blocks / fused_waves : 1;
+    constexpr int slots = blocks * waves_per_block; // partial-dot slots per (column, row)
     __shared__ __attribute__((aligned(16))) int8_t q[max_columns * K];
     __shared__ float scales[max_columns * blocks];
-    __shared__ int dots[blocks * max_columns * tile_rows];
+    __shared__ int dots[slots * max_columns * tile_rows];
     const int lane = threadIdx.x % wave;
     const int warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
     const int tile = blockIdx.x;
     const int M = a.M, N = int(a.w.N);
-    for (int m = warp; m < M; m += 4)
+
+    // 1. Weight loads of the first round, issued before anything else.
+    const int first_block = rounds > 1 ? warp : warp / waves_per_block;
+    const int first_segment = rounds > 1 ? 0 : (warp % waves_per_block) * wave_segments;
+    uint4 w[wave_segments];
     {
-        input_row<V, I>(a, m, lane, q + m * K, scales + m * blocks, tile == 0);
-    }
-    __syncthreads();
-    for (int b = warp; b < blocks; b += 4)
-    {
-        uint4 w[segments];
-        const int8_t* base = a.w.values + tile_offset(tile, b, 0, blocks) + lane * 16;
+        const int8_t* base = a.w.values + tile_offset(tile, first_block, first_segment, blocks) + lane * 16;
 #pragma unroll
-        for (int s = 0; s < segments; ++s)
+        for (int s = 0; s < wave_segments; ++s)
         {
             w[s] = *reinterpret_cast<const uint4*>(base + s * tile_rows * 16);
         }
+    }
+    // Chain constants for this thread's (row pair, column).
+    const int pair = threadIdx.x % 32, column = threadIdx.x / 32;
+    const int n0 = tile * tile_rows + 2 * pair;
+    const float bias0 = a.w.bias[n0], bias1 = a.w.bias[n0 + 1];
+    float ws0[blocks], ws1[blocks];
+#pragma unroll
+    for (int b = 0; b < blocks; ++b)
+    {
+        const float2 s = *reinterpret_cast<const float2*>(a.w.scales + std::size_t(b) * N + n0);
+        ws0[b] = s.x;
+        ws1[b] = s.y;
+    }
+
+    // 2. Inputs: one row per wave, quantised into LDS.
+    if (warp < M)
+    {
+        input_row<V, I>(a, warp, lane, q + warp * K, scales + warp * blocks, tile == 0);
+    }
+    __syncthreads();
+
+    // 3. Exact partial dots.
+#pragma unroll
+    for (int r = 0; r < rounds; ++r)
+    {
+        const int b = rounds > 1 ? warp + r * fused_waves : first_block;
+        if (r > 0)
+        {
+            const int8_t* base = a.w.values + tile_offset(tile, b, 0, blocks) + lane * 16;
+#pragma unroll
+            for (int s = 0; s < wave_segments; ++s)
+            {
+                w[s] = *reinterpret_cast<const uint4*>(base + s * tile_rows * 16);
+            }
+        }
+        const int slot = b * waves_per_block + (rounds > 1 ? 0 : warp % waves_per_block);
         for (int m = 0; m < M; ++m)
         {
-            const uint4* x = reinterpret_cast<const uint4*>(q + m * K + b * 256);
+            const uint4* x = reinterpret_cast<const uint4*>(q + m * K + b * 256 + first_segment * 16);
             int dot = 0;
 #pragma unroll
-            for (int s = 0; s < segments; ++s)
+            for (int s = 0; s < wave_segments; ++s)
             {
                 const uint4 u = x[s];
                 dot = __builtin_amdgcn_sdot4(int(w[s].x), int(u.x), dot, false);
@@ -125,28 +172,38 @@ __global__ __launch_bounds__(256) void fused_linear_kernel(const FusedLinear a)
                 dot = __builtin_amdgcn_sdot4(int(w[s].z), int(u.z), dot, false);
                 dot = __builtin_amdgcn_sdot4(int(w[s].w), int(u.w), dot, false);
             }
-            dots[(b * max_columns + m) * tile_rows + lane] = dot;
+            dots[(slot * max_columns + m) * tile_rows + lane] = dot;
         }
     }
     __syncthreads();
-    // Two adjacent rows per thread (rotary pairs), one column.
-    const int pair = threadIdx.x % 32, m = threadIdx.x / 32;
-    if (m >= M)
+
+    // 4. Ordered chain: ascending blocks, one fma each (the exact block dot is
+    //    the integer sum of its partial slots).
+    if (column >= M)
     {
         return;
     }
-    const int r0 = 2 * pair, n0 = tile * tile_rows + r0;
+    const int m = column;
     float sum0 = 0.0f, sum1 = 0.0f;
+#pragma unroll
     for (int b = 0; b < blocks; ++b)
     {
+        int d0 = 0, d1 = 0;
+#pragma unroll
+        for (int p = 0; p < waves_per_block; ++p)
+        {
+            const int* d = dots + ((b * waves_per_block + p) * max_columns + m) * tile_rows + 2 * pair;
+            d0 += d[0];
+            d1 += d[1];
+        }
         const float as = scales[m * blocks + b];
-        const float scale0 = a.w.scales[std::size_t(b) * N + n0] * as;
-        const float scale1 = a.w.scales[std::size_t(b) * N + n0 + 1] * as;
-        sum0 = __builtin_fmaf(float(dots[(b * max_columns + m) * tile_rows + r0]), scale0, sum0);
-        sum1 = __builtin_fmaf(float(dots[(b * max_columns + m) * tile_rows + r0 + 1]), scale1, sum1);
+        const float scale0 = ws0[b] * as;
+        const float scale1 = ws1[b] * as;
+        sum0 = __builtin_fmaf(float(d0), scale0, sum0);
+        sum1 = __builtin_fmaf(float(d1), scale1, sum1);
     }
-    uint16_t y0 = float_to_bf16(sum0 + a.w.bias[n0]);
-    uint16_t y1 = float_to_bf16(sum1 + a.w.bias[n0 + 1]);
+    uint16_t y0 = float_to_bf16(sum0 + bias0);
+    uint16_t y1 = float_to_bf16(sum1 + bias1);
     switch (a.output)
     {
     case Output::plain:
@@ -165,25 +222,25 @@ __global__ __launch_bounds__(256) void fused_linear_kernel(const FusedLinear a)
     case Output::qkv:
     {
         const int position = a.position ? *a.position : a.fixed_position;
-        const int w = a.width;
+        const int width = a.width;
         float re = bf16_to_float(y0), im = bf16_to_float(y1);
-        if (n0 < 2 * w && a.rotations)
+        if (n0 < 2 * width && a.rotations)
         {
             rotate(re, im, a.rotations + std::size_t(position) * a.head_width + n0 % a.head_width);
         }
         const uint32_t packed = float_to_bf16(re) | (uint32_t(float_to_bf16(im)) << 16);
         uint16_t* dst;
-        if (n0 < w)
+        if (n0 < width)
         {
-            dst = a.query + std::size_t(m) * w + n0;
+            dst = a.query + std::size_t(m) * width + n0;
         }
-        else if (n0 < 2 * w)
+        else if (n0 < 2 * width)
         {
-            dst = a.keys + std::size_t(m) * a.lane_stride + std::size_t(position) * w + (n0 - w);
+            dst = a.keys + std::size_t(m) * a.lane_stride + std::size_t(position) * width + (n0 - width);
         }
         else
         {
-            dst = a.values + std::size_t(m) * a.lane_stride + std::size_t(position) * w + (n0 - 2 * w);
+            dst = a.values + std::size_t(m) * a.lane_stride + std::size_t(position) * width + (n0 - 2 * width);
         }
         *reinterpret_cast<uint32_t*>(dst) = packed;
         return;
@@ -194,64 +251,104 @@ __global__ __launch_bounds__(256) void fused_linear_kernel(const FusedLinear a)
 
 template <int V> void launch_fused(const FusedLinear& a, hipStream_t stream)
 {
-    const dim3 grid(unsigned(a.w.N / tile_rows));
+    const dim3 grid(unsigned(a.w.N / tile_rows)), block(fused_waves * wave);
     switch (a.input)
     {
     case Input::bf16:
-        fused_linear_kernel<V, Input::bf16><<<grid, 256, 0, stream>>>(a);
+        fused_linear_kernel<V, Input::bf16><<<grid, block, 0, stream>>>(a);
         break;
     case Input::layer_norm:
-        fused_linear_kernel<V, Input::layer_norm><<<grid, 256, 0, stream>>>(a);
+        fused_linear_kernel<V, Input::layer_norm><<<grid, block, 0, stream>>>(a);
         break;
     case Input::embed_sum:
-        fused_linear_kernel<V, Input::embed_sum><<<grid, 256, 0, stream>>>(a);
+        fused_linear_kernel<V, Input::embed_sum><<<grid, block, 0, stream>>>(a);
         break;
     case Input::embed_accumulate:
-        fused_linear_kernel<V, Input::embed_accumulate><<<grid, 256, 0, stream>>>(a);
+        fused_linear_kernel<V, Input::embed_accumulate><<<grid, block, 0, stream>>>(a);
         break;
     }
 }
 
 // ------------------------------------------------------------------ attention
 
-constexpr int step_waves = 16;
+constexpr int step_waves = 8;
 
+// One workgroup per (lane, head); wave w owns key blocks w, w + waves, ...
+// Every lane of a wave loads its key row and its value columns of the block up
+// front, so one memory round trip precedes the serial fma chains.
 template <int HW>
 __global__ __launch_bounds__(step_waves * wave) void attention_step_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ keys,
     const uint16_t* __restrict__ values, long long lane_stride, int width, int heads, float scale,
     const int* position_ptr, int fixed_position, int replay, uint16_t* __restrict__ out)
 {
+    constexpr int per_lane = HW / 64; // value columns per lane (adjacent)
     extern __shared__ float partial[]; // [blocks][2 + HW]
     __shared__ float qf[HW];
     __shared__ float weights[step_waves][64];
     const int lane_index = blockIdx.x / heads, head = blockIdx.x % heads;
     const int lane = threadIdx.x % wave;
     const int warp = threadIdx.x / wave;
+    const int waves = blockDim.x / wave;
     const int time = (position_ptr ? *position_ptr : fixed_position) + 1;
     const int blocks = (time + 63) / 64;
     const bool round_values = time > 64 || replay;
     const uint16_t* k = keys + std::size_t(lane_index) * lane_stride + head * HW;
     const uint16_t* v = values + std::size_t(lane_index) * lane_stride + head * HW;
+    // Key row of this lane and value columns [per_lane*lane, +per_lane) of every
+    // row of one block; the first block's loads are issued before the query is
+    // staged.
+    uint4 key[HW / 8];
+    uint32_t value[64];
+    const auto load_block = [&](int block)
+    {
+        const int start = block * 64;
+        const int count = time - start < 64 ? time - start : 64;
+        if (lane < count)
+        {
+            const uint4* row = reinterpret_cast<const uint4*>(k + std::size_t(start + lane) * width);
+#pragma unroll
+            for (int c = 0; c < HW / 8; ++c)
+            {
+                key[c] = row[c];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 64; ++t)
+        {
+            value[t] = 0;
+            if (t < count)
+            {
+                const uint16_t* src = v + std::size_t(start + t) * width + per_lane * lane;
+                value[t] = per_lane == 2 ? *reinterpret_cast<const uint32_t*>(src) : uint32_t(src[0]);
+            }
+        }
+    };
+    if (warp < blocks)
+    {
+        load_block(warp);
+    }
     for (int j = threadIdx.x; j < HW; j += blockDim.x)
     {
         qf[j] = bf16_to_float(query[std::size_t(lane_index) * width + head * HW + j]);
     }
     __syncthreads();
-    for (int block = warp; block < blocks; block += step_waves)
+    for (int block = warp; block < blocks; block += waves)
     {
+        if (block != warp)
+        {
+            load_block(block);
+        }
         const int start = block * 64;
         const int count = time - start < 64 ? time - start : 64;
         float score = -__builtin_inff();
         if (lane < count)
         {
-            const uint16_t* row = k + std::size_t(start + lane) * width;
             float dot = 0.0f;
 #pragma unroll
             for (int c = 0; c < HW / 8; ++c)
             {
-                const uint4 u = reinterpret_cast<const uint4*>(row)[c];
-                const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+                const uint32_t w4[4] = {key[c].x, key[c].y, key[c].z, key[c].w};
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                 {
@@ -273,20 +370,30 @@ __global__ __launch_bounds__(step_waves * wave) void attention_step_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 64; ++t)
+        {
+            if (t < count)
+            {
+                const float wt = weights[warp][t];
+                s0 = __builtin_fmaf(bf16_to_float(uint16_t(value[t] & 0xffff)), wt, s0);
+                if (per_lane == 2)
+                {
+                    s1 = __builtin_fmaf(bf16_to_float(uint16_t(value[t] >> 16)), wt, s1);
+                }
+            }
+        }
         float* record = partial + std::size_t(block) * (2 + HW);
         if (lane == 0)
         {
             record[0] = maximum;
             record[1] = sum;
         }
-        for (int j = lane; j < HW; j += 64)
+        record[2 + per_lane * lane] = round_values ? round_bf16(s0) : s0;
+        if (per_lane == 2)
         {
-            float s = 0.0f;
-            for (int t = 0; t < count; ++t)
-            {
-                s = __builtin_fmaf(bf16_to_float(v[std::size_t(start + t) * width + j]), weights[warp][t], s);
-            }
-            record[2 + j] = round_values ? round_bf16(s) : s;
+            record[3 + per_lane * lane] = round_values ? round_bf16(s1) : s1;
         }
         __builtin_amdgcn_wave_barrier();
     }
@@ -295,7 +402,6 @@ __global__ __launch_bounds__(step_waves * wave) void attention_step_kernel(
     {
         return;
     }
-    constexpr int per_lane = (HW + 63) / 64;
     float numerator[per_lane];
 #pragma unroll
     for (int i = 0; i < per_lane; ++i)
@@ -316,24 +422,17 @@ __global__ __launch_bounds__(step_waves * wave) void attention_step_kernel(
 #pragma unroll
         for (int i = 0; i < per_lane; ++i)
         {
-            const int j = lane + 64 * i;
-            if (j < HW)
-            {
-                const float old = numerator[i] * old_scale;
-                numerator[i] = __builtin_fmaf(record[2 + j], new_scale, old);
-            }
+            const float old = numerator[i] * old_scale;
+            numerator[i] = __builtin_fmaf(record[2 + per_lane * lane + i], new_scale, old);
         }
         running_maximum = running_maximum < maximum ? maximum : running_maximum;
     }
     const float reciprocal = 1.0f / total;
+    uint16_t* o = out + std::size_t(lane_index) * width + head * HW + per_lane * lane;
 #pragma unroll
     for (int i = 0; i < per_lane; ++i)
     {
-        const int j = lane + 64 * i;
-        if (j < HW)
-        {
-            out[std::size_t(lane_index) * width + head * HW + j] = float_to_bf16(numerator[i] * reciprocal);
-        }
+        o[i] = float_to_bf16(numerator[i] * reciprocal);
     }
 }
 
@@ -385,6 +484,9 @@ __device__ __forceinline__ uint16_t q15(float left, float mass)
 }
 
 constexpr int sample_waves = 8;
+// Payload bytes staged per launch: each of at most 8 symbols consumes at most
+// 10 decisions x 2 bytes, so 256 bytes always cover a launch.
+constexpr int window = 256;
 
 // Heap-ordered subtree masses of one 1024-symbol row held 16 per lane, into
 // nodes[1..1023] (shared memory).
@@ -430,137 +532,168 @@ __device__ __forceinline__ bool build_masses(const float (&leaf)[16], int lane, 
     return __all(valid);
 }
 
+// Up to `sample_waves` lanes: one wavefront each for the softmax and masses,
+// then thread 0 decodes the lanes' symbols in stream order.
 __global__ __launch_bounds__(sample_waves * wave) void sample_kernel(const Sample a)
 {
     __shared__ float nodes[sample_waves][1024];
     __shared__ uint16_t leaves[sample_waves][1024];
     __shared__ int valid[sample_waves];
+    __shared__ int rows[sample_waves];
+    __shared__ uint8_t bytes[window];
+    __shared__ DecoderState shared_state;
     const int lane = threadIdx.x % wave, warp = threadIdx.x / wave;
     const int step = a.step ? *a.step : a.fixed_step;
-    for (int first = 0; first < a.lanes; first += sample_waves)
+    const int i = warp;
+    const bool active = i < a.lanes;
+    // Independent loads first: logits, row offset, decoder state.
+    uint16_t v[16];
+    int row = 0;
+    if (active)
     {
-        const int i = first + warp;
-        if (i < a.lanes)
+        load_row<16>(a.logits + std::size_t(i) * 1024 + lane * 16, v);
+        row = a.row_base[i] + step * a.step_stride + a.book;
+    }
+    if (a.state && threadIdx.x == 0)
+    {
+        shared_state = *a.state;
+    }
+    __syncthreads();
+    // The payload window after the current offset, held in a register until
+    // the softmax is done.
+    uint32_t byte = 0;
+    const unsigned long long base_offset = a.state ? shared_state.offset : 0;
+    if (a.state && threadIdx.x < window && base_offset + threadIdx.x < a.payload_bytes)
+    {
+        byte = a.payload[base_offset + threadIdx.x];
+    }
+    if (active)
+    {
+        if (lane == 0)
         {
-            // Softmax (src/common/probability.cpp:96-122), 16 values per lane.
-            uint16_t v[16];
-            load_row<16>(a.logits + std::size_t(i) * 1024 + lane * 16, v);
-            float maximum = -__builtin_inff();
-            bool finite = true;
+            rows[warp] = row;
+        }
+        // Softmax (src/common/probability.cpp:96-122).
+        float maximum = -__builtin_inff();
+        bool finite = true;
 #pragma unroll
-            for (int k = 0; k < 16; ++k)
-            {
-                const float value = bf16_to_float(v[k]);
-                finite = finite && is_finite(value);
-                maximum = maximum < value ? value : maximum;
-            }
-            if (!finite)
-            {
-                a.error[0] = 1u;
-            }
-            maximum = group_max<wave>(maximum);
-            float e[16], leaves_sum[16];
+        for (int k = 0; k < 16; ++k)
+        {
+            const float value = bf16_to_float(v[k]);
+            finite = finite && is_finite(value);
+            maximum = maximum < value ? value : maximum;
+        }
+        if (!finite)
+        {
+            a.error[0] = 1u;
+        }
+        maximum = group_max<wave>(maximum);
+        float e[16], leaves_sum[16];
 #pragma unroll
-            for (int k = 0; k < 16; ++k)
-            {
-                const float shifted = bf16_to_float(v[k]) - maximum;
-                e[k] = original_exp(shifted);
-                leaves_sum[k] = e[k];
-            }
-            const float total = row_sum<16>(leaves_sum);
-            const float reciprocal = 1.0f / total;
-            float p[16];
+        for (int k = 0; k < 16; ++k)
+        {
+            const float shifted = bf16_to_float(v[k]) - maximum;
+            e[k] = original_exp(shifted);
+            leaves_sum[k] = e[k];
+        }
+        const float total = row_sum<16>(leaves_sum);
+        const float reciprocal = 1.0f / total;
+        float p[16];
 #pragma unroll
-            for (int k = 0; k < 16; ++k)
+        for (int k = 0; k < 16; ++k)
+        {
+            v[k] = float_to_bf16(e[k] * reciprocal);
+            p[k] = bf16_to_float(v[k]);
+        }
+        store_row<16>(&leaves[warp][lane * 16], v);
+        if (a.distributions)
+        {
+            store_row<16>(a.distributions + std::size_t(row) * 1024 + lane * 16, v);
+        }
+        if (a.state)
+        {
+            const bool ok = build_masses(p, lane, nodes[warp]);
+            if (lane == 0)
             {
-                v[k] = float_to_bf16(e[k] * reciprocal);
-                p[k] = bf16_to_float(v[k]);
-            }
-            store_row<16>(&leaves[warp][lane * 16], v);
-            const std::size_t row = std::size_t(a.row_base[i]) + std::size_t(step) * a.step_stride + a.book;
-            if (a.distributions)
-            {
-                store_row<16>(a.distributions + row * 1024 + lane * 16, v);
-            }
-            if (a.state)
-            {
-                const bool ok = build_masses(p, lane, nodes[warp]);
-                if (lane == 0)
-                {
-                    valid[warp] = ok;
-                }
+                valid[warp] = ok;
             }
         }
-        __syncthreads();
-        if (threadIdx.x == 0)
+    }
+    if (threadIdx.x < window)
+    {
+        bytes[threadIdx.x] = uint8_t(byte);
+    }
+    __syncthreads();
+    if (threadIdx.x != 0)
+    {
+        return;
+    }
+    DecoderState s = a.state ? shared_state : DecoderState{};
+    for (int w = 0; w < a.lanes; ++w)
+    {
+        const int r = rows[w];
+        int token;
+        if (a.known)
         {
-            const int count = a.lanes - first < sample_waves ? a.lanes - first : sample_waves;
-            for (int w = 0; w < count; ++w)
+            token = a.known[r];
+        }
+        else
+        {
+            // decode_categorical + RangeDecoder::get.
+            if (!valid[w])
             {
-                const int lane_index = first + w;
-                const std::size_t row =
-                    std::size_t(a.row_base[lane_index]) + std::size_t(step) * a.step_stride + a.book;
-                int token;
-                if (a.known)
+                s.failed = 1;
+            }
+            int base = 0, left_count = 1024;
+            float mass = 1.0f;
+            while (left_count > 1 && !s.failed)
+            {
+                const int half = left_count / 2;
+                const float left = half == 1 ? flush(bf16_to_float(leaves[w][base]))
+                                             : nodes[w][1024 / half + base / half];
+                const uint16_t p0 = q15(left, mass);
+                const uint32_t range0 = uint32_t((uint64_t(s.range) * p0) >> 15);
+                if (s.code >= range0)
                 {
-                    token = a.known[row];
+                    s.code -= range0;
+                    s.range -= range0;
+                    base += half;
+                    left_count -= half;
+                    mass = flush(flush(mass) - flush(left));
                 }
                 else
                 {
-                    // decode_categorical + RangeDecoder::get.
-                    DecoderState s = *a.state;
-                    if (!valid[w])
-                    {
-                        s.failed = 1;
-                    }
-                    int base = 0, count_left = 1024;
-                    float mass = 1.0f;
-                    while (count_left > 1 && !s.failed)
-                    {
-                        const int half = count_left / 2;
-                        const float left = half == 1 ? flush(bf16_to_float(leaves[w][base]))
-                                                     : nodes[w][1024 / half + base / half];
-                        const uint16_t p0 = q15(left, mass);
-                        const uint32_t range0 = uint32_t((uint64_t(s.range) * p0) >> 15);
-                        const bool bit = s.code >= range0;
-                        if (bit)
-                        {
-                            s.code -= range0;
-                            s.range -= range0;
-                            base += half;
-                            count_left -= half;
-                            mass = flush(flush(mass) - flush(left));
-                        }
-                        else
-                        {
-                            s.range = range0;
-                            count_left = half;
-                            mass = left;
-                        }
-                        while (s.range < 0xff01u)
-                        {
-                            s.range <<= 8;
-                            const uint32_t byte = s.offset < a.payload_bytes ? a.payload[s.offset] : 0u;
-                            s.offset += s.offset < a.payload_bytes ? 1 : 0;
-                            s.code = (s.code << 8) + byte;
-                        }
-                        if (!(s.code < s.range))
-                        {
-                            s.failed = 1;
-                        }
-                    }
-                    *a.state = s;
-                    if (s.failed)
-                    {
-                        a.error[1] = 1u;
-                    }
-                    token = base;
+                    s.range = range0;
+                    left_count = half;
+                    mass = left;
                 }
-                a.current[std::size_t(lane_index) * a.books + a.book] = uint16_t(token);
-                a.tokens[row] = uint16_t(token);
+                while (s.range < 0xff01u)
+                {
+                    s.range <<= 8;
+                    const unsigned long long at = s.offset - base_offset;
+                    const uint32_t next = s.offset < a.payload_bytes
+                                              ? (at < window ? bytes[at] : a.payload[s.offset])
+                                              : 0u;
+                    s.offset += s.offset < a.payload_bytes ? 1 : 0;
+                    s.code = (s.code << 8) + next;
+                }
+                if (!(s.code < s.range))
+                {
+                    s.failed = 1;
+                }
             }
+            token = base;
         }
-        __syncthreads();
+        a.current[std::size_t(w) * a.books + a.book] = uint16_t(token);
+        a.tokens[r] = uint16_t(token);
+    }
+    if (a.state)
+    {
+        *a.state = s;
+        if (s.failed)
+        {
+            a.error[1] = 1u;
+        }
     }
 }
 
@@ -574,9 +707,16 @@ __global__ void gather_frame_kernel(const uint16_t* tokens, const int* row_base,
     }
 }
 
-__global__ void advance_kernel(int* counter, int amount)
+__global__ void set_counters_kernel(int* counters, int position, int step)
 {
-    *counter += amount;
+    counters[0] = position;
+    counters[1] = step;
+}
+
+__global__ void advance_counters_kernel(int* counters)
+{
+    counters[0] += 1;
+    counters[1] += 1;
 }
 } // namespace
 
@@ -615,18 +755,22 @@ void attention_step(const uint16_t* query, const uint16_t* keys, const uint16_t*
                     hipStream_t stream)
 {
     require(lanes > 0 && max_time > 0 && width == heads * head_width, "attention step: shape");
-    const std::size_t lds = (max_time + 63) / 64 * (2 + head_width) * sizeof(float);
+    const std::size_t blocks = (max_time + 63) / 64;
+    const std::size_t lds = blocks * (2 + head_width) * sizeof(float);
     require(lds <= 64 * 1024, "attention step: history too long");
     const unsigned grid = unsigned(lanes * heads);
+    // With a host-known position only the needed wavefronts are launched.
+    const std::size_t needed = position ? blocks : (std::size_t(fixed_position) + 64) / 64;
+    const unsigned threads = unsigned(std::min<std::size_t>(needed, step_waves) * wave);
     switch (head_width)
     {
     case 64:
-        attention_step_kernel<64><<<grid, step_waves * wave, lds, stream>>>(
+        attention_step_kernel<64><<<grid, threads, lds, stream>>>(
             query, keys, values, lane_stride, int(width), int(heads), scale, position, fixed_position,
             replay ? 1 : 0, out);
         break;
     case 128:
-        attention_step_kernel<128><<<grid, step_waves * wave, lds, stream>>>(
+        attention_step_kernel<128><<<grid, threads, lds, stream>>>(
             query, keys, values, lane_stride, int(width), int(heads), scale, position, fixed_position,
             replay ? 1 : 0, out);
         break;
@@ -666,7 +810,8 @@ void layer_norm_add(const uint16_t* x, std::size_t rows, std::size_t width, cons
 
 void sample_step(const Sample& a, hipStream_t stream)
 {
-    require(a.lanes > 0 && a.current && a.tokens && a.row_base && a.error, "sample: arguments");
+    require(a.lanes > 0 && a.lanes <= sample_waves && a.current && a.tokens && a.row_base && a.error,
+            "sample: arguments");
     require(a.known || a.state, "sample: needs known tokens or a decoder");
     sample_kernel<<<1, sample_waves * wave, 0, stream>>>(a);
     check_hip(hipGetLastError(), "sample launch");
@@ -685,9 +830,15 @@ void gather_frame(const uint16_t* tokens, const int* row_base, int frame, int st
     check_hip(hipGetLastError(), "gather launch");
 }
 
-void advance(int* counter, int amount, hipStream_t stream)
+void set_counters(int* counters, int position, int step, hipStream_t stream)
 {
-    advance_kernel<<<1, 1, 0, stream>>>(counter, amount);
-    check_hip(hipGetLastError(), "advance launch");
+    set_counters_kernel<<<1, 1, 0, stream>>>(counters, position, step);
+    check_hip(hipGetLastError(), "counter launch");
+}
+
+void advance_counters(int* counters, hipStream_t stream)
+{
+    advance_counters_kernel<<<1, 1, 0, stream>>>(counters);
+    check_hip(hipGetLastError(), "counter launch");
 }
 } // namespace tsac_hip

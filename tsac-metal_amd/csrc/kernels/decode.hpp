@@ -106,6 +106,8 @@ void sample_step(const Sample& args, hipStream_t stream);
 // dst[i][b] = tokens[row_base[i] + frame * step_stride + b] for b < books.
 void gather_frame(const uint16_t* tokens, const int* row_base, int frame, int step_stride,
                   int books, int lanes, uint16_t* dst, hipStream_t stream);
-// *counter += 1 (one thread).
-void advance(int* counter, int amount, hipStream_t stream);
+// counters[0] = position, counters[1] = step (one thread).
+void set_counters(int* counters, int position, int step, hipStream_t stream);
+// ++counters[0], ++counters[1] (one thread).
+void advance_counters(int* counters, hipStream_t stream);
 } // namespace tsac_hip

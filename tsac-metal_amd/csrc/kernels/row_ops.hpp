@@ -139,10 +139,11 @@ __device__ __forceinline__ void bf8l_lane(const uint16_t (&v)[V], int lane, int8
     }
 }
 
-// LayerNorm of one row (src/common/probability.cpp:138-169), in place.
+// LayerNorm of one row (src/common/probability.cpp:138-169), in place, with
+// this lane's gain and bias values already loaded.
 template <int V>
-__device__ __forceinline__ void layer_norm_lane(uint16_t (&v)[V], const uint16_t* gain,
-                                                const uint16_t* bias, int lane)
+__device__ __forceinline__ void layer_norm_values(uint16_t (&v)[V], const uint16_t (&g)[V],
+                                                  const uint16_t (&b)[V])
 {
     float values[V], squares[V], x[V];
 #pragma unroll
@@ -162,14 +163,22 @@ __device__ __forceinline__ void layer_norm_lane(uint16_t (&v)[V], const uint16_t
     variance += 1e-5f;
     const float inverse = 1.0f / __builtin_sqrtf(variance);
     const float offset = -mean * inverse;
-    uint16_t g[V], b[V];
-    load_row<V>(gain + lane * V, g);
-    load_row<V>(bias + lane * V, b);
 #pragma unroll
     for (int i = 0; i < V; ++i)
     {
         const float normalized = __builtin_fmaf(x[i], inverse, offset);
         v[i] = float_to_bf16(__builtin_fmaf(normalized, bf16_to_float(g[i]), bf16_to_float(b[i])));
     }
+}
+
+// LayerNorm of one row (src/common/probability.cpp:138-169), in place.
+template <int V>
+__device__ __forceinline__ void layer_norm_lane(uint16_t (&v)[V], const uint16_t* gain,
+                                                const uint16_t* bias, int lane)
+{
+    uint16_t g[V], b[V];
+    load_row<V>(gain + lane * V, g);
+    load_row<V>(bias + lane * V, b);
+    layer_norm_values<V>(v, g, b);
 }
 } // namespace tsac_hip
