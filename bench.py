@@ -106,29 +106,46 @@ def gemv_roofline(torch, native, launches):
 
 
 def gemm_roofline(torch, native, launches=20):
-    """Encode MFMA GEMM on the codebook qkv shape (M = 2580*12 rows)."""
-    M, K, N = 30960, 512, 1536
-    rng = np.random.default_rng(23)
+    """Encode MFMA GEMM on operand-tile activations (the encode's layout) for the
+    codebook stack's projections at M = 2580*12 rows; the first shape (qkv) is
+    the headline, the rest are listed with their rates. HIP events on the
+    launch stream (the default stream, as torch's events)."""
     from tsac_hip.synthetic import random_linear
 
-    linear = native.DeviceLinear(*random_linear(rng, K, N))
-    q = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda")
-    s = torch.full((M, K // 256), 0.01, dtype=torch.float32, device="cuda")
-    y = torch.empty((M, N), dtype=torch.int16, device="cuda")
-    for _ in range(3):
-        linear.apply_quantized(q, s, M, y, path=native.PATH_GEMM)
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(launches):
-        linear.apply_quantized(q, s, M, y, path=native.PATH_GEMM)
-    stop.record()
-    torch.cuda.synchronize()
-    seconds = start.elapsed_time(stop) / 1000 / launches
-    tops = 2 * M * N * K / seconds / 1e12
-    return {"kernel": "gemm_kernel", "bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
-            "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
-            "avg_launch_us": round(seconds * 1e6, 2), "shape": {"M": M, "K": K, "N": N}}
+    shapes = [(30960, 512, 1536, False), (30960, 512, 512, True), (30960, 512, 2048, False),
+              (30960, 2048, 512, True), (30960, 512, 1024, False)]
+    rng = np.random.default_rng(23)
+    rows = []
+    for M, K, N, with_residual in shapes:
+        linear = native.DeviceLinear(*random_linear(rng, K, N))
+        P = native.tile_rows(M)
+        x = torch.from_numpy(np.ascontiguousarray(
+            (rng.standard_normal((M, K)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16).view(np.int16)))
+        x = x.cuda()
+        q = torch.empty(P * K, dtype=torch.int8, device="cuda")
+        s = torch.empty(K // 256 * P, dtype=torch.float32, device="cuda")
+        native.bf8l_tiles(x, M, K, q, s)
+        y = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+        residual = y if with_residual else None
+        for _ in range(3):
+            linear.apply_quantized(q, s, M, y, residual=residual, path=native.PATH_GEMM_TILES)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(launches):
+            linear.apply_quantized(q, s, M, y, residual=residual, path=native.PATH_GEMM_TILES)
+        stop.record()
+        torch.cuda.synchronize()
+        seconds = start.elapsed_time(stop) / 1000 / launches
+        tops = 2 * M * N * K / seconds / 1e12
+        rows.append({"M": M, "K": K, "N": N, "residual": with_residual, "us": round(seconds * 1e6, 2),
+                     "TOP/s": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)})
+        del linear, x, q, s, y
+    head = rows[0]
+    return {"kernel": "gemm_kernel<true, Config<128, 2, 2, true>>", "bound": "mfma", "achieved": head["TOP/s"],
+            "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": head["frac"], "traffic": None,
+            "avg_launch_us": head["us"], "shape": {"M": head["M"], "K": head["K"], "N": head["N"]},
+            "shapes": rows}
 
 
 def qlinear_table(torch, native):

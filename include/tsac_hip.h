@@ -139,10 +139,14 @@ int tsac_hip_linear_create(const tsac_hip_linear* weights, size_t K, size_t N,
                            tsac_hip_device_linear** linear);
 void tsac_hip_linear_destroy(tsac_hip_device_linear* linear);
 
-/* path: 0 automatic (GEMV for M <= 8, else MFMA GEMM), 1 GEMV, 2 GEMM. */
+/* path: 0 automatic (GEMV for M <= 8, else MFMA GEMM), 1 GEMV, 2 GEMM; the GEMM
+ * needs y and residual 16-byte aligned.
+ * 3 = GEMM on activations in MFMA operand tiles (tsac_hip_bf8l_tiles);
+ * accepted by tsac_hip_linear_apply_quantized only. */
 #define TSAC_HIP_PATH_AUTO 0
 #define TSAC_HIP_PATH_GEMV 1
 #define TSAC_HIP_PATH_GEMM 2
+#define TSAC_HIP_PATH_GEMM_TILES 3
 
 /* PackedLinear::apply_into (src/common/packed_linear.tpp:264-302) on device
  * memory: x [M][K] BF16 -> y [M][N] BF16. Quantisation scratch comes from the
@@ -162,6 +166,16 @@ int tsac_hip_linear_apply_quantized(const tsac_hip_device_linear* linear, const 
  * K in {256, 512, 1024, 2048, 4096}. Fails if any input is not finite. */
 int tsac_hip_bf8l(const uint16_t* x, size_t rows, size_t K, int8_t* q, float* scales,
                   void* stream);
+
+/* The same quantisation written as MFMA operand tiles for the encode GEMM
+ * (no reference counterpart: the layout is this library's). Rows are padded
+ * to P = tsac_hip_tile_rows(rows); byte k of row m is at
+ * ((m/32)*(K/32) + k/32)*1024 + ((m%32) + 32*((k/16)%2))*16 + k%16 of q
+ * (P*K bytes), and scales are transposed, scales[b*P + m] (P*K/256 floats).
+ * Padding rows are left unwritten. */
+int tsac_hip_bf8l_tiles(const uint16_t* x, size_t rows, size_t K, int8_t* q, float* scales,
+                        void* stream);
+size_t tsac_hip_tile_rows(size_t rows);
 
 /* probability_layer_norm_bf16_into (src/common/probability.cpp:138-169), rows
  * of `width` in {256, 512, 1024, 2048}. */

@@ -140,6 +140,97 @@ def test_qlinear_fused_residual(torch, native, oracle):
         assert np.array_equal(host(y), expected)
 
 
+def _tile_offsets(m, k):
+    """Byte offset of (row, k) in the MFMA operand-tile layout of bf8l_tiles."""
+    r = np.arange(m)[:, None]
+    c = np.arange(k)[None, :]
+    return ((r // 32) * (k // 32) + c // 32) * 1024 + ((r % 32) + 32 * ((c // 16) % 2)) * 16 + c % 16
+
+
+@pytest.mark.parametrize("m,k,n", [(9, 256, 64), (130, 512, 192), (77, 2048, 512), (300, 512, 1536),
+                                   (129, 4096, 1024), (1000, 1024, 320)])
+def test_gemm_tiles_and_rows_layouts_agree(torch, native, oracle, m, k, n):
+    """The GEMM on operand tiles (encode path), on row-major activations, and
+    the GEMV in blocks of eight columns agree bit for bit with the oracle, with
+    and without a residual, at row and column counts that leave partial tiles."""
+    rng = np.random.default_rng(m * 31 + k + n)
+    values, scales, bias = random_linear(rng, k, n, bias_std=0.1)
+    x = _activations(rng, m, k)
+    linear = native.DeviceLinear(values, scales, bias)
+    padded = native.tile_rows(m)
+    assert padded % 128 == 0 and padded >= m
+    q_rows = empty(torch, (m, k), torch.int8)
+    s_rows = empty(torch, (m, k // 256), torch.float32)
+    native.bf8l(dev(torch, x), m, k, q_rows, s_rows)
+    q_tiles = empty(torch, (padded * k,), torch.int8)
+    s_tiles = empty(torch, (k // 256, padded), torch.float32)
+    native.bf8l_tiles(dev(torch, x), m, k, q_tiles, s_tiles)
+    # The tile layout holds the same bytes and scales as the rows.
+    assert np.array_equal(host(q_tiles, np.int8)[_tile_offsets(m, k)], host(q_rows, np.int8))
+    assert np.array_equal(host(s_tiles, np.float32)[:, :m].T, host(s_rows, np.float32))
+    expected = oracle.qlinear(values, scales, bias, x)
+    skip = bf16_bits(rng.standard_normal((m, n)).astype(np.float32))
+    with_skip = np.array([[oracle.add_bf16(int(a), int(b)) for a, b in zip(r1, r2)]
+                          for r1, r2 in zip(skip, expected)], np.uint16)
+    for residual, want in ((False, expected), (True, with_skip)):
+        results = []
+        for q, s, path in ((q_tiles, s_tiles, native.PATH_GEMM_TILES), (q_rows, s_rows, native.PATH_GEMM)):
+            y = dev(torch, skip) if residual else empty(torch, (m, n), torch.int16)
+            linear.apply_quantized(q, s, m, y, residual=y if residual else None, path=path)
+            results.append(host(y))
+        y = dev(torch, skip) if residual else empty(torch, (m, n), torch.int16)
+        for r in range(0, m, 8):
+            linear.apply_quantized(q_rows[r:r + 8], s_rows[r:r + 8], min(8, m - r), y[r:r + 8],
+                                   residual=y[r:r + 8] if residual else None, path=native.PATH_GEMV)
+        results.append(host(y))
+        for got in results:
+            assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("k,n,with_residual", [(512, 1536, False), (2048, 512, True)])
+def test_gemm_many_tiles_per_workgroup(torch, native, k, n, with_residual):
+    """At the encode's 2580 x 12 rows every persistent workgroup walks several
+    tiles (LDS reuse across tiles, output staging between them); the GEMM on
+    operand tiles must equal the GEMV in blocks of eight columns, on two runs."""
+    rng = np.random.default_rng(k + n)
+    m = 30960
+    linear = native.DeviceLinear(*random_linear(rng, k, n, bias_std=0.1))
+    x = dev(torch, _activations(rng, m, k))
+    skip = dev(torch, bf16_bits(rng.standard_normal((m, n)).astype(np.float32)))
+    padded = native.tile_rows(m)
+    q_tiles = empty(torch, (padded * k,), torch.int8)
+    s_tiles = empty(torch, (k // 256 * padded,), torch.float32)
+    native.bf8l_tiles(x, m, k, q_tiles, s_tiles)
+    q_rows = empty(torch, (m, k), torch.int8)
+    s_rows = empty(torch, (m, k // 256), torch.float32)
+    native.bf8l(x, m, k, q_rows, s_rows)
+    want = skip.clone()
+    for r in range(0, m, 8):
+        native_rows = min(8, m - r)
+        linear.apply_quantized(q_rows[r:r + 8], s_rows[r:r + 8], native_rows, want[r:r + 8],
+                               residual=want[r:r + 8] if with_residual else None, path=native.PATH_GEMV)
+    want = host(want)
+    for _ in range(2):
+        y = skip.clone()
+        linear.apply_quantized(q_tiles, s_tiles, m, y, residual=y if with_residual else None,
+                               path=native.PATH_GEMM_TILES)
+        assert np.array_equal(host(y), want)
+
+
+def test_gemm_repeatable(torch, native):
+    """Two launches of the persistent GEMM give identical bytes."""
+    rng = np.random.default_rng(8)
+    m, k, n = 4000, 512, 1536
+    linear = native.DeviceLinear(*random_linear(rng, k, n))
+    x = dev(torch, _activations(rng, m, k))
+    outputs = []
+    for _ in range(2):
+        y = empty(torch, (m, n), torch.int16)
+        linear.apply(x, y, native.PATH_GEMM)
+        outputs.append(host(y))
+    assert np.array_equal(outputs[0], outputs[1])
+
+
 def test_bf8l_matches_oracle(torch, native, oracle):
     rng = np.random.default_rng(4)
     for k in (256, 512, 1024, 2048, 4096):

@@ -283,13 +283,20 @@ int tsac_hip_linear_apply(const tsac_hip_device_linear* linear, const uint16_t* 
             require(linear && (x || !M) && (y || !M), "missing argument");
             const auto s = as_stream(stream);
             const std::size_t K = linear->linear.K;
-            AsyncScratch scratch(M * K + M * (K / 256) * 4 + 256 + 8, s);
+            const LinearPath chosen = path_of(path);
+            // The GEMM reads MFMA operand tiles; the GEMV reads rows.
+            const bool tiles = chosen == LinearPath::gemm ||
+                               (chosen == LinearPath::automatic && M > gemv_max_rows());
+            const Layout layout = tiles ? Layout::tiles : Layout::rows;
+            const std::size_t rows = tiles ? tile_padded_rows(M) : M;
+            AsyncScratch scratch(rows * K + rows * (K / 256) * 4 + 256 + 8, s);
             auto* q = static_cast<int8_t*>(scratch.pointer);
-            auto* scales = reinterpret_cast<float*>(static_cast<uint8_t*>(scratch.pointer) + (M * K + 255) / 256 * 256);
-            auto* error = reinterpret_cast<uint32_t*>(scales + M * (K / 256));
+            auto* scales =
+                reinterpret_cast<float*>(static_cast<uint8_t*>(scratch.pointer) + (rows * K + 255) / 256 * 256);
+            auto* error = reinterpret_cast<uint32_t*>(scales + rows * (K / 256));
             check_hip(hipMemsetAsync(error, 0, 8, s), "hipMemsetAsync");
-            quantize_rows(x, M, K, Prologue::none, nullptr, nullptr, q, scales, nullptr, error, s);
-            tsac_hip::linear(linear->linear, q, scales, M, y, nullptr, path_of(path), s);
+            quantize_rows(x, M, K, Prologue::none, nullptr, nullptr, q, scales, nullptr, error, s, layout);
+            tsac_hip::linear(linear->linear, q, scales, M, y, nullptr, chosen, s, layout);
             uint32_t flags[2];
             check_hip(hipMemcpyAsync(flags, error, 8, hipMemcpyDeviceToHost, s), "read error words");
             check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -305,6 +312,12 @@ int tsac_hip_linear_apply_quantized(const tsac_hip_device_linear* linear, const 
         [&]
         {
             require(linear && (q || !M) && (scales || !M) && (y || !M), "missing argument");
+            if (path == TSAC_HIP_PATH_GEMM_TILES)
+            {
+                tsac_hip::linear(linear->linear, q, scales, M, y, residual, LinearPath::gemm, as_stream(stream),
+                                 Layout::tiles);
+                return;
+            }
             tsac_hip::linear(linear->linear, q, scales, M, y, residual, path_of(path), as_stream(stream));
         });
 }
@@ -324,6 +337,29 @@ int tsac_hip_bf8l(const uint16_t* x, size_t rows, size_t K, int8_t* q, float* sc
             check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
             require(!flags[0], "BF8L activations must be finite");
         });
+}
+
+int tsac_hip_bf8l_tiles(const uint16_t* x, size_t rows, size_t K, int8_t* q, float* scales, void* stream)
+{
+    return guarded(
+        [&]
+        {
+            const auto s = as_stream(stream);
+            AsyncScratch scratch(8, s);
+            auto* error = static_cast<uint32_t*>(scratch.pointer);
+            check_hip(hipMemsetAsync(error, 0, 8, s), "hipMemsetAsync");
+            quantize_rows(x, rows, K, Prologue::none, nullptr, nullptr, q, scales, nullptr, error, s,
+                          Layout::tiles);
+            uint32_t flags[2];
+            check_hip(hipMemcpyAsync(flags, error, 8, hipMemcpyDeviceToHost, s), "read error words");
+            check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+            require(!flags[0], "BF8L activations must be finite");
+        });
+}
+
+size_t tsac_hip_tile_rows(size_t rows)
+{
+    return tile_padded_rows(rows);
 }
 
 int tsac_hip_layer_norm(const uint16_t* x, size_t rows, size_t width, const uint16_t* gain,

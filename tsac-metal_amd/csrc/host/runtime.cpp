@@ -27,6 +27,13 @@ bool supported_width(std::size_t k)
 {
     return k == 256 || k == 512 || k == 1024 || k == 2048 || k == 4096;
 }
+
+// Quantised activations feed the MFMA GEMM in operand tiles; a handful of
+// rows stays row-major for the GEMV.
+Layout activation_layout(std::size_t rows)
+{
+    return rows > gemv_max_rows() ? Layout::tiles : Layout::rows;
+}
 } // namespace
 
 // ---------------------------------------------------------------- geometry
@@ -331,8 +338,9 @@ void Session::stack_rows(bool temporal, uint16_t* x, std::size_t rows, const int
     const Model& m = *model_;
     const std::size_t w = g.width;
     const std::size_t widest = std::max<std::size_t>({w, g.ffn, g.latent});
-    auto* q8 = arena_.get<int8_t>(tag + ".q8", rows * widest);
-    auto* s8 = arena_.get<float>(tag + ".s8", rows * widest / 256);
+    const Layout layout = activation_layout(rows);
+    auto* q8 = arena_.get<int8_t>(tag + ".q8", tile_padded_rows(rows) * widest);
+    auto* s8 = arena_.get<float>(tag + ".s8", tile_padded_rows(rows) * widest / 256);
     auto* qkv = arena_.get<uint16_t>(tag + ".qkv", rows * 3 * w);
     auto* att = arena_.get<uint16_t>(tag + ".att", rows * w);
     auto* hidden = arena_.get<uint16_t>(tag + ".hidden", rows * g.ffn);
@@ -342,18 +350,18 @@ void Session::stack_rows(bool temporal, uint16_t* x, std::size_t rows, const int
     {
         const std::size_t n1 = m.norm_index(temporal, l, false), n2 = m.norm_index(temporal, l, true);
         quantize_rows(x, rows, w, Prologue::layer_norm, m.norm_gain(n1), m.norm_bias(n1), q8, s8,
-                      nullptr, err, stream_);
-        linear(m.layer(temporal, l, 0), q8, s8, rows, qkv, nullptr, LinearPath::automatic, stream_);
+                      nullptr, err, stream_, layout);
+        linear(m.layer(temporal, l, 0), q8, s8, rows, qkv, nullptr, LinearPath::automatic, stream_, layout);
         attention_prefill(qkv, w, g.heads, g.head_width, starts, lengths, replays, sequences,
                           max_length, temporal ? m.rotations() : nullptr, g.attention_scale, att,
                           stream_);
-        quantize_rows(att, rows, w, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err, stream_);
-        linear(m.layer(temporal, l, 1), q8, s8, rows, x, x, LinearPath::automatic, stream_);
+        quantize_rows(att, rows, w, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err, stream_, layout);
+        linear(m.layer(temporal, l, 1), q8, s8, rows, x, x, LinearPath::automatic, stream_, layout);
         quantize_rows(x, rows, w, Prologue::layer_norm, m.norm_gain(n2), m.norm_bias(n2), q8, s8,
-                      nullptr, err, stream_);
-        linear(m.layer(temporal, l, 2), q8, s8, rows, hidden, nullptr, LinearPath::automatic, stream_);
-        quantize_rows(hidden, rows, g.ffn, Prologue::gelu, nullptr, nullptr, q8, s8, nullptr, err, stream_);
-        linear(m.layer(temporal, l, 3), q8, s8, rows, x, x, LinearPath::automatic, stream_);
+                      nullptr, err, stream_, layout);
+        linear(m.layer(temporal, l, 2), q8, s8, rows, hidden, nullptr, LinearPath::automatic, stream_, layout);
+        quantize_rows(hidden, rows, g.ffn, Prologue::gelu, nullptr, nullptr, q8, s8, nullptr, err, stream_, layout);
+        linear(m.layer(temporal, l, 3), q8, s8, rows, x, x, LinearPath::automatic, stream_, layout);
     }
 }
 
@@ -462,12 +470,13 @@ void Session::temporal_rows(const Header& h, const uint16_t* tokens, uint16_t* c
                   "upload rows");
         auto* embedded = arena_.get<uint16_t>("t.embedded", batch * g.latent);
         auto* x = arena_.get<uint16_t>("t.x", batch * w);
-        auto* q8 = arena_.get<int8_t>("t.q8", batch * std::max<std::size_t>({w, g.ffn, g.latent}));
-        auto* s8 = arena_.get<float>("t.s8", batch * std::max<std::size_t>({w, g.ffn, g.latent}) / 256);
+        const Layout layout = activation_layout(batch);
+        auto* q8 = arena_.get<int8_t>("t.q8", tile_padded_rows(batch) * std::max<std::size_t>({w, g.ffn, g.latent}));
+        auto* s8 = arena_.get<float>("t.s8", tile_padded_rows(batch) * std::max<std::size_t>({w, g.ffn, g.latent}) / 256);
         embed_sum(m.embeddings(), g.alphabet, g.latent, d_feedback, C, batch, embedded, stream_);
         quantize_rows(embedded, batch, g.latent, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err,
-                      stream_);
-        linear(m.temporal_projection(), q8, s8, batch, x, nullptr, LinearPath::automatic, stream_);
+                      stream_, layout);
+        linear(m.temporal_projection(), q8, s8, batch, x, nullptr, LinearPath::automatic, stream_, layout);
         stack_rows(true, x, batch, d_info, d_info + count, d_info + 2 * count, count, max_length, "t");
         const std::size_t f = m.final_norm_index(true);
         layer_norm_rows(x, batch, w, m.norm_gain(f), m.norm_bias(f), x, stream_);
@@ -517,19 +526,20 @@ void Session::batched(const Header& h, const uint16_t* tokens, uint16_t* distrib
         const std::size_t n = std::min(chunk_steps, steps - s0), rows = n * C;
         auto* prefix = arena_.get<uint16_t>("c.prefix", rows * g.latent);
         auto* y = arena_.get<uint16_t>("c.y", rows * w);
-        auto* q8 = arena_.get<int8_t>("c.q8", rows * widest);
-        auto* s8 = arena_.get<float>("c.s8", rows * widest / 256);
+        const Layout layout = activation_layout(rows);
+        auto* q8 = arena_.get<int8_t>("c.q8", tile_padded_rows(rows) * widest);
+        auto* s8 = arena_.get<float>("c.s8", tile_padded_rows(rows) * widest / 256);
         auto* logits = arena_.get<uint16_t>("c.logits", rows * g.alphabet);
         embed_prefixes(m.embeddings(), g.alphabet, g.latent, d_tokens + s0 * C, C, n, prefix, stream_);
-        quantize_rows(prefix, rows, g.latent, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err, stream_);
-        linear(m.codebook_projection(), q8, s8, rows, y, nullptr, LinearPath::automatic, stream_);
+        quantize_rows(prefix, rows, g.latent, Prologue::none, nullptr, nullptr, q8, s8, nullptr, err, stream_, layout);
+        linear(m.codebook_projection(), q8, s8, rows, y, nullptr, LinearPath::automatic, stream_, layout);
         scatter_rows(conditioning + s0 * w, n, w, C, 0, y, stream_);
         add_rows(y, m.positions(), rows, w, C, y, stream_);
         stack_rows(false, y, rows, d_info, d_info + chunk_steps, d_info + 2 * chunk_steps, n, C, "c");
         const std::size_t f = m.final_norm_index(false);
         quantize_rows(y, rows, w, Prologue::layer_norm, m.norm_gain(f), m.norm_bias(f), q8, s8, nullptr,
-                      err, stream_);
-        linear(m.output_projection(), q8, s8, rows, logits, nullptr, LinearPath::automatic, stream_);
+                      err, stream_, layout);
+        linear(m.output_projection(), q8, s8, rows, logits, nullptr, LinearPath::automatic, stream_, layout);
         auto* probs = arena_.get<uint16_t>("c.probs", rows * g.alphabet);
         softmax_rows(logits, rows, g.alphabet, probs, err, stream_);
         if (distributions)

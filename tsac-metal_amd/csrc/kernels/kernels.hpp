@@ -46,11 +46,27 @@ enum class Prologue
     gelu,       // GELU first (src/common/probability.cpp:45-63)
 };
 
-// x: [rows][K] BF16. q: [rows][K] int8. scales: [rows][K/256] fp32 (widened BF16).
+// Storage of quantised activations.
+//  rows:  q [rows][K] int8, scales [rows][K/256].
+//  tiles: MFMA operand tiles for the GEMM. Rows are padded to
+//         tile_padded_rows(rows) (a multiple of gemm_tile_rows); byte k of row m
+//         is at ((m/32)*(K/32) + k/32)*1024 + ((m%32) + 32*((k/16)%2))*16 + k%16,
+//         and scales are transposed: scales[b*padded + m]. Padding rows are never
+//         written and only ever feed outputs that are not stored.
+enum class Layout
+{
+    rows,
+    tiles
+};
+constexpr std::size_t gemm_tile_rows = 128;
+std::size_t tile_padded_rows(std::size_t rows);
+
+// x: [rows][K] BF16 -> q, scales in `layout` (fp32 scales are widened BF16).
 // normalized (optional, layer_norm only): [rows][K] BF16 of the normalised values.
 void quantize_rows(const uint16_t* x, std::size_t rows, std::size_t K, Prologue prologue,
                    const uint16_t* gain, const uint16_t* bias, int8_t* q, float* scales,
-                   uint16_t* normalized, uint32_t* error, hipStream_t stream);
+                   uint16_t* normalized, uint32_t* error, hipStream_t stream,
+                   Layout layout = Layout::rows);
 
 // ---- quantised linear (src/scalar/packed_linear.cpp:8-30) ---------------------
 struct DeviceLinear
@@ -76,8 +92,10 @@ enum class LinearPath
 
 // y[m][n] = bf16(chain_b fma(dot_b, ws[b][n]*as[m][b]) + bias[n]); with a residual,
 // y[m][n] = bf16(float(residual[m][n]) + float(that)). residual may alias y.
+// Activations in Layout::tiles take the GEMM path.
 void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M,
-            uint16_t* y, const uint16_t* residual, LinearPath path, hipStream_t stream);
+            uint16_t* y, const uint16_t* residual, LinearPath path, hipStream_t stream,
+            Layout layout = Layout::rows);
 std::size_t gemv_max_rows();
 
 // ---- row-wise elementwise kernels --------------------------------------------

@@ -16,13 +16,15 @@
 //    wavefront per block; every lane accumulates its row's whole block dot with
 //    v_dot4 against wave-uniform activations (no cross-lane reduction), then the
 //    ordered chain runs per (row, column) from LDS.
-//  * GEMM (encode, large M): 128x128 output tiles per 256-thread workgroup,
-//    int8 MFMA 32x32x32 into int32 accumulators per 256-wide K block, LDS-staged
-//    operand tiles, and the per-block fp32 fma epilogue into a second
-//    accumulator set.
+//  * GEMM (encode, large M): persistent 256-thread workgroups over 128x128
+//    output tiles, int8 MFMA 32x32x32 into int32 accumulators per 256-wide K
+//    block, operands streamed through an LDS ring by direct global->LDS loads,
+//    and the per-block fp32 fma epilogue into a second accumulator set.
 #include "device_numeric.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+#include <cstdint>
 #include <cstring>
 
 namespace tsac_hip
@@ -137,171 +139,435 @@ void launch_gemv(const DeviceLinear& w, const int8_t* q, const float* scales, st
 }
 
 // ------------------------------------------------------------------ GEMM (MFMA)
+//
+// Persistent workgroups (two per CU) walk 128 x 128 output tiles. The tiles of
+// each XCD are one contiguous run in (row panel, column tile) order, so a
+// 128-row activation panel is fetched from HBM once and then reused from that
+// XCD's L2 by all column tiles. Operands stream through a four-slot LDS ring
+// filled by direct global->LDS loads (global_load_lds_dwordx4) three stages
+// ahead of the MFMAs; the stream runs on across tile boundaries, so the next
+// tile's first stages load during the current tile's epilogue.
+//
+// The MFMA's first operand is the weight tile and its second the activations:
+// lane l, register r of a 32 x 32 result holds column n = 8*(r/4) + 4*(l/32) + r%4
+// of row m = l%32, so each lane owns runs of four consecutive outputs of a row
+// and stores 8 bytes at a time.
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int tile_m = 128, tile_n = 128, stage_k = 128, lds_stride = stage_k + 16;
-
-__global__ __launch_bounds__(256) void gemm_kernel(
-    const int8_t* __restrict__ weights, const float* __restrict__ weight_scales,
-    const float* __restrict__ bias, int N, int K, const int8_t* __restrict__ q,
-    const float* __restrict__ activation_scales, int M, uint16_t* y, const uint16_t* residual)
+namespace gemm
 {
-    __shared__ __attribute__((aligned(16))) int8_t a_tile[tile_m * lds_stride];
-    __shared__ __attribute__((aligned(16))) int8_t b_tile[tile_n * lds_stride];
-    __shared__ float a_scale[tile_m];
-    __shared__ float w_scale[tile_n];
+constexpr int tile_n = 128, tile_m = int(gemm_tile_rows);
+constexpr int scale_bytes = 4 * (tile_n + tile_m); // ws[128], then as[128]
+constexpr int bias_bytes = 4 * tile_n;
+constexpr int out_stride = 2 * tile_n + 16; // bytes per row of the LDS output tile
+constexpr int threads = 256;
+constexpr int xcds = 8;
 
-    const int tid = threadIdx.x, lane = tid % wave, warp = tid / wave;
-    const int wm = warp / 2, wn = warp % 2;
-    const int n0 = blockIdx.x * tile_n, m0 = blockIdx.y * tile_m;
-    const int blocks = K / 256;
-    const int row_tiles = N / tile_rows;
+// StageK bytes of K per pipeline stage, Ring LDS stage slots, PerCU resident
+// workgroups per CU; Preload reads a stage's operand fragments from LDS before
+// its MFMAs (more registers, fewer exposed LDS latencies).
+template <int StageK, int Ring, int PerCU, bool Preload> struct Config
+{
+    static_assert(StageK == 64 || StageK == 128, "stage depth");
+    static_assert(Ring >= 2, "ring depth");
+    static constexpr int stage_k = StageK, ring = Ring, per_cu = PerCU;
+    static constexpr bool preload = Preload;
+    static constexpr int slices = StageK / 32; // 32-byte MFMA k-slices per stage
+    static constexpr int copies = StageK / 16; // 1 KiB operand copies per wave per stage
+    static constexpr int stages_per_block = 256 / StageK;
+    // Block b's scales are copied with its first stage, Ring-1 stages ahead,
+    // and read after its last stage: the copies of the blocks issued in
+    // between need slots of their own.
+    static constexpr int scale_slots = (Ring - 2) / stages_per_block + 2;
+    static constexpr int weight_bytes = tile_n * StageK; // 2 row tiles x StageK/16 segments
+    static constexpr int stage_bytes = weight_bytes + tile_m * StageK; // + 4 row groups x slices
+    static constexpr int lds_bytes = Ring * stage_bytes + scale_slots * scale_bytes + bias_bytes;
+};
+using Default = Config<128, 2, 2, true>;
+} // namespace gemm
 
-    v16i acc[2][2];
-    float sum[2][2][16];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-        {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-            {
-                acc[i][j][r] = 0;
-                sum[i][j][r] = 0.0f;
-            }
-        }
+// One wavefront copies 64 x 16 bytes (or 64 x 4) from per-lane global addresses
+// to LDS at `lds` + 16*lane (4*lane); `lds` is wave-uniform. Issued as inline
+// assembly: the compiler's wait insertion treats the builtin form as aliasing
+// every later LDS read and drains all loads in flight before each one, which
+// would serialise the ring. Completion is tracked explicitly with
+// wait_vector_memory, and the "memory" clobber keeps LDS accesses in order.
+__device__ __forceinline__ uint32_t lds_address(const void* p)
+{
+    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+// M0 is reserved, so clang warns about naming it as a clobber; these kernels
+// use M0 for nothing else, and naming it keeps the compiler from assuming
+// that a value it put there survives.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void copy_to_lds16(const void* src, const void* lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_address(lds))
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void copy_to_lds4(const void* src, const void* lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_address(lds))
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
-    for (int k0 = 0; k0 < K; k0 += stage_k)
+// s_waitcnt vmcnt(N) lgkmcnt(0): at most N of this wave's vector memory
+// operations still outstanding (they complete in issue order), LDS reads done.
+template <int N> __device__ __forceinline__ void wait_vector_memory()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+// The same for a wave-uniform count known only at run time (binary search
+// over the immediates; counts above 63 wait for 63, which is stricter).
+template <int Lo, int Hi> __device__ __forceinline__ void wait_vector_memory_at_most(int n)
+{
+    if constexpr (Lo == Hi)
     {
-        const int block = k0 / 256, first_segment = (k0 % 256) / 16;
-        // Global -> registers: 128 rows x 128 bytes per operand, 4 x 16 B per thread.
-        uint4 ra[4], rb[4];
-#pragma unroll
-        for (int it = 0; it < 4; ++it)
+        wait_vector_memory<Lo>();
+    }
+    else
+    {
+        constexpr int mid = (Lo + Hi + 1) / 2;
+        if (n >= mid)
         {
-            const int index = it * 256 + tid, row = index / 8, chunk = index % 8;
-            const int m = m0 + row;
-            ra[it] = m < M ? *reinterpret_cast<const uint4*>(q + std::size_t(m) * K + k0 + chunk * 16)
-                           : make_uint4(0, 0, 0, 0);
-            // Weights: 2 row tiles x 8 segments, each a contiguous 1 KiB.
-            const int c = index / 64, t = n0 / tile_rows + c / 8;
-            rb[it] = t < row_tiles
-                         ? *reinterpret_cast<const uint4*>(
-                               weights + tile_offset(t, block, first_segment + c % 8, blocks) + (index % 64) * 16)
-                         : make_uint4(0, 0, 0, 0);
+            wait_vector_memory_at_most<mid, Hi>(n);
         }
-        const bool block_start = k0 % 256 == 0;
-        float scale_value = 0.0f;
-        if (block_start)
+        else
         {
-            if (tid < tile_m)
-            {
-                const int m = m0 + tid;
-                scale_value = m < M ? activation_scales[std::size_t(m) * blocks + block] : 0.0f;
-            }
-            else
-            {
-                const int n = n0 + tid - tile_m;
-                scale_value = n < N ? weight_scales[std::size_t(block) * N + n] : 0.0f;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int it = 0; it < 4; ++it)
-        {
-            const int index = it * 256 + tid, row = index / 8, chunk = index % 8;
-            *reinterpret_cast<uint4*>(a_tile + row * lds_stride + chunk * 16) = ra[it];
-            const int c = index / 64;
-            *reinterpret_cast<uint4*>(b_tile + ((c / 8) * tile_rows + index % 64) * lds_stride + (c % 8) * 16) =
-                rb[it];
-        }
-        if (block_start)
-        {
-            if (tid < tile_m)
-            {
-                a_scale[tid] = scale_value;
-            }
-            else
-            {
-                w_scale[tid - tile_m] = scale_value;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < stage_k; kk += 32)
-        {
-            v4i a[2], b[2];
-            const int koff = kk + (lane / 32) * 16;
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-            {
-                a[i] = *reinterpret_cast<const v4i*>(a_tile + (wm * 64 + i * 32 + lane % 32) *
-                                                                  lds_stride + koff);
-                b[i] = *reinterpret_cast<const v4i*>(b_tile + (wn * 64 + i * 32 + lane % 32) *
-                                                                  lds_stride + koff);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                {
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-                }
-        }
-        if ((k0 + stage_k) % 256 == 0)
-        {
-            // Block epilogue: one fp32 fma per output in ascending block order.
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                {
-                    const float ws = w_scale[wn * 64 + j * 32 + lane % 32];
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                    {
-                        const int row = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-                        const float scale = ws * a_scale[row];
-                        sum[i][j][r] = __builtin_fmaf(float(acc[i][j][r]), scale, sum[i][j][r]);
-                        acc[i][j][r] = 0;
-                    }
-                }
+            wait_vector_memory_at_most<Lo, mid - 1>(n);
         }
     }
+}
+
+// Workgroup barrier without the vmcnt(0) that __syncthreads() implies, which
+// would drain the loads in flight. It does wait for this wave's own LDS
+// accesses (lgkmcnt(0)), so LDS writes before it are visible to every wave
+// after it. The empty asm statements keep the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void ring_barrier()
+{
+    asm volatile("" ::: "memory");
+    wait_vector_memory<63>(); // vmcnt(63) waits for nothing; lgkmcnt(0) does
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <bool Tiles, class Cfg>
+__global__ __launch_bounds__(gemm::threads, Cfg::per_cu) void gemm_kernel(
+    const int8_t* __restrict__ weights, const float* __restrict__ weight_scales,
+    const float* __restrict__ bias, int N, int K, const int8_t* __restrict__ q,
+    const float* __restrict__ activation_scales, int M, int padded_rows, uint16_t* y,
+    const uint16_t* residual)
+{
+    using namespace gemm;
+    constexpr int stage_k = Cfg::stage_k, ring = Cfg::ring, slices = Cfg::slices, copies = Cfg::copies;
+    constexpr int stages_per_block = Cfg::stages_per_block, weight_bytes = Cfg::weight_bytes;
+    constexpr int stage_bytes = Cfg::stage_bytes;
+    __shared__ __attribute__((aligned(1024))) int8_t lds[Cfg::lds_bytes];
+    const int lane = threadIdx.x % wave;
+    const int warp = __builtin_amdgcn_readfirstlane(threadIdx.x / wave);
+    const int wn = warp % 2, wm = warp / 2;
+    const int blocks = K / 256, stages = K / stage_k;
+    const int row_tiles = N / tile_rows;
+    const int n_tiles = (N + tile_n - 1) / tile_n;
+    const int total = n_tiles * ((M + tile_m - 1) / tile_m);
+    const int per_xcd = gridDim.x / xcds;
+    const int xcd = blockIdx.x % xcds;
+    const int end = int(int64_t(total) * (xcd + 1) / xcds);
+    float* const scale_ring = reinterpret_cast<float*>(lds + ring * stage_bytes);
+    float* const bias_tile = scale_ring + Cfg::scale_slots * (scale_bytes / 4);
+
+    for (int tile = int(int64_t(total) * xcd / xcds) + int(blockIdx.x / xcds); tile < end; tile += per_xcd)
+    {
+        const int m_tile = tile / n_tiles, n_tile = tile % n_tiles;
+        // Stage s of this tile: `copies` 1 KiB operand copies per wave (waves
+        // 0-1 weights, 2-3 activations) and, at a block start, one 256-byte
+        // scale copy per wave. Stage 0 also brings the tile's bias (waves 0-1);
+        // it precedes every copy that a wait below counts.
+        const auto issue = [&](int s)
+        {
+            const int b = s / stages_per_block;
+            int8_t* slot = lds + (s % ring) * stage_bytes;
+            if (warp < 2)
+            {
+                const int t = min(n_tile * 2 + warp, row_tiles - 1);
+                const int8_t* src =
+                    weights + tile_offset(t, b, (s % stages_per_block) * copies, blocks) + lane * 16;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+                for (int i = 0; i < copies; ++i)
+                {
+                    copy_to_lds16(src + i * tile_rows * 16, slot + (warp * copies + i) * 1024);
+                }
+            }
+            else
+            {
+#pragma unroll
+                for (int i = 0; i < copies; ++i)
+                {
+                    const int c = (warp - 2) * copies + i, group = c / slices, slice = c % slices;
+                    const int8_t* src;
+                    if constexpr (Tiles)
+                    {
+                        src = q + (std::size_t(m_tile * 4 + group) * (K / 32) + s * slices + slice) * 1024 +
+                              lane * 16;
+                    }
+                    else
+                    {
+                        const int row = min(m_tile * tile_m + group * 32 + lane % 32, M - 1);
+                        src = q + std::size_t(row) * K + s * stage_k + slice * 32 + (lane / 32) * 16;
+                    }
+                    copy_to_lds16(src, slot + weight_bytes + (group * slices + slice) * 1024);
+                }
+            }
+            if (s % stages_per_block == 0)
+            {
+                float* scales = scale_ring + (b % Cfg::scale_slots) * (scale_bytes / 4);
+                const float* src;
+                if (warp < 2)
+                {
+                    const int n = min(n_tile * tile_n + warp * 64 + lane, N - 1);
+                    src = weight_scales + std::size_t(b) * N + n;
+                }
+                else
+                {
+                    const int m = m_tile * tile_m + (warp - 2) * 64 + lane;
+                    src = Tiles ? activation_scales + std::size_t(b) * padded_rows + m
+                                : activation_scales + std::size_t(min(m, M - 1)) * blocks + b;
+                }
+                copy_to_lds4(src, scales + warp * 64);
+                if (s == 0 && warp < 2)
+                {
+                    copy_to_lds4(bias + min(n_tile * tile_n + warp * 64 + lane, N - 1), bias_tile + warp * 64);
+                }
+            }
+        };
+
+        v16i acc[2][2];
+        float sum[2][2][16];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                {
+                    acc[j][i][r] = 0;
+                    sum[j][i][r] = 0.0f;
+                }
+
+        // The previous tile's readers of every slot passed this barrier.
+        ring_barrier();
+        for (int s = 0; s < ring - 1 && s < stages; ++s)
         {
-            const int n = n0 + wn * 64 + j * 32 + lane % 32;
-            if (n >= N)
+            issue(s);
+        }
+        for (int s = 0; s < stages; ++s)
+        {
+            // Stage s has landed once only the copies of the later stages
+            // already issued (s+1 .. s+ring-2) may still be outstanding.
+            const int last = min(s + ring - 2, stages - 1);
+            wait_vector_memory_at_most<0, 63>((last - s) * copies + (last / stages_per_block - s / stages_per_block));
+            ring_barrier();
+            if (s + ring - 1 < stages)
+            {
+                issue(s + ring - 1);
+            }
+
+            const int8_t* slot = lds + (s % ring) * stage_bytes;
+            const auto fragment_w = [&](int slice, int j)
+            {
+                return *reinterpret_cast<const v4i*>(slot + (wn * copies + 2 * slice + lane / 32) * 1024 +
+                                                     (j * 32 + lane % 32) * 16);
+            };
+            const auto fragment_x = [&](int slice, int i)
+            {
+                return *reinterpret_cast<const v4i*>(slot + weight_bytes + ((wm * 2 + i) * slices + slice) * 1024 +
+                                                     lane * 16);
+            };
+            if constexpr (Cfg::preload)
+            {
+                v4i a[slices][2], x[slices][2];
+#pragma unroll
+                for (int slice = 0; slice < slices; ++slice)
+                {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                    {
+                        a[slice][j] = fragment_w(slice, j);
+                        x[slice][j] = fragment_x(slice, j);
+                    }
+                }
+#pragma unroll
+                for (int slice = 0; slice < slices; ++slice)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int i = 0; i < 2; ++i)
+                        {
+                            acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[slice][j], x[slice][i], acc[j][i],
+                                                                              0, 0, 0);
+                        }
+            }
+            else
+            {
+#pragma unroll
+                for (int slice = 0; slice < slices; ++slice)
+                {
+                    const v4i a[2] = {fragment_w(slice, 0), fragment_w(slice, 1)};
+                    const v4i x[2] = {fragment_x(slice, 0), fragment_x(slice, 1)};
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int i = 0; i < 2; ++i)
+                        {
+                            acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], x[i], acc[j][i], 0, 0, 0);
+                        }
+                }
+            }
+
+            if (s % stages_per_block == stages_per_block - 1)
+            {
+                // Block epilogue: one fp32 fma per output, blocks in ascending order.
+                const float* scales = scale_ring + ((s / stages_per_block) % Cfg::scale_slots) * (scale_bytes / 4);
+                float as[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                {
+                    as[i] = scales[tile_n + wm * 64 + i * 32 + lane % 32];
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int group = 0; group < 4; ++group)
+                    {
+                        const float4 w4 = *reinterpret_cast<const float4*>(scales + wn * 64 + j * 32 + 8 * group +
+                                                                           4 * (lane / 32));
+                        const float ws[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+#pragma unroll
+                            for (int i = 0; i < 2; ++i)
+                            {
+                                const int r = 4 * group + e;
+                                sum[j][i][r] = __builtin_fmaf(float(acc[j][i][r]), ws[e] * as[i], sum[j][i][r]);
+                                acc[j][i][r] = 0;
+                            }
+                    }
+            }
+        }
+
+        // Tile epilogue; every copy has landed (the last stage waited for all),
+        // so the ring is free. Each wave rounds its 64 x 64 outputs to BF16
+        // into an LDS copy of the tile, then the workgroup writes whole rows
+        // with 16-byte stores (and reads any residual the same way).
+        static_assert(tile_m * out_stride <= Cfg::ring * stage_bytes, "output tile must fit the ring");
+        uint16_t* const out_tile = reinterpret_cast<uint16_t*>(lds);
+        ring_barrier(); // every wave has finished reading the ring
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int group = 0; group < 4; ++group)
+            {
+                const int column = wn * 64 + j * 32 + 8 * group + 4 * (lane / 32);
+                const float4 b4 = *reinterpret_cast<const float4*>(bias_tile + column);
+                const float bn[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                {
+                    const int row = wm * 64 + i * 32 + lane % 32;
+                    uint16_t out[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                    {
+                        out[e] = float_to_bf16(sum[j][i][4 * group + e] + bn[e]);
+                    }
+                    *reinterpret_cast<uint2*>(out_tile + row * (out_stride / 2) + column) =
+                        make_uint2(out[0] | (uint32_t(out[1]) << 16), out[2] | (uint32_t(out[3]) << 16));
+                }
+            }
+        ring_barrier();
+        // 16 threads per 128-column row, 16 rows per pass.
+        const int chunk = threadIdx.x % 16, n = n_tile * tile_n + chunk * 8;
+#pragma unroll
+        for (int pass = 0; pass < tile_m / 16; ++pass)
+        {
+            const int row = pass * 16 + int(threadIdx.x) / 16, m = m_tile * tile_m + row;
+            if (m >= M || n >= N)
             {
                 continue;
             }
-            const float b = bias[n];
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
+            uint4 v = *reinterpret_cast<const uint4*>(out_tile + row * (out_stride / 2) + chunk * 8);
+            const std::size_t index = std::size_t(m) * N + n;
+            if (residual)
             {
-                const int m = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-                if (m < M)
+                const uint4 r4 = *reinterpret_cast<const uint4*>(residual + index);
+                const uint32_t rw[4] = {r4.x, r4.y, r4.z, r4.w};
+                uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
                 {
-                    const std::size_t index = std::size_t(m) * N + n;
-                    y[index] = finish(sum[i][j][r], b, residual, index);
+                    const uint32_t lo = float_to_bf16(bf16_to_float(uint16_t(rw[e] & 0xffff)) +
+                                                      bf16_to_float(uint16_t(vw[e] & 0xffff)));
+                    const uint32_t hi = float_to_bf16(bf16_to_float(uint16_t(rw[e] >> 16)) +
+                                                      bf16_to_float(uint16_t(vw[e] >> 16)));
+                    vw[e] = lo | (hi << 16);
                 }
+                v = make_uint4(vw[0], vw[1], vw[2], vw[3]);
             }
+            *reinterpret_cast<uint4*>(y + index) = v;
         }
+    }
 }
 
-void launch_gemm(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M,
-                 uint16_t* y, const uint16_t* residual, hipStream_t stream)
+int compute_units()
 {
+    static const int count = []
+    {
+        int device = 0, units = 0;
+        check_hip(hipGetDevice(&device), "hipGetDevice");
+        check_hip(hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device),
+                  "hipDeviceGetAttribute");
+        return units > 0 ? units : 1;
+    }();
+    return count;
+}
+
+template <class Cfg>
+void launch_gemm_config(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M, uint16_t* y,
+                        const uint16_t* residual, Layout layout, hipStream_t stream)
+{
+    using namespace gemm;
     require(M < (std::size_t(1) << 30), "gemm: too many rows");
-    const dim3 grid(unsigned((w.N + tile_n - 1) / tile_n), unsigned((M + tile_m - 1) / tile_m));
-    gemm_kernel<<<grid, 256, 0, stream>>>(w.values, w.scales, w.bias, int(w.N), int(w.K), q, scales,
-                                          int(M), y, residual);
+    require(reinterpret_cast<uintptr_t>(y) % 16 == 0 && reinterpret_cast<uintptr_t>(residual) % 16 == 0,
+            "gemm: output and residual must be 16-byte aligned");
+    const std::size_t n_tiles = (w.N + tile_n - 1) / tile_n, m_tiles = (M + tile_m - 1) / tile_m;
+    require(n_tiles * m_tiles < (std::size_t(1) << 30), "gemm: too many tiles");
+    const std::size_t total = n_tiles * m_tiles;
+    std::size_t grid = std::size_t(compute_units()) * Cfg::per_cu;
+    grid = std::min(grid, (total + xcds - 1) / xcds * xcds);
+    grid = std::max<std::size_t>(grid / xcds * xcds, xcds);
+    const int padded = int(tile_padded_rows(M));
+    if (layout == Layout::tiles)
+    {
+        gemm_kernel<true, Cfg><<<unsigned(grid), threads, 0, stream>>>(
+            w.values, w.scales, w.bias, int(w.N), int(w.K), q, scales, int(M), padded, y, residual);
+    }
+    else
+    {
+        gemm_kernel<false, Cfg><<<unsigned(grid), threads, 0, stream>>>(
+            w.values, w.scales, w.bias, int(w.N), int(w.K), q, scales, int(M), padded, y, residual);
+    }
+}
+
+void launch_gemm(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M, uint16_t* y,
+                 const uint16_t* residual, Layout layout, hipStream_t stream)
+{
+    launch_gemm_config<gemm::Default>(w, q, scales, M, y, residual, layout, stream);
 }
 } // namespace
 
@@ -329,7 +595,7 @@ void tile_weights(const int8_t* canonical, std::size_t K, std::size_t N, int8_t*
 }
 
 void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M,
-            uint16_t* y, const uint16_t* residual, LinearPath path, hipStream_t stream)
+            uint16_t* y, const uint16_t* residual, LinearPath path, hipStream_t stream, Layout layout)
 {
     require(w.K >= 256 && w.K % 256 == 0 && w.K <= 4096, "linear: K must be a multiple of 256 <= 4096");
     require(w.N > 0 && w.N % tile_rows == 0 && w.N < (std::size_t(1) << 30),
@@ -340,16 +606,17 @@ void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::si
     }
     if (path == LinearPath::automatic)
     {
-        path = M <= gemv_max_columns ? LinearPath::gemv : LinearPath::gemm;
+        path = M <= gemv_max_columns && layout == Layout::rows ? LinearPath::gemv : LinearPath::gemm;
     }
     if (path == LinearPath::gemv)
     {
         require(M <= gemv_max_columns, "gemv: at most 8 columns");
+        require(layout == Layout::rows, "gemv: activations must be row-major");
         launch_gemv(w, q, scales, M, y, residual, stream);
     }
     else
     {
-        launch_gemm(w, q, scales, M, y, residual, stream);
+        launch_gemm(w, q, scales, M, y, residual, layout, stream);
     }
     check_hip(hipGetLastError(), "linear launch");
 }

@@ -21,7 +21,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restric
                                                        int8_t* __restrict__ q,
                                                        float* __restrict__ scales,
                                                        uint16_t* __restrict__ normalized,
-                                                       uint32_t* __restrict__ error)
+                                                       uint32_t* __restrict__ error,
+                                                       std::size_t padded_rows)
 {
     constexpr int K = 64 * V;
     const int lane = threadIdx.x % wave;
@@ -48,36 +49,48 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restric
             v[i] = gelu_bf16(v[i]);
         }
     }
-    bf8l_lane<V>(v, lane, q + size_t(row) * K, scales + size_t(row) * (K / 256), error);
+    if (padded_rows)
+    {
+        bf8l_tiles<V>(v, lane, std::size_t(row), q, scales, padded_rows, error);
+    }
+    else
+    {
+        bf8l_lane<V>(v, lane, q + size_t(row) * K, scales + size_t(row) * (K / 256), error);
+    }
 }
 
 template <int V>
 void launch_quantize(const uint16_t* x, std::size_t rows, Prologue prologue, const uint16_t* gain,
                      const uint16_t* bias, int8_t* q, float* scales, uint16_t* normalized,
-                     uint32_t* error, hipStream_t stream)
+                     uint32_t* error, std::size_t padded_rows, hipStream_t stream)
 {
     const dim3 grid(unsigned((rows + rows_per_block - 1) / rows_per_block)), block(256);
     switch (prologue)
     {
     case Prologue::none:
         quantize_kernel<V, Prologue::none><<<grid, block, 0, stream>>>(
-            x, int(rows), gain, bias, q, scales, normalized, error);
+            x, int(rows), gain, bias, q, scales, normalized, error, padded_rows);
         break;
     case Prologue::layer_norm:
         quantize_kernel<V, Prologue::layer_norm><<<grid, block, 0, stream>>>(
-            x, int(rows), gain, bias, q, scales, normalized, error);
+            x, int(rows), gain, bias, q, scales, normalized, error, padded_rows);
         break;
     case Prologue::gelu:
         quantize_kernel<V, Prologue::gelu><<<grid, block, 0, stream>>>(
-            x, int(rows), gain, bias, q, scales, normalized, error);
+            x, int(rows), gain, bias, q, scales, normalized, error, padded_rows);
         break;
     }
 }
 } // namespace
 
+std::size_t tile_padded_rows(std::size_t rows)
+{
+    return (rows + gemm_tile_rows - 1) / gemm_tile_rows * gemm_tile_rows;
+}
+
 void quantize_rows(const uint16_t* x, std::size_t rows, std::size_t K, Prologue prologue,
                    const uint16_t* gain, const uint16_t* bias, int8_t* q, float* scales,
-                   uint16_t* normalized, uint32_t* error, hipStream_t stream)
+                   uint16_t* normalized, uint32_t* error, hipStream_t stream, Layout layout)
 {
     require(rows < (std::size_t(1) << 31), "too many rows");
     require(prologue != Prologue::layer_norm || (gain && bias), "layer norm needs gain and bias");
@@ -85,22 +98,23 @@ void quantize_rows(const uint16_t* x, std::size_t rows, std::size_t K, Prologue 
     {
         return;
     }
+    const std::size_t padded = layout == Layout::tiles ? tile_padded_rows(rows) : 0;
     switch (K)
     {
     case 256:
-        launch_quantize<4>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        launch_quantize<4>(x, rows, prologue, gain, bias, q, scales, normalized, error, padded, stream);
         break;
     case 512:
-        launch_quantize<8>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        launch_quantize<8>(x, rows, prologue, gain, bias, q, scales, normalized, error, padded, stream);
         break;
     case 1024:
-        launch_quantize<16>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        launch_quantize<16>(x, rows, prologue, gain, bias, q, scales, normalized, error, padded, stream);
         break;
     case 2048:
-        launch_quantize<32>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        launch_quantize<32>(x, rows, prologue, gain, bias, q, scales, normalized, error, padded, stream);
         break;
     case 4096:
-        launch_quantize<64>(x, rows, prologue, gain, bias, q, scales, normalized, error, stream);
+        launch_quantize<64>(x, rows, prologue, gain, bias, q, scales, normalized, error, padded, stream);
         break;
     default:
         throw Error("quantize: K must be one of 256, 512, 1024, 2048, 4096");

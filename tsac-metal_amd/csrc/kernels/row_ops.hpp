@@ -80,11 +80,11 @@ template <int V> __device__ __forceinline__ float row_sum(float (&v)[V])
 }
 
 // BF8L quantisation of one row held V-per-lane (src/scalar/probability.cpp:20-38):
-// q_row/s_row are the row's int8 values and block scales (fp32, widened BF16).
-// Sets error[0] when a value is not finite.
+// packs this lane's V int8 values four to a word and returns the BF16 scale of
+// its 256-value block. Sets error[0] when a value is not finite.
 template <int V>
-__device__ __forceinline__ void bf8l_lane(const uint16_t (&v)[V], int lane, int8_t* q_row,
-                                          float* s_row, uint32_t* error)
+__device__ __forceinline__ uint16_t bf8l_pack(const uint16_t (&v)[V], uint32_t (&packed)[(V + 3) / 4],
+                                              uint32_t* error)
 {
     constexpr int lanes_per_block = 256 / V;
     float values[V];
@@ -107,7 +107,6 @@ __device__ __forceinline__ void bf8l_lane(const uint16_t (&v)[V], int lane, int8
     s = s < 1e-35f ? 1e-35f : s;
     const uint16_t scale = float_to_bf16(s);
     const float reciprocal = ftz_divide(1.0f, bf16_to_float(scale));
-    uint32_t packed[(V + 3) / 4];
 #pragma unroll
     for (int i = 0; i < (V + 3) / 4; ++i)
     {
@@ -120,6 +119,18 @@ __device__ __forceinline__ void bf8l_lane(const uint16_t (&v)[V], int lane, int8
         r = r < -128.0f ? -128.0f : (127.0f < r ? 127.0f : r);
         packed[i / 4] |= (uint32_t(int(r)) & 0xffu) << (8 * (i % 4));
     }
+    return scale;
+}
+
+// BF8L of one row into row-major storage: q_row/s_row are the row's int8
+// values [K] and block scales [K/256] (fp32, widened BF16).
+template <int V>
+__device__ __forceinline__ void bf8l_lane(const uint16_t (&v)[V], int lane, int8_t* q_row,
+                                          float* s_row, uint32_t* error)
+{
+    constexpr int lanes_per_block = 256 / V;
+    uint32_t packed[(V + 3) / 4];
+    const uint16_t scale = bf8l_pack<V>(v, packed, error);
     int8_t* q = q_row + lane * V;
     if constexpr (V == 4)
     {
@@ -136,6 +147,39 @@ __device__ __forceinline__ void bf8l_lane(const uint16_t (&v)[V], int lane, int8
     if (lane % lanes_per_block == 0)
     {
         s_row[lane / lanes_per_block] = bf16_to_float(scale);
+    }
+}
+
+// BF8L of row `row` into MFMA operand tiles. Byte k of row m lives at
+//   ((m/32)*(K/32) + k/32)*1024 + ((m%32) + 32*((k/16)%2))*16 + k%16,
+// so each block of 32 rows x 32 bytes is 1 KiB in the lane order of the int8
+// MFMA's 16-byte operand (lane = row + 32*half). Block scales are stored
+// transposed, scales[b*padded_rows + m], so a run of rows is contiguous.
+template <int V>
+__device__ __forceinline__ void bf8l_tiles(const uint16_t (&v)[V], int lane, std::size_t row,
+                                           int8_t* q, float* scales, std::size_t padded_rows,
+                                           uint32_t* error)
+{
+    constexpr int K = 64 * V, lanes_per_block = 256 / V;
+    uint32_t packed[(V + 3) / 4];
+    const uint16_t scale = bf8l_pack<V>(v, packed, error);
+    int8_t* base = q + (row / 32) * (K / 32) * 1024 + (row % 32) * 16;
+    const auto at = [&](int k) { return base + (k / 32) * 1024 + ((k / 16) % 2) * 512 + k % 16; };
+    if constexpr (V == 4)
+    {
+        *reinterpret_cast<uint32_t*>(at(lane * V)) = packed[0];
+    }
+    else
+    {
+#pragma unroll
+        for (int c = 0; c < V / 8; ++c)
+        {
+            *reinterpret_cast<uint2*>(at(lane * V + 8 * c)) = make_uint2(packed[2 * c], packed[2 * c + 1]);
+        }
+    }
+    if (lane % lanes_per_block == 0)
+    {
+        scales[std::size_t(lane / lanes_per_block) * padded_rows + row] = bf16_to_float(scale);
     }
 }
 

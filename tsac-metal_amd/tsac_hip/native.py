@@ -30,10 +30,10 @@ EXPORTS = (
     "tsac_hip_session_timing", "tsac_hip_linear_create", "tsac_hip_linear_destroy",
     "tsac_hip_linear_apply", "tsac_hip_linear_apply_quantized", "tsac_hip_bf8l",
     "tsac_hip_layer_norm", "tsac_hip_softmax", "tsac_hip_gelu", "tsac_hip_rotary", "tsac_hip_add",
-    "tsac_hip_attention", "tsac_hip_attention_causal",
+    "tsac_hip_attention", "tsac_hip_attention_causal", "tsac_hip_bf8l_tiles", "tsac_hip_tile_rows",
 )
 
-PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
+PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_TILES = 0, 1, 2, 3
 PASS_ENCODE, PASS_DECODE = 0, 1
 
 
@@ -98,6 +98,9 @@ def library() -> C.CDLL:
         lib.tsac_hip_linear_apply.argtypes = [vp, vp, sz, vp, C.c_int, vp]
         lib.tsac_hip_linear_apply_quantized.argtypes = [vp, vp, vp, sz, vp, vp, C.c_int, vp]
         lib.tsac_hip_bf8l.argtypes = [vp, sz, sz, vp, vp, vp]
+        lib.tsac_hip_bf8l_tiles.argtypes = [vp, sz, sz, vp, vp, vp]
+        lib.tsac_hip_tile_rows.argtypes = [sz]
+        lib.tsac_hip_tile_rows.restype = sz
         lib.tsac_hip_layer_norm.argtypes = [vp, sz, sz, vp, vp, vp, vp]
         lib.tsac_hip_softmax.argtypes = [vp, sz, sz, vp, vp]
         lib.tsac_hip_gelu.argtypes = [vp, sz, vp, vp]
@@ -258,6 +261,16 @@ class DeviceLinear:
 
 def bf8l(x, rows, k, q, scales, stream=None):
     check(library().tsac_hip_bf8l(_dp(x), rows, k, _dp(q), _dp(scales), _stream(stream)))
+
+
+def bf8l_tiles(x, rows, k, q, scales, stream=None):
+    """BF8L into MFMA operand tiles: q holds tile_rows(rows)*k bytes, scales
+    tile_rows(rows)*k/256 floats (transposed)."""
+    check(library().tsac_hip_bf8l_tiles(_dp(x), rows, k, _dp(q), _dp(scales), _stream(stream)))
+
+
+def tile_rows(rows):
+    return int(library().tsac_hip_tile_rows(rows))
 
 
 def layer_norm(x, rows, width, gain, bias, out, stream=None):
