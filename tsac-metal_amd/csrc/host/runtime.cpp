@@ -222,6 +222,26 @@ Model::Model(const Geometry& g, const LinearHost* projections, const uint16_t* c
     positions_ = reinterpret_cast<const uint16_t*>(constants + positions_offset);
     rotations_ = reinterpret_cast<const uint16_t*>(constants + rotations_offset);
     embeddings_ = reinterpret_cast<const uint16_t*>(constants + embeddings_offset);
+
+    // Device copies of the projection and norm tables for the frame kernel.
+    const std::size_t linear_bytes = align_up(count * sizeof(DeviceLinear), 256);
+    const std::size_t pointer_bytes = align_up(g.norms() * sizeof(const uint16_t*), 256);
+    tables_ = DeviceBuffer(linear_bytes + 2 * pointer_bytes);
+    auto* tables = tables_.as<uint8_t>();
+    check_hip(hipMemcpy(tables, projections_.data(), count * sizeof(DeviceLinear), hipMemcpyHostToDevice),
+              "upload projection table");
+    check_hip(hipMemcpy(tables + linear_bytes, gain_.data(), g.norms() * sizeof(const uint16_t*),
+                        hipMemcpyHostToDevice),
+              "upload norm table");
+    check_hip(hipMemcpy(tables + linear_bytes + pointer_bytes, bias_.data(), g.norms() * sizeof(const uint16_t*),
+                        hipMemcpyHostToDevice),
+              "upload norm table");
+    frame_.linears = reinterpret_cast<const DeviceLinear*>(tables);
+    frame_.gain = reinterpret_cast<const uint16_t* const*>(tables + linear_bytes);
+    frame_.bias = reinterpret_cast<const uint16_t* const*>(tables + linear_bytes + pointer_bytes);
+    frame_.positions = positions_;
+    frame_.rotations = rotations_;
+    frame_.embeddings = embeddings_;
 }
 
 const DeviceLinear& Model::layer(bool temporal, std::size_t layer, int op) const
@@ -282,15 +302,16 @@ void Session::clear()
 
 void Session::reset_errors()
 {
-    check_hip(hipMemsetAsync(errors_.get(), 0, 8, stream_), "hipMemsetAsync");
+    check_hip(hipMemsetAsync(errors_.get(), 0, 12, stream_), "hipMemsetAsync");
 }
 
 void Session::check_errors()
 {
-    check_hip(hipMemcpyAsync(pinned_errors_.as<uint32_t>(), errors_.get(), 8, hipMemcpyDeviceToHost, stream_),
+    check_hip(hipMemcpyAsync(pinned_errors_.as<uint32_t>(), errors_.get(), 12, hipMemcpyDeviceToHost, stream_),
               "read error words");
     check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
     const uint32_t* e = pinned_errors_.as<uint32_t>();
+    require(!e[2], "decode frame step stalled");
     require(!(e[0] & error_nonfinite), "probability model activation is not finite");
     require(!e[1], "invalid range decoder state");
 }

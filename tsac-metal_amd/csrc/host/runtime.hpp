@@ -3,6 +3,7 @@
 
 #include "../kernels/attention.hpp"
 #include "../kernels/codec.hpp"
+#include "../kernels/frame.hpp"
 #include "../kernels/kernels.hpp"
 #include "format.hpp"
 
@@ -155,12 +156,18 @@ public:
     {
         return embeddings_;
     }
+    // Device-resident tables of the model for the frame kernel.
+    const FrameModel& frame_tables() const
+    {
+        return frame_;
+    }
 
 private:
     Geometry g_;
     Limits limits_;
     int device_ = 0;
-    DeviceBuffer values_, constants_;
+    DeviceBuffer values_, constants_, tables_;
+    FrameModel frame_;
     std::vector<DeviceLinear> projections_;
     std::vector<const uint16_t*> gain_, bias_;
     const uint16_t *positions_ = nullptr, *rotations_ = nullptr, *embeddings_ = nullptr;

@@ -6,6 +6,7 @@
 // captured HIP graph whose kernels read the context position and step index
 // from device counters.
 #include "../kernels/decode.hpp"
+#include "../kernels/frame.hpp"
 #include "runtime.hpp"
 
 #include <algorithm>
@@ -321,12 +322,62 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
         codebooks(active, step, device ? counters + 1 : nullptr);
     };
 
+    // Frame steps without a context rollover run as one persistent launch each
+    // when the geometry has a frame kernel and all lanes fit one launch.
+    const bool framed = frame_supported(int(w), int(g.heads), int(g.head_width), int(g.ffn), int(g.latent),
+                                        int(g.alphabet), int(independent)) &&
+                        extent <= 1024;
+    FrameArgs frame;
+    if (framed)
+    {
+        const std::size_t count = frame_exchange_words(int(w), int(g.ffn), int(g.latent), int(g.alphabet), int(C),
+                                                       int(g.temporal_layers), int(g.codebook_layers));
+        auto* exchange = arena_.get<unsigned long long>("s.exchange", count);
+        check_hip(hipMemsetAsync(exchange, 0, count * 8, stream_), "clear exchange words");
+        frame.model = m.frame_tables();
+        frame.books = int(C);
+        frame.temporal_layers = int(g.temporal_layers);
+        frame.codebook_layers = int(g.codebook_layers);
+        frame.width = int(w);
+        frame.heads = int(g.heads);
+        frame.head_width = int(g.head_width);
+        frame.ffn = int(g.ffn);
+        frame.latent = int(g.latent);
+        frame.alphabet = int(g.alphabet);
+        frame.scale = g.attention_scale;
+        frame.keys = arena_.get<uint16_t>("s.tk", 0);
+        frame.values = arena_.get<uint16_t>("s.tv", 0);
+        frame.lane_stride = static_cast<long long>(g.temporal_layers * extent * w);
+        frame.extent = int(extent);
+        frame.current = current;
+        frame.row_base = row_base;
+        frame.step_stride = int(G * C);
+        frame.tokens = tokens;
+        frame.known = d_known;
+        frame.distributions = d_distributions;
+        frame.state = known ? nullptr : state;
+        frame.payload = d_payload;
+        frame.payload_bytes = payload_bytes;
+        frame.error = err;
+        frame.words = exchange;
+        frame.abort = err + 2;
+    }
+
     Graph graph;
     std::size_t context_used = 0;
     for (std::size_t step = 0; step < lanes.steps(); ++step)
     {
         const std::size_t active = step < lanes.base ? independent : lanes.extra * G;
-        if (context_used == g.context)
+        if (framed && context_used != g.context)
+        {
+            frame.lanes = int(active);
+            frame.position = int(context_used);
+            frame.step = int(step);
+            frame.epoch = uint32_t(step + 1); // exchange words are cleared for every pass
+            frame_step(frame, stream_);
+            ++context_used;
+        }
+        else if (context_used == g.context)
         {
             // Context rollover: reset and replay the last 256 complete frames
             // (src/common/transformer.cpp:187-203).

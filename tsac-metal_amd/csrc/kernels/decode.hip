@@ -12,31 +12,13 @@
 // prologue arithmetic.
 #include "decode.hpp"
 #include "row_ops.hpp"
+#include "step_ops.hpp"
 
 namespace tsac_hip
 {
 namespace
 {
-constexpr int tile_rows = 64;
-constexpr int segments = 16;
-constexpr int max_columns = 8;
-
-__device__ __forceinline__ std::size_t tile_offset(int t, int b, int s, int blocks)
-{
-    return ((std::size_t(t) * blocks + b) * segments + s) * (tile_rows * 16);
-}
-
-__device__ __forceinline__ void rotate(float& re, float& im, const uint16_t* c)
-{
-    const float cosine = bf16_to_float(c[0]), sine = bf16_to_float(c[1]);
-    const float im_sine = im * sine;
-    const float re_sine = re * sine;
-    const float r = __builtin_fmaf(re, cosine, -im_sine);
-    const float i = __builtin_fmaf(im, cosine, re_sine);
-    re = bf16_to_float(float_to_bf16(r));
-    im = bf16_to_float(float_to_bf16(i));
-}
-
+using namespace step;
 // ------------------------------------------------------------------ fused projection
 
 template <int V, Input I>
@@ -470,67 +452,10 @@ __global__ __launch_bounds__(256) void layer_norm_add_kernel(const uint16_t* x, 
 
 // ------------------------------------------------------------------ sampling
 
-// conditional_q15 (src/format/categorical.cpp:76-89).
-__device__ __forceinline__ uint16_t q15(float left, float mass)
-{
-    const float value = ftz_divide(ftz_multiply(left, 32768.0f), mass);
-    if (!is_finite(value) || value >= 0x1p63f || value < -0x1p63f)
-    {
-        return 1;
-    }
-    const long long integer = static_cast<long long>(__builtin_rintf(value));
-    const int low = int(uint32_t(uint64_t(integer)));
-    return uint16_t(low < 1 ? 1 : (low > 32767 ? 32767 : low));
-}
-
 constexpr int sample_waves = 8;
 // Payload bytes staged per launch: each of at most 8 symbols consumes at most
 // 10 decisions x 2 bytes, so 256 bytes always cover a launch.
 constexpr int window = 256;
-
-// Heap-ordered subtree masses of one 1024-symbol row held 16 per lane, into
-// nodes[1..1023] (shared memory).
-__device__ __forceinline__ bool build_masses(const float (&leaf)[16], int lane, float* nodes)
-{
-    bool valid = true;
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-    {
-        valid = valid && is_finite(leaf[i]) && leaf[i] >= 0.0f;
-    }
-    float level[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-    {
-        level[i] = ftz_add(leaf[2 * i], leaf[2 * i + 1]);
-        nodes[512 + lane * 8 + i] = level[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-    {
-        level[i] = ftz_add(level[2 * i], level[2 * i + 1]);
-        nodes[256 + lane * 4 + i] = level[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-    {
-        level[i] = ftz_add(level[2 * i], level[2 * i + 1]);
-        nodes[128 + lane * 2 + i] = level[i];
-    }
-    float v = ftz_add(level[0], level[1]);
-    nodes[64 + lane] = v;
-#pragma unroll
-    for (int l = 0; l < 6; ++l)
-    {
-        v = ftz_add(v, lane_xor(v, 1 << l));
-        const int size = 32 << l;
-        if ((lane * 16) % size == 0)
-        {
-            nodes[1024 / size + lane * 16 / size] = v;
-        }
-    }
-    return __all(valid);
-}
 
 // Up to `sample_waves` lanes: one wavefront each for the softmax and masses,
 // then thread 0 decodes the lanes' symbols in stream order.

@@ -1,0 +1,1468 @@
+// Frame-step kernel (frame.hpp). Every job computes exactly what the matching
+// decode kernel in decode.hip computes, in the same order (BF8L quantiser,
+// LayerNorm, exact int8 block dots and ordered per-block fma chain of
+// src/scalar/packed_linear.cpp:16-27, attention recurrence of
+// src/scalar/attention.cpp:62-101, softmax of src/common/probability.cpp:96-122,
+// categorical bisection of src/format/categorical.cpp:119-142 with the range
+// decoder of src/format/range.cpp:131-151); only where its inputs come from and
+// where its outputs go differ.
+#include "frame.hpp"
+#include "row_ops.hpp"
+#include "step_ops.hpp"
+
+#include <algorithm>
+
+namespace tsac_hip
+{
+namespace
+{
+using namespace step;
+using word = unsigned long long;
+
+constexpr int frame_waves = 8;
+constexpr int frame_threads = frame_waves * wave;
+constexpr int max_lanes = 8;
+constexpr int max_blocks = 16; // 64-key blocks of one attention query (context <= 1024)
+constexpr int max_books = 16;  // codebook positions of one frame
+// Polls of one word before a wait is declared stalled (each poll sleeps ~64
+// clocks and makes one device-scope load): seconds, far beyond any real wait.
+constexpr unsigned spin_limit = 1u << 22;
+
+// ------------------------------------------------------------------ exchange words
+
+struct Exchange
+{
+    uint32_t epoch;
+    unsigned* abort;
+};
+
+__device__ __forceinline__ void publish(word* w, std::size_t index, uint32_t payload, uint32_t epoch)
+{
+    __hip_atomic_store(w + index, (word(epoch) << 32) | payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Global-address views: job arguments reach the jobs through memory, so their
+// pointers are generic; these keep the loads global (not flat).
+template <class T> __device__ __forceinline__ const __attribute__((address_space(1))) T* global(const T* p)
+{
+    return (const __attribute__((address_space(1))) T*)(p);
+}
+
+// Job arguments reach each job through memory, so the compiler cannot see that
+// they are the same in every lane; these move them into scalar registers (and
+// make branches on them scalar).
+__device__ __forceinline__ int uniform(int v)
+{
+    return __builtin_amdgcn_readfirstlane(v);
+}
+__device__ __forceinline__ std::size_t uniform(std::size_t v)
+{
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v)), hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+    return (std::size_t(hi) << 32) | lo;
+}
+__device__ __forceinline__ long long uniform(long long v)
+{
+    return static_cast<long long>(uniform(static_cast<std::size_t>(v)));
+}
+__device__ __forceinline__ float uniform(float v)
+{
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+template <class T> __device__ __forceinline__ T* uniform(T* p)
+{
+    return reinterpret_cast<T*>(uniform(reinterpret_cast<std::size_t>(p)));
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint4 load16(const void* p)
+{
+    const u32x4 v = *global(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float2 load_float2(const float* p)
+{
+    const f32x2 v = *global(reinterpret_cast<const f32x2*>(p));
+    return make_float2(v.x, v.y);
+}
+
+__device__ __forceinline__ word peek(const word* w, std::size_t index)
+{
+    return __hip_atomic_load(global(w + index), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// This lane's V consecutive BF16 values of a row in (global) memory.
+template <int V> __device__ __forceinline__ void load_values(const uint16_t* p, uint16_t (&v)[V])
+{
+    static_assert(V % 8 == 0, "whole 16-byte chunks");
+#pragma unroll
+    for (int c = 0; c < V / 8; ++c)
+    {
+        const uint4 u = load16(p + 8 * c);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            v[8 * c + 2 * i] = uint16_t(w[i] & 0xffff);
+            v[8 * c + 2 * i + 1] = uint16_t(w[i] >> 16);
+        }
+    }
+}
+
+// Payload of word `index` once it carries the epoch; `seen` is a value already
+// loaded. After a stall (or once any wait has stalled) returns 0 at once.
+__device__ __forceinline__ bool keep_polling(unsigned& spins, const Exchange& x);
+__device__ __forceinline__ uint32_t settle(const word* w, std::size_t index, word seen, const Exchange& x)
+{
+    unsigned spins = 0;
+    while (uint32_t(seen >> 32) != x.epoch)
+    {
+        if (!keep_polling(spins, x))
+        {
+            return 0u;
+        }
+        seen = peek(w, index);
+    }
+    return uint32_t(seen);
+}
+
+__device__ __forceinline__ uint32_t take(const word* w, std::size_t index, const Exchange& x)
+{
+    return settle(w, index, peek(w, index), x);
+}
+
+// Gives up on a wait after too many polls (raising the abort word) or once
+// another wait has; true while polling should go on.
+__device__ __forceinline__ bool keep_polling(unsigned& spins, const Exchange& x)
+{
+    if (++spins % 64 == 0)
+    {
+        if (__hip_atomic_load(x.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+        {
+            return false;
+        }
+        if (spins > spin_limit)
+        {
+            __hip_atomic_store(x.abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+    }
+    // Short waits poll at once; long ones back off, which keeps the many
+    // workgroups waiting for later jobs from crowding memory.
+    if (spins < 32)
+    {
+        __builtin_amdgcn_s_sleep(1);
+    }
+    else if (spins < 128)
+    {
+        __builtin_amdgcn_s_sleep(4);
+    }
+    else
+    {
+        __builtin_amdgcn_s_sleep(12);
+    }
+    return true;
+}
+
+// Payloads of N words, at address(i) for word i, once each carries the epoch.
+// Every word is requested before any is waited for; only words not yet
+// current are polled again.
+template <int N, class Address>
+__device__ __forceinline__ void take_words(const Address& address, const Exchange& x, uint32_t (&out)[N])
+{
+    static_assert(N <= 64, "one pending mask");
+    unsigned long long pending = 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+    {
+        const word v = __hip_atomic_load(global(address(i)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        out[i] = uint32_t(v);
+        pending |= uint32_t(v >> 32) != x.epoch ? 1ull << i : 0ull;
+    }
+    unsigned spins = 0;
+    while (pending && keep_polling(spins, x))
+    {
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+        {
+            if ((pending >> i) & 1ull)
+            {
+                const word v = __hip_atomic_load(global(address(i)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (uint32_t(v >> 32) == x.epoch)
+                {
+                    out[i] = uint32_t(v);
+                    pending &= ~(1ull << i);
+                }
+            }
+        }
+    }
+}
+
+// Called by a whole wave: returns once values [first, first + count) of a word
+// vector (first and count multiples of 64) show the epoch at one word per
+// 64-value producer tile. Polling one word per tile instead of every word
+// keeps long waits from flooding memory; the reads that follow still check
+// every word.
+constexpr bool sentinel_waits = false;
+__device__ __forceinline__ void await_tiles(const word* w, std::size_t first, int count, const Exchange& x)
+{
+    if constexpr (!sentinel_waits)
+    {
+        return;
+    }
+    const int lane = threadIdx.x % wave;
+    const int tiles = count / 64;
+    bool ready = true;
+    for (int t = lane; t < tiles; t += wave)
+    {
+        ready = ready && uint32_t(peek(w, (first + std::size_t(t) * 64) / 2) >> 32) == x.epoch;
+    }
+    unsigned spins = 0;
+    while (!__all(ready) && keep_polling(spins, x))
+    {
+        if (!ready)
+        {
+            ready = true;
+            for (int t = lane; t < tiles; t += wave)
+            {
+                ready = ready && uint32_t(peek(w, (first + std::size_t(t) * 64) / 2) >> 32) == x.epoch;
+            }
+        }
+    }
+}
+
+// This lane's V consecutive BF16 values starting at value `first` (even) of a
+// word vector.
+template <int V>
+__device__ __forceinline__ void take_row(const word* w, std::size_t first, const Exchange& x, uint16_t (&v)[V])
+{
+    static_assert(V % 2 == 0, "whole words");
+    uint32_t p[V / 2];
+    take_words<V / 2>([&](int i) { return w + first / 2 + i; }, x, p);
+#pragma unroll
+    for (int i = 0; i < V / 2; ++i)
+    {
+        v[2 * i] = uint16_t(p[i] & 0xffff);
+        v[2 * i + 1] = uint16_t(p[i] >> 16);
+    }
+}
+
+template <int V>
+__device__ __forceinline__ void give_row(word* w, std::size_t first, const Exchange& x, const uint16_t (&v)[V])
+{
+#pragma unroll
+    for (int i = 0; i < V / 2; ++i)
+    {
+        publish(w, first / 2 + i, v[2 * i] | (uint32_t(v[2 * i + 1]) << 16), x.epoch);
+    }
+}
+
+// ------------------------------------------------------------------ exchange layout
+
+// Word offsets of every exchanged matrix of one step, rows of 8 lanes, row m of
+// an N-wide matrix at m*N/2.
+struct Words
+{
+    std::size_t w, qkv, hid, logit, pre, layer, temporal, book, total;
+
+    __host__ __device__ Words(int width, int ffn, int latent, int alphabet, int books, int temporal_layers,
+                               int codebook_layers)
+    {
+        w = 4 * std::size_t(width);
+        qkv = 12 * std::size_t(width);
+        hid = 4 * std::size_t(ffn);
+        logit = 4 * std::size_t(alphabet);
+        pre = 4 * std::size_t(latent);
+        layer = qkv + w + w + hid + w; // qkv, attention, mid residual, hidden, out
+        temporal = w + temporal_layers * layer;
+        book = pre + w + codebook_layers * layer + logit + 8;
+        total = temporal + std::size_t(books) * book;
+    }
+    // Temporal stack: input of layer l (l == layers is its output).
+    __host__ __device__ std::size_t t_x(int l) const
+    {
+        return l == 0 ? 0 : w + (l - 1) * layer + qkv + w + w + hid;
+    }
+    __host__ __device__ std::size_t t_qkv(int l) const
+    {
+        return w + l * layer;
+    }
+    __host__ __device__ std::size_t t_att(int l) const
+    {
+        return t_qkv(l) + qkv;
+    }
+    __host__ __device__ std::size_t t_mid(int l) const
+    {
+        return t_att(l) + w;
+    }
+    __host__ __device__ std::size_t t_hid(int l) const
+    {
+        return t_mid(l) + w;
+    }
+    __host__ __device__ std::size_t c_base(int b) const
+    {
+        return temporal + b * book;
+    }
+    __host__ __device__ std::size_t c_prefix(int b) const
+    {
+        return c_base(b);
+    }
+    __host__ __device__ std::size_t c_x(int b, int l) const
+    {
+        return l == 0 ? c_base(b) + pre : c_base(b) + pre + w + (l - 1) * layer + qkv + w + w + hid;
+    }
+    __host__ __device__ std::size_t c_qkv(int b, int l) const
+    {
+        return c_base(b) + pre + w + l * layer;
+    }
+    __host__ __device__ std::size_t c_att(int b, int l) const
+    {
+        return c_qkv(b, l) + qkv;
+    }
+    __host__ __device__ std::size_t c_mid(int b, int l) const
+    {
+        return c_att(b, l) + w;
+    }
+    __host__ __device__ std::size_t c_hid(int b, int l) const
+    {
+        return c_mid(b, l) + w;
+    }
+    __host__ __device__ std::size_t c_logits(int b, int codebook_layers) const
+    {
+        return c_base(b) + pre + w + codebook_layers * layer;
+    }
+    __host__ __device__ std::size_t c_token(int b, int codebook_layers) const
+    {
+        return c_logits(b, codebook_layers) + logit;
+    }
+};
+
+// ------------------------------------------------------------------ projection job
+
+enum class In
+{
+    words,            // BF16 rows from exchange words
+    words_norm,       // LayerNorm of those rows
+    embed_sum,        // sum of the previous frame's feedback embeddings (memory tokens)
+    embed_accumulate, // prefix (words) + embedding of the previous book's token (words)
+};
+
+enum class Out
+{
+    plain,          // y
+    residual_words, // bf16(residual row from words + y)
+    residual_row,   // bf16(one memory row + y)
+    gelu,           // gelu(y)
+    qkv,            // rotary on Q and K, all three exchanged, K and V also into the cache
+};
+
+struct Projection
+{
+    DeviceLinear w;
+    const word* x = nullptr;
+    const uint16_t* gain = nullptr;
+    const uint16_t* beta = nullptr;
+    const uint16_t* embeddings = nullptr;
+    int alphabet = 0, books = 0, book = 0;
+    const uint16_t* tokens = nullptr; // embed_sum: [lanes][token_stride]
+    int token_stride = 0;
+    const word* token_words = nullptr; // embed_accumulate: previous book's tokens
+    const word* prefix_in = nullptr;   // embed_accumulate: previous prefix (null for the first)
+    word* prefix_out = nullptr;        // embed_accumulate: published by tile 0
+    const word* residual = nullptr;
+    const uint16_t* residual_row = nullptr;
+    word* y = nullptr;
+    uint16_t* keys = nullptr; // qkv: this layer's cache at position 0 of lane 0 (null: no cache)
+    uint16_t* values = nullptr;
+    long long lane_stride = 0;
+    int position = 0;
+    const uint16_t* rotations = nullptr;
+    int width = 0, head_width = 0;
+};
+
+template <int V> constexpr int projection_lds()
+{
+    constexpr int K = wave * V, blocks = K / 256, slots = blocks > frame_waves ? blocks : frame_waves;
+    return max_lanes * K + max_lanes * blocks * 4 + slots * max_lanes * tile_rows * 4;
+}
+
+// One 64-row tile of a projection for M lanes (decode.hip fused_linear_kernel).
+template <int V, In I, Out O>
+__device__ __noinline__ void project_tile(const Projection& job, int M, int tile, const Exchange& exchange, uint32_t* error,
+                                          uint8_t* lds)
+{
+    const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
+    Projection p;
+    p.w.values = uniform(job.w.values);
+    p.w.scales = uniform(job.w.scales);
+    p.w.bias = uniform(job.w.bias);
+    p.w.K = uniform(job.w.K);
+    p.w.N = uniform(job.w.N);
+    p.x = uniform(job.x);
+    p.gain = uniform(job.gain);
+    p.beta = uniform(job.beta);
+    p.embeddings = uniform(job.embeddings);
+    p.alphabet = uniform(job.alphabet);
+    p.books = uniform(job.books);
+    p.book = uniform(job.book);
+    p.tokens = uniform(job.tokens);
+    p.token_stride = uniform(job.token_stride);
+    p.token_words = uniform(job.token_words);
+    p.prefix_in = uniform(job.prefix_in);
+    p.prefix_out = uniform(job.prefix_out);
+    p.residual = uniform(job.residual);
+    p.residual_row = uniform(job.residual_row);
+    p.y = uniform(job.y);
+    p.keys = uniform(job.keys);
+    p.values = uniform(job.values);
+    p.lane_stride = uniform(job.lane_stride);
+    p.position = uniform(job.position);
+    p.rotations = uniform(job.rotations);
+    p.width = uniform(job.width);
+    p.head_width = uniform(job.head_width);
+    M = uniform(M);
+    tile = uniform(tile);
+    error = uniform(error);
+    constexpr int K = wave * V, blocks = K / 256;
+    constexpr int waves_per_block = blocks >= frame_waves ? 1 : frame_waves / blocks;
+    constexpr int wave_segments = segments / waves_per_block;
+    constexpr int rounds = blocks > frame_waves ? blocks / frame_waves : 1;
+    int8_t* q = reinterpret_cast<int8_t*>(lds);
+    float* scales = reinterpret_cast<float*>(lds + max_lanes * K);
+    int* dots = reinterpret_cast<int*>(lds + max_lanes * K + max_lanes * blocks * 4);
+    const int lane = threadIdx.x % wave;
+    const int warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
+    const int N = int(p.w.N);
+
+    // 1. Weight loads first, then the chain constants and the residual word.
+    const int first_block = rounds > 1 ? warp : warp / waves_per_block;
+    const int first_segment = rounds > 1 ? 0 : (warp % waves_per_block) * wave_segments;
+    uint4 w[wave_segments];
+    {
+        const int8_t* base = p.w.values + tile_offset(tile, first_block, first_segment, blocks) + lane * 16;
+#pragma unroll
+        for (int s = 0; s < wave_segments; ++s)
+        {
+            w[s] = load16(base + s * tile_rows * 16);
+        }
+    }
+    const int pair = threadIdx.x % 32, column = threadIdx.x / 32;
+    const int n0 = tile * tile_rows + 2 * pair;
+    const float2 bias = load_float2(p.w.bias + n0);
+    const float bias0 = bias.x, bias1 = bias.y;
+    float ws0[blocks], ws1[blocks];
+#pragma unroll
+    for (int b = 0; b < blocks; ++b)
+    {
+        const float2 s = load_float2(p.w.scales + std::size_t(b) * N + n0);
+        ws0[b] = s.x;
+        ws1[b] = s.y;
+    }
+    const std::size_t out_word = (std::size_t(column) * N + n0) / 2;
+    // Rotary (cosine, sine) of this pair at the position, before any wait.
+    uint32_t rotation = 0;
+    if constexpr (O == Out::qkv)
+    {
+        if (p.rotations && n0 < 2 * p.width)
+        {
+            rotation = *global(reinterpret_cast<const uint32_t*>(
+                p.rotations + std::size_t(p.position) * p.head_width + n0 % p.head_width));
+        }
+    }
+    // LayerNorm constants of this lane's input values, before any wait.
+    uint16_t norm_gain[V], norm_bias[V];
+    if constexpr (I == In::words_norm)
+    {
+        if (warp < M)
+        {
+            load_values<V>(p.gain + lane * V, norm_gain);
+            load_values<V>(p.beta + lane * V, norm_bias);
+        }
+    }
+    __syncthreads(); // the previous job's readers of LDS are done
+
+    // 2. Inputs: one row per wave, quantised into LDS.
+    if (warp < M)
+    {
+        uint16_t v[V];
+        const std::size_t first = std::size_t(warp) * K + lane * V;
+        if constexpr (I == In::words || I == In::words_norm)
+        {
+            await_tiles(p.x, std::size_t(warp) * K, K, x);
+            take_row<V>(p.x, first, x, v);
+            if constexpr (I == In::words_norm)
+            {
+                layer_norm_values<V>(v, norm_gain, norm_bias);
+            }
+        }
+        else if constexpr (I == In::embed_sum)
+        {
+            // src/common/cpu_transformer.tpp:205-224: copy book 0, add later books in order.
+            const uint16_t* t = p.tokens + std::size_t(warp) * p.token_stride;
+            const int t0 = min(int(t[0]), p.alphabet - 1);
+            load_row<V>(p.embeddings + std::size_t(t0) * K + lane * V, v);
+            for (int b = 1; b < p.books; ++b)
+            {
+                const int tb = min(int(t[b]), p.alphabet - 1);
+                uint16_t e[V];
+                load_row<V>(p.embeddings + (std::size_t(b) * p.alphabet + tb) * K + lane * V, e);
+#pragma unroll
+                for (int i = 0; i < V; ++i)
+                {
+                    v[i] = float_to_bf16(bf16_to_float(v[i]) + bf16_to_float(e[i]));
+                }
+            }
+        }
+        else
+        {
+            const int token = min(int(take(p.token_words, warp, x) & 0xffffu), p.alphabet - 1);
+            load_row<V>(p.embeddings + (std::size_t(p.book) * p.alphabet + token) * K + lane * V, v);
+            if (p.prefix_in)
+            {
+                uint16_t prev[V];
+                await_tiles(p.prefix_in, std::size_t(warp) * K, K, x);
+                take_row<V>(p.prefix_in, first, x, prev);
+#pragma unroll
+                for (int i = 0; i < V; ++i)
+                {
+                    v[i] = float_to_bf16(bf16_to_float(prev[i]) + bf16_to_float(v[i]));
+                }
+            }
+            if (tile == 0)
+            {
+                give_row<V>(p.prefix_out, first, x, v);
+            }
+        }
+        bf8l_lane<V>(v, lane, q + warp * K, scales + warp * blocks, error);
+    }
+    // The residual rows come from an earlier job than the inputs just read, so
+    // requesting them now costs no wait of its own.
+    word residual_seen = 0;
+    if constexpr (O == Out::residual_words)
+    {
+        if (column < M)
+        {
+            residual_seen = peek(p.residual, out_word);
+        }
+    }
+    __syncthreads();
+
+    // 3. Exact partial dots.
+#pragma unroll
+    for (int r = 0; r < rounds; ++r)
+    {
+        const int b = rounds > 1 ? warp + r * frame_waves : first_block;
+        if (r > 0)
+        {
+            const int8_t* base = p.w.values + tile_offset(tile, b, 0, blocks) + lane * 16;
+#pragma unroll
+            for (int s = 0; s < wave_segments; ++s)
+            {
+                w[s] = load16(base + s * tile_rows * 16);
+            }
+        }
+        const int slot = b * waves_per_block + (rounds > 1 ? 0 : warp % waves_per_block);
+        for (int m = 0; m < M; ++m)
+        {
+            const uint4* xq = reinterpret_cast<const uint4*>(q + m * K + b * 256 + first_segment * 16);
+            int dot = 0;
+#pragma unroll
+            for (int s = 0; s < wave_segments; ++s)
+            {
+                const uint4 u = xq[s];
+                dot = __builtin_amdgcn_sdot4(int(w[s].x), int(u.x), dot, false);
+                dot = __builtin_amdgcn_sdot4(int(w[s].y), int(u.y), dot, false);
+                dot = __builtin_amdgcn_sdot4(int(w[s].z), int(u.z), dot, false);
+                dot = __builtin_amdgcn_sdot4(int(w[s].w), int(u.w), dot, false);
+            }
+            dots[(slot * max_lanes + m) * tile_rows + lane] = dot;
+        }
+    }
+    __syncthreads();
+
+    // 4. Ordered chain per (row pair, column), then the output.
+    if (column >= M)
+    {
+        return;
+    }
+    const int m = column;
+    float sum0 = 0.0f, sum1 = 0.0f;
+#pragma unroll
+    for (int b = 0; b < blocks; ++b)
+    {
+        int d0 = 0, d1 = 0;
+#pragma unroll
+        for (int s = 0; s < waves_per_block; ++s)
+        {
+            const int* d = dots + ((b * waves_per_block + s) * max_lanes + m) * tile_rows + 2 * pair;
+            d0 += d[0];
+            d1 += d[1];
+        }
+        const float as = scales[m * blocks + b];
+        const float scale0 = ws0[b] * as;
+        const float scale1 = ws1[b] * as;
+        sum0 = __builtin_fmaf(float(d0), scale0, sum0);
+        sum1 = __builtin_fmaf(float(d1), scale1, sum1);
+    }
+    uint16_t y0 = float_to_bf16(sum0 + bias0);
+    uint16_t y1 = float_to_bf16(sum1 + bias1);
+    if constexpr (O == Out::residual_words)
+    {
+        const uint32_t r = settle(p.residual, out_word, residual_seen, x);
+        y0 = float_to_bf16(bf16_to_float(uint16_t(r & 0xffff)) + bf16_to_float(y0));
+        y1 = float_to_bf16(bf16_to_float(uint16_t(r >> 16)) + bf16_to_float(y1));
+    }
+    else if constexpr (O == Out::residual_row)
+    {
+        y0 = float_to_bf16(bf16_to_float(p.residual_row[n0]) + bf16_to_float(y0));
+        y1 = float_to_bf16(bf16_to_float(p.residual_row[n0 + 1]) + bf16_to_float(y1));
+    }
+    else if constexpr (O == Out::gelu)
+    {
+        y0 = gelu_bf16(y0);
+        y1 = gelu_bf16(y1);
+    }
+    else if constexpr (O == Out::qkv)
+    {
+        const int width = p.width;
+        if (n0 < 2 * width && p.rotations)
+        {
+            // rotate() of step_ops.hpp on the prefetched coefficients.
+            const float cosine = bf16_to_float(uint16_t(rotation & 0xffff)), sine = bf16_to_float(uint16_t(rotation >> 16));
+            const float re = bf16_to_float(y0), im = bf16_to_float(y1);
+            const float im_sine = im * sine;
+            const float re_sine = re * sine;
+            y0 = float_to_bf16(__builtin_fmaf(re, cosine, -im_sine));
+            y1 = float_to_bf16(__builtin_fmaf(im, cosine, re_sine));
+        }
+        if (p.keys && n0 >= width)
+        {
+            uint16_t* cache = n0 < 2 * width ? p.keys + (n0 - width) : p.values + (n0 - 2 * width);
+            *reinterpret_cast<uint32_t*>(cache + std::size_t(m) * p.lane_stride + std::size_t(p.position) * width) =
+                y0 | (uint32_t(y1) << 16);
+        }
+    }
+    publish(p.y, out_word, y0 | (uint32_t(y1) << 16), x.epoch);
+}
+
+// ------------------------------------------------------------------ attention job
+
+struct Attend
+{
+    int heads = 0, width = 0;
+    float scale = 0.0f;
+    int time = 0; // keys 0 .. time-1
+    // Temporal: rows before time-1 from the cache (this layer, lane 0, row 0),
+    // row time-1 from `qkv`. Codebook (keys == null): row t from the qkv words
+    // of book t at qkv + t*book_words.
+    const uint16_t* keys = nullptr;
+    const uint16_t* values = nullptr;
+    long long lane_stride = 0;
+    const word* qkv = nullptr;
+    std::size_t book_words = 0;
+    word* out = nullptr;
+};
+
+template <int HW> constexpr int attend_lds()
+{
+    // partial records, query words, staged exchanged rows (keys then values)
+    return (max_blocks * (2 + HW) + HW / 2 + max_books * HW) * 4;
+}
+
+// One (lane, head) query over all its keys (decode.hip attention_step_kernel).
+// The rows that come through exchange words (the current position's, or every
+// codebook row) and the query are staged in LDS first, so the block loops read
+// only the cache and LDS.
+template <int HW>
+__device__ __noinline__ void attend_item(const Attend& job, int item, const Exchange& exchange, uint8_t* lds)
+{
+    const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
+    Attend a;
+    a.heads = uniform(job.heads);
+    a.width = uniform(job.width);
+    a.scale = uniform(job.scale);
+    a.time = uniform(job.time);
+    a.keys = uniform(job.keys);
+    a.values = uniform(job.values);
+    a.lane_stride = uniform(job.lane_stride);
+    a.qkv = uniform(job.qkv);
+    a.book_words = uniform(job.book_words);
+    a.out = uniform(job.out);
+    item = uniform(item);
+    constexpr int per_lane = HW / 64; // value columns per lane (adjacent)
+    constexpr int row_words = HW;     // staged row: HW/2 key words, then HW/2 value words
+    float* partial = reinterpret_cast<float*>(lds); // [blocks][2 + HW]
+    uint32_t* query_words = reinterpret_cast<uint32_t*>(partial + max_blocks * (2 + HW)); // [HW/2]
+    uint32_t* staged = query_words + HW / 2; // [max_books][row_words]
+    const int m = item / a.heads, head = item % a.heads;
+    const int lane = threadIdx.x % wave;
+    const int warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
+    const int time = a.time;
+    const int blocks = (time + 63) / 64;
+    const bool round_values = time > 64;
+    const int width = a.width;
+    const bool temporal = a.keys != nullptr;
+    const int cached = temporal ? time - 1 : 0; // rows 0..cached-1 come from the cache
+    const int exchanged = time - cached;        // the rest from words (1, or time <= max_books)
+    const std::size_t row_values = 3 * std::size_t(width);
+    const std::size_t q_value = std::size_t(m) * row_values + head * HW;
+    const auto row_words_of = [&](int t) -> const word*
+    { return temporal ? a.qkv : a.qkv + std::size_t(t) * a.book_words; };
+    const uint16_t* k = temporal ? a.keys + std::size_t(m) * a.lane_stride + head * HW : nullptr;
+    const uint16_t* v = temporal ? a.values + std::size_t(m) * a.lane_stride + head * HW : nullptr;
+
+    // 1. Stage the query and the exchanged rows: word i of the query is i < HW/2;
+    //    then row r's key words, then its value words.
+    await_tiles(row_words_of(time - 1), q_value, HW, x);
+    await_tiles(row_words_of(time - 1), q_value + width, HW, x);
+    await_tiles(row_words_of(time - 1), q_value + 2 * width, HW, x);
+    __syncthreads(); // the previous job's readers of LDS are done
+    {
+        constexpr int per_thread = (HW / 2 + max_books * row_words + frame_threads - 1) / frame_threads;
+        const int total = HW / 2 + exchanged * row_words;
+        uint32_t got[per_thread];
+        const auto address = [&](int i) -> const word*
+        {
+            int index = int(threadIdx.x) + i * frame_threads;
+            index = index < total ? index : total - 1;
+            if (index < HW / 2)
+            {
+                return row_words_of(time - 1) + q_value / 2 + index;
+            }
+            const int r = (index - HW / 2) / row_words, c = (index - HW / 2) % row_words;
+            const std::size_t value0 = q_value + (c < HW / 2 ? width : 2 * width);
+            return row_words_of(cached + r) + value0 / 2 + c % (HW / 2);
+        };
+        take_words<per_thread>(address, x, got);
+#pragma unroll
+        for (int i = 0; i < per_thread; ++i)
+        {
+            const int index = int(threadIdx.x) + i * frame_threads;
+            if (index < HW / 2)
+            {
+                query_words[index] = got[i];
+            }
+            else if (index < total)
+            {
+                staged[index - HW / 2] = got[i];
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. Blocks of 64 keys: wave w owns blocks w, w + waves, ... The query is
+    //    held in registers as packed BF16 pairs; block weights move between
+    //    lanes with readlane.
+    uint32_t query[HW / 2];
+#pragma unroll
+    for (int c = 0; c < HW / 8; ++c)
+    {
+        const uint4 u = reinterpret_cast<const uint4*>(query_words)[c];
+        query[4 * c] = u.x;
+        query[4 * c + 1] = u.y;
+        query[4 * c + 2] = u.z;
+        query[4 * c + 3] = u.w;
+    }
+    uint32_t key[HW / 2];
+    uint32_t value[64];
+    const auto load_block = [&](int block)
+    {
+        const int start = block * 64;
+        const int count = time - start < 64 ? time - start : 64;
+        const int t = start + lane;
+        if (lane < count)
+        {
+            if (t < cached)
+            {
+                const uint16_t* row = k + std::size_t(t) * width;
+#pragma unroll
+                for (int c = 0; c < HW / 8; ++c)
+                {
+                    const uint4 u = load16(row + 8 * c);
+                    key[4 * c] = u.x;
+                    key[4 * c + 1] = u.y;
+                    key[4 * c + 2] = u.z;
+                    key[4 * c + 3] = u.w;
+                }
+            }
+            else
+            {
+                const uint32_t* row = staged + (t - cached) * row_words;
+#pragma unroll
+                for (int c = 0; c < HW / 2; ++c)
+                {
+                    key[c] = row[c];
+                }
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 64; ++tt)
+        {
+            const int row = start + tt;
+            uint32_t value_word = 0;
+            if (tt < count)
+            {
+                if (row < cached)
+                {
+                    const uint16_t* src = v + std::size_t(row) * width + per_lane * lane;
+                    value_word = per_lane == 2 ? *global(reinterpret_cast<const uint32_t*>(src)) : uint32_t(*global(src));
+                }
+                else
+                {
+                    const uint32_t pw = staged[(row - cached) * row_words + HW / 2 + (per_lane * lane) / 2];
+                    value_word = per_lane == 2 ? pw : ((lane & 1) ? (pw >> 16) : (pw & 0xffff));
+                }
+            }
+            value[tt] = value_word;
+        }
+    };
+    if (warp < blocks)
+    {
+        load_block(warp);
+    }
+    for (int block = warp; block < blocks; block += frame_waves)
+    {
+        if (block != warp)
+        {
+            load_block(block);
+        }
+        const int start = block * 64;
+        const int count = time - start < 64 ? time - start : 64;
+        float score = -__builtin_inff();
+        if (lane < count)
+        {
+            float dot = 0.0f;
+#pragma unroll
+            for (int c = 0; c < HW / 2; ++c)
+            {
+                dot = __builtin_fmaf(bf16_to_float(uint16_t(query[c] & 0xffff)),
+                                     bf16_to_float(uint16_t(key[c] & 0xffff)), dot);
+                dot = __builtin_fmaf(bf16_to_float(uint16_t(query[c] >> 16)), bf16_to_float(uint16_t(key[c] >> 16)),
+                                     dot);
+            }
+            score = dot * a.scale;
+        }
+        const float maximum = group_max<wave>(score);
+        float e = 0.0f;
+        if (lane < count)
+        {
+            e = original_exp(score - maximum);
+        }
+        const float sum = tree_sum<wave>(e);
+        const int e_bits = __float_as_int(e);
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 64; ++tt)
+        {
+            if (tt < count)
+            {
+                const float wt = __int_as_float(__builtin_amdgcn_readlane(e_bits, tt));
+                s0 = __builtin_fmaf(bf16_to_float(uint16_t(value[tt] & 0xffff)), wt, s0);
+                if (per_lane == 2)
+                {
+                    s1 = __builtin_fmaf(bf16_to_float(uint16_t(value[tt] >> 16)), wt, s1);
+                }
+            }
+        }
+        float* record = partial + std::size_t(block) * (2 + HW);
+        if (lane == 0)
+        {
+            record[0] = maximum;
+            record[1] = sum;
+        }
+        record[2 + per_lane * lane] = round_values ? round_bf16(s0) : s0;
+        if (per_lane == 2)
+        {
+            record[3 + per_lane * lane] = round_values ? round_bf16(s1) : s1;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    if (warp != 0)
+    {
+        return;
+    }
+    // 3. Ordered merge of the blocks (src/scalar/attention.cpp:86-101).
+    float numerator[per_lane];
+#pragma unroll
+    for (int i = 0; i < per_lane; ++i)
+    {
+        numerator[i] = 0.0f;
+    }
+    float running_maximum = -__builtin_inff(), total = 0.0f;
+    for (int b = 0; b < blocks; ++b)
+    {
+        const float* record = partial + std::size_t(b) * (2 + HW);
+        const float maximum = record[0];
+        const float difference = maximum - running_maximum;
+        const float factor = original_exp(-__builtin_fabsf(difference));
+        const float old_scale = running_maximum > maximum ? 1.0f : factor;
+        const float new_scale = running_maximum > maximum ? factor : 1.0f;
+        const float old_total = total * old_scale;
+        total = __builtin_fmaf(record[1], new_scale, old_total);
+#pragma unroll
+        for (int i = 0; i < per_lane; ++i)
+        {
+            const float old = numerator[i] * old_scale;
+            numerator[i] = __builtin_fmaf(record[2 + per_lane * lane + i], new_scale, old);
+        }
+        running_maximum = running_maximum < maximum ? maximum : running_maximum;
+    }
+    const float reciprocal = 1.0f / total;
+    const std::size_t at = std::size_t(m) * width + head * HW + per_lane * lane;
+    if constexpr (per_lane == 2)
+    {
+        const uint32_t packed = float_to_bf16(numerator[0] * reciprocal) |
+                                (uint32_t(float_to_bf16(numerator[1] * reciprocal)) << 16);
+        publish(a.out, at / 2, packed, x.epoch);
+    }
+    else
+    {
+        const uint32_t mine = float_to_bf16(numerator[0] * reciprocal);
+        const uint32_t other = uint32_t(__shfl_xor(int(mine), 1));
+        if ((lane & 1) == 0)
+        {
+            publish(a.out, at / 2, mine | (other << 16), x.epoch);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ conditioning job
+
+// Book 0's codebook input: bf16(LayerNorm(x) + positions[0]) for every lane,
+// one wave per lane (decode.hip layer_norm_add_kernel).
+template <int V>
+__device__ __noinline__ void condition_rows(const word* in, const uint16_t* gain, const uint16_t* bias,
+                                            const uint16_t* add_row, word* out, int M, const Exchange& exchange)
+{
+    const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
+    in = uniform(in);
+    gain = uniform(gain);
+    bias = uniform(bias);
+    add_row = uniform(add_row);
+    out = uniform(out);
+    M = uniform(M);
+    constexpr int width = wave * V;
+    const int lane = threadIdx.x % wave;
+    const int row = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
+    if (row >= M)
+    {
+        return;
+    }
+    uint16_t v[V];
+    await_tiles(in, std::size_t(row) * width, width, x);
+    take_row<V>(in, std::size_t(row) * width + lane * V, x, v);
+    layer_norm_lane<V>(v, gain, bias, lane);
+    uint16_t p[V];
+    load_row<V>(add_row + lane * V, p);
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+    {
+        v[i] = float_to_bf16(bf16_to_float(v[i]) + bf16_to_float(p[i]));
+    }
+    give_row<V>(out, std::size_t(row) * width + lane * V, x, v);
+}
+
+// ------------------------------------------------------------------ sampling job
+
+constexpr int window = 256;
+constexpr int draw_lds = max_lanes * 1024 * 4 + max_lanes * 1024 * 2 + window + 2 * max_lanes * 4;
+
+struct Draw
+{
+    int book = 0, books = 0;
+    const word* logits = nullptr; // [lanes][1024] in words
+    word* token_words = nullptr;  // one per lane
+    uint16_t* current = nullptr;
+    uint16_t* tokens = nullptr;
+    const int* row_base = nullptr;
+    int step = 0, step_stride = 0;
+    const uint16_t* known = nullptr;
+    uint16_t* distributions = nullptr;
+    const uint8_t* payload = nullptr;
+    unsigned long long payload_bytes = 0;
+};
+
+// Softmax and masses per lane (one wave each), then thread 0 decodes the
+// lanes' symbols in stream order with the decoder held in `state` (LDS)
+// (decode.hip sample_kernel).
+__device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* state, const Exchange& exchange,
+                                         uint32_t* error, uint8_t* lds)
+{
+    const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
+    Draw a;
+    a.book = uniform(job.book);
+    a.books = uniform(job.books);
+    a.logits = uniform(job.logits);
+    a.token_words = uniform(job.token_words);
+    a.current = uniform(job.current);
+    a.tokens = uniform(job.tokens);
+    a.row_base = uniform(job.row_base);
+    a.step = uniform(job.step);
+    a.step_stride = uniform(job.step_stride);
+    a.known = uniform(job.known);
+    a.distributions = uniform(job.distributions);
+    a.payload = uniform(job.payload);
+    a.payload_bytes = uniform(std::size_t(job.payload_bytes));
+    M = uniform(M);
+    error = uniform(error);
+    float* nodes = reinterpret_cast<float*>(lds);                                  // [8][1024]
+    uint16_t* leaves = reinterpret_cast<uint16_t*>(lds + max_lanes * 1024 * 4);    // [8][1024]
+    uint8_t* bytes = lds + max_lanes * 1024 * 6;                                   // [window]
+    int* valid = reinterpret_cast<int*>(lds + max_lanes * 1024 * 6 + window);      // [8]
+    int* rows = valid + max_lanes;                                                 // [8]
+    const int lane = threadIdx.x % wave, warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
+    const bool active = warp < M;
+    const bool decoding = a.known == nullptr;
+    int row = 0;
+    if (active)
+    {
+        row = a.row_base[warp] + a.step * a.step_stride + a.book;
+    }
+    __syncthreads(); // the previous job's readers of LDS are done; `state` is current
+    uint32_t byte = 0;
+    const unsigned long long base_offset = decoding ? state->offset : 0;
+    if (decoding && threadIdx.x < window && base_offset + threadIdx.x < a.payload_bytes)
+    {
+        byte = a.payload[base_offset + threadIdx.x];
+    }
+    if (active)
+    {
+        uint16_t v[16];
+        await_tiles(a.logits, std::size_t(warp) * 1024, 1024, x);
+        take_row<16>(a.logits, std::size_t(warp) * 1024 + lane * 16, x, v);
+        if (lane == 0)
+        {
+            rows[warp] = row;
+        }
+        float maximum = -__builtin_inff();
+        bool finite = true;
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+        {
+            const float value = bf16_to_float(v[k]);
+            finite = finite && is_finite(value);
+            maximum = maximum < value ? value : maximum;
+        }
+        if (!finite)
+        {
+            error[0] = 1u;
+        }
+        maximum = group_max<wave>(maximum);
+        float e[16], leaves_sum[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+        {
+            e[k] = original_exp(bf16_to_float(v[k]) - maximum);
+            leaves_sum[k] = e[k];
+        }
+        const float total = row_sum<16>(leaves_sum);
+        const float reciprocal = 1.0f / total;
+        float prob[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+        {
+            v[k] = float_to_bf16(e[k] * reciprocal);
+            prob[k] = bf16_to_float(v[k]);
+        }
+        store_row<16>(leaves + warp * 1024 + lane * 16, v);
+        if (a.distributions)
+        {
+            store_row<16>(a.distributions + std::size_t(row) * 1024 + lane * 16, v);
+        }
+        if (decoding)
+        {
+            const bool ok = build_masses(prob, lane, nodes + warp * 1024);
+            if (lane == 0)
+            {
+                valid[warp] = ok;
+            }
+        }
+    }
+    if (threadIdx.x < window)
+    {
+        bytes[threadIdx.x] = uint8_t(byte);
+    }
+    __syncthreads();
+    if (threadIdx.x != 0)
+    {
+        return;
+    }
+    DecoderState s = decoding ? *state : DecoderState{};
+    for (int w = 0; w < M; ++w)
+    {
+        const int r = rows[w];
+        int token;
+        if (!decoding)
+        {
+            token = a.known[r];
+        }
+        else
+        {
+            if (!valid[w])
+            {
+                s.failed = 1;
+            }
+            int base = 0, left_count = 1024;
+            float mass = 1.0f;
+            const float* node = nodes + w * 1024;
+            while (left_count > 1 && !s.failed)
+            {
+                const int half = left_count / 2;
+                const float left = half == 1 ? flush(bf16_to_float(leaves[w * 1024 + base])) : node[1024 / half + base / half];
+                const uint16_t p0 = q15(left, mass);
+                const uint32_t range0 = uint32_t((uint64_t(s.range) * p0) >> 15);
+                if (s.code >= range0)
+                {
+                    s.code -= range0;
+                    s.range -= range0;
+                    base += half;
+                    left_count -= half;
+                    mass = flush(flush(mass) - flush(left));
+                }
+                else
+                {
+                    s.range = range0;
+                    left_count = half;
+                    mass = left;
+                }
+                while (s.range < 0xff01u)
+                {
+                    s.range <<= 8;
+                    const unsigned long long at = s.offset - base_offset;
+                    const uint32_t next =
+                        s.offset < a.payload_bytes ? (at < window ? bytes[at] : a.payload[s.offset]) : 0u;
+                    s.offset += s.offset < a.payload_bytes ? 1 : 0;
+                    s.code = (s.code << 8) + next;
+                }
+                if (!(s.code < s.range))
+                {
+                    s.failed = 1;
+                }
+            }
+            token = base;
+        }
+        a.current[std::size_t(w) * a.books + a.book] = uint16_t(token);
+        a.tokens[r] = uint16_t(token);
+        publish(a.token_words, w, uint32_t(token), x.epoch);
+    }
+    if (decoding)
+    {
+        *state = s;
+    }
+}
+
+// ------------------------------------------------------------------ the step
+
+// V* = K/64 of the width, FFN and latent rows; HW the head width.
+template <int VW, int VF, int VL, int HW> constexpr int frame_lds()
+{
+    return std::max({projection_lds<VW>(), projection_lds<VF>(), projection_lds<VL>(), attend_lds<HW>(), draw_lds});
+}
+
+template <int VW, int VF, int VL, int HW>
+__global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t lds[frame_lds<VW, VF, VL, HW>()];
+    __shared__ DecoderState decoder;
+    const Exchange x{a.epoch, a.abort};
+    const Words L(a.width, a.ffn, a.latent, a.alphabet, a.books, a.temporal_layers, a.codebook_layers);
+    word* const words = reinterpret_cast<word*>(a.words);
+    const FrameModel& model = a.model;
+    const int M = a.lanes, G = int(gridDim.x), me = int(blockIdx.x);
+    const int TL = a.temporal_layers, CL = a.codebook_layers, C = a.books, width = a.width;
+    const int sampler = 0;
+    if (me == sampler && threadIdx.x == 0 && a.known == nullptr)
+    {
+        decoder = *a.state;
+    }
+    // Workgroup 0 only samples. Every other workgroup runs one kind of job
+    // (one function, so its code stays in the instruction cache), for every
+    // layer and book: each kind owns a contiguous group of workgroups sized to
+    // its tiles (scaled down if they do not all fit), tile t of a job going to
+    // member t mod size. Consecutive jobs therefore run on different
+    // workgroups, and each workgroup loads its next job's weights long before
+    // that job's inputs exist.
+    enum Kind
+    {
+        embed,
+        qkv,
+        attend,
+        out,
+        up,
+        down,
+        condition,
+        prefix,
+        head,
+        kinds
+    };
+    const int kind_tiles[kinds] = {width / tile_rows, 3 * width / tile_rows, M * a.heads, width / tile_rows,
+                                   a.ffn / tile_rows, width / tile_rows, 1, width / tile_rows,
+                                   a.alphabet / tile_rows};
+    int group_size[kinds], group_base[kinds];
+    {
+        const int workers = G - 1;
+        int total = 0;
+        for (int k = 0; k < kinds; ++k)
+        {
+            total += kind_tiles[k];
+        }
+        int base = 1;
+        for (int k = 0; k < kinds; ++k)
+        {
+            group_size[k] = total <= workers ? kind_tiles[k] : max(1, kind_tiles[k] * (workers - kinds) / total);
+            group_base[k] = base;
+            base += group_size[k];
+        }
+    }
+    // This workgroup's first tile of a job of `kind` (>= any tile count if none).
+    const auto first_tile = [&](int kind)
+    {
+        const int member = me - group_base[kind];
+        return member >= 0 && member < group_size[kind] ? member : G * max_lanes * 64;
+    };
+    const auto linear = [&](bool temporal, int layer, int op) -> const DeviceLinear&
+    { return model.linears[(temporal ? 0 : 4 * TL) + 4 * layer + op]; };
+    const auto norm = [&](bool temporal, int layer, bool mlp) { return (temporal ? 0 : 2 * TL + 1) + 2 * layer + (mlp ? 1 : 0); };
+    const int final_temporal = 2 * TL, final_codebook = 2 * TL + 1 + 2 * CL;
+    const DeviceLinear& temporal_projection = model.linears[4 * (TL + CL)];
+    const DeviceLinear& codebook_projection = model.linears[4 * (TL + CL) + 1];
+    const DeviceLinear& output_projection = model.linears[4 * (TL + CL) + 2];
+
+    // One stack layer; `x_of`... words of the layer's input, qkv, attention,
+    // mid residual, hidden and output.
+    const auto run_layer = [&](bool temporal, int layer, std::size_t in, std::size_t qkv, std::size_t att,
+                               std::size_t mid, std::size_t hid, std::size_t output, const Attend& attention)
+    {
+        {
+            Projection p;
+            p.w = linear(temporal, layer, 0);
+            p.x = words + in;
+            p.gain = model.gain[norm(temporal, layer, false)];
+            p.beta = model.bias[norm(temporal, layer, false)];
+            p.y = words + qkv;
+            p.width = width;
+            p.head_width = a.head_width;
+            if (temporal)
+            {
+                p.keys = a.keys + std::size_t(layer) * a.extent * width;
+                p.values = a.values + std::size_t(layer) * a.extent * width;
+                p.lane_stride = a.lane_stride;
+                p.position = a.position;
+                p.rotations = model.rotations;
+            }
+            for (int t = first_tile(Kind::qkv); t < int(p.w.N) / tile_rows; t += group_size[Kind::qkv])
+            {
+                project_tile<VW, In::words_norm, Out::qkv>(p, M, t, x, a.error, lds);
+            }
+        }
+        for (int t = first_tile(Kind::attend); t < M * a.heads; t += group_size[Kind::attend])
+        {
+            attend_item<HW>(attention, t, x, lds);
+        }
+        {
+            Projection p;
+            p.w = linear(temporal, layer, 1);
+            p.x = words + att;
+            p.residual = words + in;
+            p.y = words + mid;
+            for (int t = first_tile(Kind::out); t < int(p.w.N) / tile_rows; t += group_size[Kind::out])
+            {
+                project_tile<VW, In::words, Out::residual_words>(p, M, t, x, a.error, lds);
+            }
+        }
+        {
+            Projection p;
+            p.w = linear(temporal, layer, 2);
+            p.x = words + mid;
+            p.gain = model.gain[norm(temporal, layer, true)];
+            p.beta = model.bias[norm(temporal, layer, true)];
+            p.y = words + hid;
+            for (int t = first_tile(Kind::up); t < int(p.w.N) / tile_rows; t += group_size[Kind::up])
+            {
+                project_tile<VW, In::words_norm, Out::gelu>(p, M, t, x, a.error, lds);
+            }
+        }
+        {
+            Projection p;
+            p.w = linear(temporal, layer, 3);
+            p.x = words + hid;
+            p.residual = words + mid;
+            p.y = words + output;
+            for (int t = first_tile(Kind::down); t < int(p.w.N) / tile_rows; t += group_size[Kind::down])
+            {
+                project_tile<VF, In::words, Out::residual_words>(p, M, t, x, a.error, lds);
+            }
+        }
+    };
+
+    // Temporal stack: feedback embeddings of the previous frame, then layers.
+    {
+        Projection p;
+        p.w = temporal_projection;
+        p.embeddings = model.embeddings;
+        p.alphabet = a.alphabet;
+        p.books = C;
+        p.tokens = a.current;
+        p.token_stride = C;
+        p.y = words + L.t_x(0);
+        for (int t = first_tile(Kind::embed); t < int(p.w.N) / tile_rows; t += group_size[Kind::embed])
+        {
+            project_tile<VL, In::embed_sum, Out::plain>(p, M, t, x, a.error, lds);
+        }
+    }
+    for (int l = 0; l < TL; ++l)
+    {
+        Attend at;
+        at.heads = a.heads;
+        at.width = width;
+        at.scale = a.scale;
+        at.time = a.position + 1;
+        at.keys = a.keys + std::size_t(l) * a.extent * width;
+        at.values = a.values + std::size_t(l) * a.extent * width;
+        at.lane_stride = a.lane_stride;
+        at.qkv = words + L.t_qkv(l);
+        at.out = words + L.t_att(l);
+        run_layer(true, l, L.t_x(l), L.t_qkv(l), L.t_att(l), L.t_mid(l), L.t_hid(l), L.t_x(l + 1), at);
+    }
+    // Book 0's input.
+    if (first_tile(Kind::condition) == 0)
+    {
+        condition_rows<VW>(words + L.t_x(TL), model.gain[final_temporal], model.bias[final_temporal], model.positions,
+                           words + L.c_x(0, 0), M, x);
+    }
+    for (int b = 0; b < C; ++b)
+    {
+        if (b > 0)
+        {
+            Projection p;
+            p.w = codebook_projection;
+            p.embeddings = model.embeddings;
+            p.alphabet = a.alphabet;
+            p.book = b - 1;
+            p.token_words = words + L.c_token(b - 1, CL);
+            p.prefix_in = b > 1 ? words + L.c_prefix(b - 1) : nullptr;
+            p.prefix_out = words + L.c_prefix(b);
+            p.residual_row = model.positions + std::size_t(b) * width;
+            p.y = words + L.c_x(b, 0);
+            for (int t = first_tile(Kind::prefix); t < int(p.w.N) / tile_rows; t += group_size[Kind::prefix])
+            {
+                project_tile<VL, In::embed_accumulate, Out::residual_row>(p, M, t, x, a.error, lds);
+            }
+        }
+        for (int l = 0; l < CL; ++l)
+        {
+            Attend at;
+            at.heads = a.heads;
+            at.width = width;
+            at.scale = a.scale;
+            at.time = b + 1;
+            at.qkv = words + L.c_qkv(0, l);
+            at.book_words = L.book;
+            at.out = words + L.c_att(b, l);
+            run_layer(false, l, L.c_x(b, l), L.c_qkv(b, l), L.c_att(b, l), L.c_mid(b, l), L.c_hid(b, l),
+                      L.c_x(b, l + 1), at);
+        }
+        {
+            Projection p;
+            p.w = output_projection;
+            p.x = words + L.c_x(b, CL);
+            p.gain = model.gain[final_codebook];
+            p.beta = model.bias[final_codebook];
+            p.y = words + L.c_logits(b, CL);
+            for (int t = first_tile(Kind::head); t < int(p.w.N) / tile_rows; t += group_size[Kind::head])
+            {
+                project_tile<VW, In::words_norm, Out::plain>(p, M, t, x, a.error, lds);
+            }
+        }
+        if (me == sampler)
+        {
+            Draw d;
+            d.book = b;
+            d.books = C;
+            d.logits = words + L.c_logits(b, CL);
+            d.token_words = words + L.c_token(b, CL);
+            d.current = a.current;
+            d.tokens = a.tokens;
+            d.row_base = a.row_base;
+            d.step = a.step;
+            d.step_stride = a.step_stride;
+            d.known = a.known;
+            d.distributions = a.distributions;
+            d.payload = a.payload;
+            d.payload_bytes = a.payload_bytes;
+            draw_tokens(d, M, &decoder, x, a.error, lds);
+        }
+    }
+    if (me == sampler && a.known == nullptr)
+    {
+        __syncthreads();
+        if (threadIdx.x == 0)
+        {
+            *a.state = decoder;
+            if (decoder.failed)
+            {
+                a.error[1] = 1u;
+            }
+        }
+    }
+}
+
+template <int VW, int VF, int VL, int HW> void launch_frame(const FrameArgs& a, hipStream_t stream)
+{
+    static int grid = 0;
+    if (!grid)
+    {
+        int device = 0, units = 0, per_unit = 0;
+        check_hip(hipGetDevice(&device), "hipGetDevice");
+        check_hip(hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
+        check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_unit, frame_kernel<VW, VF, VL, HW>,
+                                                               frame_threads, 0),
+                  "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+        require(units > 0 && per_unit > 0, "frame step: kernel does not fit a compute unit");
+        grid = std::min(128, units * per_unit);
+    }
+    FrameArgs args = a;
+    void* params[] = {&args};
+    check_hip(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(frame_kernel<VW, VF, VL, HW>), dim3(grid),
+                                         dim3(frame_threads), params, 0, stream),
+              "frame step launch");
+}
+} // namespace
+
+bool frame_supported(int width, int heads, int head_width, int ffn, int latent, int alphabet, int lanes)
+{
+    const bool reference = width == 512 && head_width == 128 && ffn == 2048 && latent == 1024;
+    const bool wide = width == 1024 && head_width == 64 && ffn == 4096 && latent == 1024;
+    return (reference || wide) && heads * head_width == width && alphabet == 1024 && lanes >= 1 &&
+           lanes <= max_lanes;
+}
+
+std::size_t frame_exchange_words(int width, int ffn, int latent, int alphabet, int books, int temporal_layers,
+                                 int codebook_layers)
+{
+    return Words(width, ffn, latent, alphabet, books, temporal_layers, codebook_layers).total;
+}
+
+void frame_step(const FrameArgs& a, hipStream_t stream)
+{
+    require(frame_supported(a.width, a.heads, a.head_width, a.ffn, a.latent, a.alphabet, a.lanes),
+            "frame step: unsupported geometry");
+    require(a.position >= 0 && a.position < a.extent && a.extent <= max_blocks * 64, "frame step: position");
+    require(a.books >= 1 && a.books <= max_books && a.temporal_layers >= 1 && a.codebook_layers >= 1,
+            "frame step: layers");
+    require(a.words && a.abort && a.error && a.current && a.tokens && a.row_base && a.epoch != 0,
+            "frame step: arguments");
+    require(a.known || (a.state && a.payload), "frame step: needs known tokens or a decoder");
+    if (a.width == 512)
+    {
+        launch_frame<8, 32, 16, 128>(a, stream);
+    }
+    else
+    {
+        launch_frame<16, 64, 16, 64>(a, stream);
+    }
+}
+} // namespace tsac_hip

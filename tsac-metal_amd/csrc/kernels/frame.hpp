@@ -1,0 +1,70 @@
+// One decode frame step (temporal stack, then every codebook with its range
+// decoding) in a single persistent launch.
+//
+// The step's ~280 dependent operations (projections, attention, sampling) run
+// as jobs of a fixed set of co-resident workgroups. Activations pass between
+// jobs through "exchange words": 8-byte words holding two BF16 values (or a
+// token) in the low half and the step's epoch in the high half, written and
+// polled with relaxed device-scope atomics. A consumer waits only for the words
+// it reads, so no device-wide barrier (and none of its cache write-back and
+// invalidation) is needed, and every workgroup issues its next job's weight
+// loads before it waits for that job's inputs.
+//
+// Key/value rows of earlier steps come from the temporal cache (written by
+// earlier launches); the current step's rows and the whole codebook stack come
+// from exchange words. Every wait is bounded: a stalled wait raises the abort
+// word, after which all waits return at once and the launch ends.
+#pragma once
+
+#include "decode.hpp"
+
+namespace tsac_hip
+{
+// Device-resident model tables for the frame kernel.
+struct FrameModel
+{
+    const DeviceLinear* linears = nullptr; // reference projection order
+    const uint16_t* const* gain = nullptr; // reference norm order
+    const uint16_t* const* bias = nullptr;
+    const uint16_t* positions = nullptr;  // [books][width]
+    const uint16_t* rotations = nullptr;  // [context][head_width]
+    const uint16_t* embeddings = nullptr; // [books][alphabet][latent]
+};
+
+struct FrameArgs
+{
+    FrameModel model;
+    int lanes = 0, books = 0, temporal_layers = 0, codebook_layers = 0;
+    int width = 0, heads = 0, head_width = 0, ffn = 0, latent = 0, alphabet = 0;
+    float scale = 0.0f;
+    // temporal cache: lane l, layer k, position p at l*lane_stride + (k*extent + p)*width
+    uint16_t* keys = nullptr;
+    uint16_t* values = nullptr;
+    long long lane_stride = 0;
+    int extent = 0;
+    int position = 0; // context position of this step
+    int step = 0;     // frame step index
+    // tokens
+    uint16_t* current = nullptr; // [lanes][books]: previous frame in, this frame out
+    const int* row_base = nullptr;
+    int step_stride = 0;
+    uint16_t* tokens = nullptr;
+    const uint16_t* known = nullptr;
+    uint16_t* distributions = nullptr;
+    DecoderState* state = nullptr;
+    const uint8_t* payload = nullptr;
+    unsigned long long payload_bytes = 0;
+    uint32_t* error = nullptr;
+    // exchange
+    unsigned long long* words = nullptr; // frame_exchange_words() words, zero before the first step
+    uint32_t epoch = 0;                  // nonzero, different for every launch over the same words
+    unsigned* abort = nullptr;           // zero before the first step; nonzero after a stalled wait
+};
+
+// Geometries the frame kernel is instantiated for, at 1..8 lanes.
+bool frame_supported(int width, int heads, int head_width, int ffn, int latent, int alphabet, int lanes);
+// Exchange words one step needs.
+std::size_t frame_exchange_words(int width, int ffn, int latent, int alphabet, int books, int temporal_layers,
+                                 int codebook_layers);
+void frame_step(const FrameArgs& args, hipStream_t stream);
+} // namespace tsac_hip

@@ -33,9 +33,9 @@ inline void check_hip(hipError_t status, const char* what)
     }
 }
 
-// Error words written by kernels (plain stores of fixed values, no atomics):
-// word 0 = a BF8L, softmax or categorical input was not finite; word 1 is reserved
-// for range-decoder state.
+// Error words written by kernels (plain stores of fixed values):
+// word 0 = a BF8L, softmax or categorical input was not finite; word 1 = the
+// range decoder failed; word 2 = a frame-step wait stalled (see frame.hpp).
 constexpr uint32_t error_nonfinite = 1u;
 
 // ---- quantisation (BF8L, src/scalar/probability.cpp:16-40) ------------------
