@@ -267,6 +267,55 @@ def test_layer_norm_matches_oracle(torch, native, oracle):
         assert np.array_equal(host(out), expected)
 
 
+def _tiny_rows(rng, width):
+    """Rows around the magnitudes where FTZ sums start to differ from plain sums:
+    values at and just below 2^-56, squares that are subnormal, sums that cancel
+    to subnormals, BF16 subnormals, signed zeros and the largest finite values."""
+    rows = []
+    for exponent in (-56, -57, -63, -64, -70, -100, -126, -130):
+        rows.append(bf16_bits((rng.standard_normal(width) * 2.0 ** exponent).astype(np.float32)))
+    mixed = bf16_bits(rng.standard_normal(width).astype(np.float32))
+    mixed[::3] = bf16_bits((rng.standard_normal(mixed[::3].size) * 1e-30).astype(np.float32))
+    rows.append(mixed)
+    boundary = np.where(rng.random(width) < 0.5, 0x2380, 0x237F).astype(np.uint16)
+    boundary |= (rng.random(width) < 0.5).astype(np.uint16) << 15
+    rows.append(boundary)
+    cancel = bf16_bits((rng.standard_normal(width) * 2.0 ** -120).astype(np.float32))
+    cancel[1::2] = cancel[0::2] ^ 0x8000  # pairs sum to signed zeros
+    cancel[-1] = 0x0003
+    rows.append(cancel)
+    rows.append(np.resize(np.array([0x0001, 0x8001, 0x007F, 0x807F, 0x0000, 0x8000], np.uint16), width))
+    rows.append(np.resize(np.array([0x7F7F, 0xFF7F, 0x0080, 0x8080], np.uint16), width))
+    return np.stack(rows)
+
+
+def test_layer_norm_small_magnitudes(torch, native, oracle):
+    rng = np.random.default_rng(15)
+    for width in (256, 512, 2048):
+        x = _tiny_rows(rng, width)
+        rows = x.shape[0]
+        g = bf16_bits((1 + 0.1 * rng.standard_normal(width)).astype(np.float32))
+        b = bf16_bits((0.1 * rng.standard_normal(width)).astype(np.float32))
+        out = empty(torch, (rows, width), torch.int16)
+        native.layer_norm(dev(torch, x), rows, width, dev(torch, g), dev(torch, b), out)
+        expected = np.stack([oracle.layer_norm(r, g, b) for r in x])
+        assert np.array_equal(host(out), expected)
+
+
+def test_bf8l_small_magnitudes(torch, native, oracle):
+    rng = np.random.default_rng(16)
+    for k in (256, 512, 2048):
+        x = _tiny_rows(rng, k)
+        rows = x.shape[0]
+        q = empty(torch, (rows, k), torch.int8)
+        s = empty(torch, (rows, k // 256), torch.float32)
+        native.bf8l(dev(torch, x), rows, k, q, s)
+        for r in range(rows):
+            eq, es = oracle.bf8l(bf16_float(x[r]))
+            assert np.array_equal(host(q, np.int8)[r], eq), r
+            assert np.array_equal(host(s, np.float32)[r], bf16_float(es)), r
+
+
 def test_softmax_matches_oracle(torch, native, oracle):
     rng = np.random.default_rng(6)
     for amplitude in (0.0, 1 / 32, 1.0, 40.0, 300.0):  # tests/metal_range.cpp:144

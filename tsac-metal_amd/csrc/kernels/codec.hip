@@ -176,12 +176,12 @@ __device__ __forceinline__ void build_tree(const uint16_t* row, int lane, Tree& 
     }
     t.local[14] = ftz_add(t.local[12], t.local[13]);
     float v = t.local[14];
-#pragma unroll
-    for (int level = 0; level < 6; ++level)
-    {
-        v = ftz_add(v, lane_xor(v, 1 << level));
-        t.wide[level] = v;
-    }
+    t.wide[0] = v = butterfly_ftz_add<1>(v);
+    t.wide[1] = v = butterfly_ftz_add<2>(v);
+    t.wide[2] = v = butterfly_ftz_add<4>(v);
+    t.wide[3] = v = butterfly_ftz_add<8>(v);
+    t.wide[4] = v = butterfly_ftz_add<16>(v);
+    t.wide[5] = v = butterfly_ftz_add<32>(v);
     t.valid = __all(valid);
     (void)leaf;
 }

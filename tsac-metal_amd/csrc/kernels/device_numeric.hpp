@@ -33,15 +33,21 @@ __device__ __forceinline__ float round_bf16(float x)
 }
 
 // Zero exponent -> signed zero (src/common/numeric/float_math.hpp:33-37).
+// Zeros map to themselves, so only subnormals (class mask 0x90) change.
 __device__ __forceinline__ float flush(float x)
 {
-    const uint32_t b = __float_as_uint(x);
-    return (b & 0x7f800000u) == 0 ? __uint_as_float(b & 0x80000000u) : x;
+    return __builtin_amdgcn_classf(x, 0x90) ? __uint_as_float(__float_as_uint(x) & 0x80000000u) : x;
 }
 
 __device__ __forceinline__ float ftz_add(float x, float y)
 {
     return flush(flush(x) + flush(y));
+}
+
+// ftz_add for operands that are already flushed (flush is idempotent).
+__device__ __forceinline__ float flushed_add(float x, float y)
+{
+    return flush(x + y);
 }
 
 __device__ __forceinline__ float ftz_multiply(float x, float y)
@@ -97,65 +103,169 @@ __device__ __forceinline__ uint16_t gelu_bf16(uint16_t bits)
 }
 
 // ---- cross-lane helpers (64-wide wavefronts) -----------------------------------
+// Every helper here must be called by a whole wave (all 64 lanes active).
 
-__device__ __forceinline__ float lane_xor(float v, int mask)
+// The value of lane (this lane ^ 1), through DPP rather than LDS.
+__device__ __forceinline__ uint32_t lane_swap1(uint32_t v)
 {
-    return __shfl_xor(v, mask, wave);
+    return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xb1, 0xf, 0xf, false)); // quad_perm:[1,0,3,2]
 }
 
-__device__ __forceinline__ int lane_xor(int v, int mask)
+// One level of a butterfly: returns combine(a, b) where {a, b} are this lane's
+// value and that of lane (this lane ^ stride), in either order, so `combine`
+// must be commutative. Precondition: every aligned group of `stride` lanes
+// holds one value, as at each level of a butterfly started from stride 1.
+// Then any lane of the neighbouring group is as good as lane ^ stride, which
+// lets the mirror DPP patterns stand in for xor 4 and 8 inside a row of 16
+// lanes, and gfx950's permlane swaps exchange rows (16) and half-waves (32).
+// No level passes through LDS.
+template <int stride, class Combine> __device__ __forceinline__ uint32_t butterfly(uint32_t v, Combine combine)
 {
-    return __shfl_xor(v, mask, wave);
+    static_assert(stride >= 1 && stride <= 32 && (stride & (stride - 1)) == 0, "power of two below 64");
+    const int x = int(v);
+    if constexpr (stride == 1)
+    {
+        return combine(v, lane_swap1(v));
+    }
+    else if constexpr (stride == 2)
+    {
+        return combine(v, uint32_t(__builtin_amdgcn_mov_dpp(x, 0x4e, 0xf, 0xf, false))); // quad_perm:[2,3,0,1]
+    }
+    else if constexpr (stride == 4)
+    {
+        return combine(v, uint32_t(__builtin_amdgcn_mov_dpp(x, 0x141, 0xf, 0xf, false))); // row_half_mirror
+    }
+    else if constexpr (stride == 8)
+    {
+        return combine(v, uint32_t(__builtin_amdgcn_mov_dpp(x, 0x140, 0xf, 0xf, false))); // row_mirror
+    }
+    else if constexpr (stride == 16)
+    {
+        // Rows (r0, r1, r2, r3) in both operands -> (r0, r0, r2, r2) and (r1, r1, r3, r3).
+        const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return combine(uint32_t(p[0]), uint32_t(p[1]));
+    }
+    else
+    {
+        // Halves (h0, h1) in both operands -> (h0, h0) and (h1, h1).
+        const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return combine(uint32_t(p[0]), uint32_t(p[1]));
+    }
 }
 
-// Balanced adjacent-pair FTZ tree across `lanes` consecutive lanes (power of two).
+// One butterfly level of FTZ sums; v must already be flushed (as every
+// ftz_add result is).
+template <int stride> __device__ __forceinline__ float butterfly_ftz_add(float v)
+{
+    return __uint_as_float(butterfly<stride>(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+        return __float_as_uint(flushed_add(__uint_as_float(a), __uint_as_float(b)));
+    }));
+}
+
+template <int stride> __device__ __forceinline__ float butterfly_add(float v)
+{
+    return __uint_as_float(butterfly<stride>(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+        return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+    }));
+}
+
+// Balanced adjacent-pair tree across `lanes` consecutive lanes (power of two).
 // Lane pairs at strides 1, 2, 4, ... combine neighbouring subtrees, so with each
 // lane holding the tree of its own consecutive leaves the result is the
 // reference's pair tree over all leaves (src/format/categorical.cpp:17-30).
-// Every lane of the group receives the sum.
+// IEEE addition is commutative, so the order inside a pair is immaterial.
+// Every lane of the group receives the sum. Ftz selects FTZ additions; plain
+// additions are for operands whose sums provably never meet a subnormal.
+template <int lanes, bool Ftz, int stride> __device__ __forceinline__ float tree_levels(float v)
+{
+    if constexpr (stride >= lanes)
+    {
+        return v;
+    }
+    else if constexpr (Ftz)
+    {
+        return tree_levels<lanes, Ftz, 2 * stride>(butterfly_ftz_add<stride>(v));
+    }
+    else
+    {
+        return tree_levels<lanes, Ftz, 2 * stride>(butterfly_add<stride>(v));
+    }
+}
+
 template <int lanes> __device__ __forceinline__ float tree_sum(float v)
 {
-#pragma unroll
-    for (int stride = 1; stride < lanes; stride *= 2)
-    {
-        v = ftz_add(v, lane_xor(v, stride));
-    }
-    return v;
+    return tree_levels<lanes, true, 1>(flush(v));
 }
 
-template <int lanes> __device__ __forceinline__ float group_max(float v)
+template <int lanes> __device__ __forceinline__ float plain_tree_sum(float v)
 {
-#pragma unroll
-    for (int stride = 1; stride < lanes; stride *= 2)
-    {
-        const float o = lane_xor(v, stride);
-        v = v < o ? o : v;
-    }
-    return v;
+    return tree_levels<lanes, false, 1>(v);
 }
 
-template <int lanes> __device__ __forceinline__ int group_isum(int v)
+// Largest value across the group. For values that compare equal but differ in
+// bits (+0 and -0) a lane may receive either.
+template <int lanes, int stride = 1> __device__ __forceinline__ float group_max(float v)
 {
-#pragma unroll
-    for (int stride = 1; stride < lanes; stride *= 2)
+    if constexpr (stride >= lanes)
     {
-        v += lane_xor(v, stride);
+        return v;
     }
-    return v;
+    else
+    {
+        const uint32_t m = butterfly<stride>(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+            return __uint_as_float(a) < __uint_as_float(b) ? b : a;
+        });
+        return group_max<lanes, 2 * stride>(__uint_as_float(m));
+    }
 }
 
-// Pair tree over `count` consecutive registers (count a power of two).
-template <int count> __device__ __forceinline__ float register_tree(float (&v)[count])
+template <int lanes, int stride = 1> __device__ __forceinline__ int group_isum(int v)
 {
+    if constexpr (stride >= lanes)
+    {
+        return v;
+    }
+    else
+    {
+        const uint32_t s = butterfly<stride>(uint32_t(v), [](uint32_t a, uint32_t b) { return a + b; });
+        return group_isum<lanes, 2 * stride>(int(s));
+    }
+}
+
+// Pair tree over `count` consecutive registers (count a power of two), FTZ or
+// plain as for tree_levels. The FTZ tree's result is flushed.
+template <int count, bool Ftz = true> __device__ __forceinline__ float register_tree(float (&v)[count])
+{
+    if constexpr (Ftz)
+    {
+#pragma unroll
+        for (int i = 0; i < count; ++i)
+        {
+            v[i] = flush(v[i]);
+        }
+    }
 #pragma unroll
     for (int width = count; width > 1; width /= 2)
     {
 #pragma unroll
         for (int i = 0; i < width / 2; ++i)
         {
-            v[i] = ftz_add(v[2 * i], v[2 * i + 1]);
+            v[i] = Ftz ? flushed_add(v[2 * i], v[2 * i + 1]) : v[2 * i] + v[2 * i + 1];
         }
     }
     return v[0];
+}
+
+// Unsigned maximum across `lanes` consecutive lanes (power of two).
+template <int lanes, int stride = 1> __device__ __forceinline__ uint32_t group_umax(uint32_t v)
+{
+    if constexpr (stride >= lanes)
+    {
+        return v;
+    }
+    else
+    {
+        return group_umax<lanes, 2 * stride>(butterfly<stride>(v, [](uint32_t a, uint32_t b) { return a < b ? b : a; }));
+    }
 }
 } // namespace tsac_hip

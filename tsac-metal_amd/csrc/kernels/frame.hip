@@ -921,7 +921,7 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
     else
     {
         const uint32_t mine = float_to_bf16(numerator[0] * reciprocal);
-        const uint32_t other = uint32_t(__shfl_xor(int(mine), 1));
+        const uint32_t other = lane_swap1(mine);
         if ((lane & 1) == 0)
         {
             publish(a.out, at / 2, mine | (other << 16), x.epoch);

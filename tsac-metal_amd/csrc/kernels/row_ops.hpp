@@ -76,7 +76,32 @@ template <int V> __device__ __forceinline__ void store_row(uint16_t* p, const ui
 template <int V> __device__ __forceinline__ float row_sum(float (&v)[V])
 {
     static_assert(V >= 2, "rows of 64 or fewer values use the single-block tree");
-    return ftz_add(0.0f, tree_sum<wave>(register_tree(v)));
+    return flushed_add(0.0f, tree_sum<wave>(register_tree(v)));
+}
+
+// row_sum with plain additions, for leaves whose sums never meet a subnormal
+// (see sums_stay_normal); then every flush of the FTZ tree is an identity and
+// the two trees agree bit for bit.
+template <int V> __device__ __forceinline__ float plain_row_sum(float (&v)[V])
+{
+    return 0.0f + plain_tree_sum<wave>(register_tree<V, false>(v));
+}
+
+// True (for the whole wave) when every value of the row is zero or at least
+// 2^-56 in magnitude (BF16 magnitude bits 0 or >= 0x2380). Such a value is a
+// multiple of 2^-63 and its square, exact in fp32, a multiple of 2^-126. Sums
+// of multiples of 2^-k stay multiples of 2^-k after fp32 rounding, so every
+// partial sum of values or of squares is zero or at least 2^-126: no leaf and
+// no partial sum is subnormal, and FTZ and plain pair trees agree.
+template <int V> __device__ __forceinline__ bool sums_stay_normal(const uint16_t (&v)[V])
+{
+    bool tiny = false;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+    {
+        tiny = tiny || (uint32_t(v[i]) & 0x7fffu) - 1u < 0x237fu;
+    }
+    return !__any(tiny);
 }
 
 // BF8L quantisation of one row held V-per-lane (src/scalar/probability.cpp:20-38):
@@ -87,26 +112,31 @@ __device__ __forceinline__ uint16_t bf8l_pack(const uint16_t (&v)[V], uint32_t (
                                               uint32_t* error)
 {
     constexpr int lanes_per_block = 256 / V;
-    float values[V];
-    float maximum = 0.0f;
-    bool finite = true;
+    // Largest magnitude as BF16 bits: on non-negative BF16 patterns integer
+    // order is numeric order, and patterns from 0x7f80 up are not finite.
+    uint32_t top = 0;
 #pragma unroll
     for (int i = 0; i < V; ++i)
     {
-        values[i] = bf16_to_float(v[i]);
-        finite = finite && is_finite(values[i]);
-        const float a = __builtin_fabsf(flush(values[i]));
-        maximum = maximum < a ? a : maximum;
+        const uint32_t magnitude = uint32_t(v[i]) & 0x7fffu;
+        top = top < magnitude ? magnitude : top;
     }
-    if (!finite)
+    top = group_umax<lanes_per_block>(top);
+    if (top >= 0x7f80u)
     {
         error[0] = 1u;
     }
-    maximum = group_max<lanes_per_block>(maximum);
-    float s = ftz_divide(maximum, 127.0f);
+    // The reference takes the largest flushed magnitude, which is the flushed
+    // largest magnitude.
+    const float maximum = top < 0x80u ? 0.0f : bf16_to_float(uint16_t(top));
+    // ftz_divide(maximum, 127): a subnormal quotient would be flushed to +0,
+    // and +0 and every subnormal alike are raised to the 1e-35 floor.
+    float s = maximum / 127.0f;
     s = s < 1e-35f ? 1e-35f : s;
     const uint16_t scale = float_to_bf16(s);
-    const float reciprocal = ftz_divide(1.0f, bf16_to_float(scale));
+    // 1e-35 <= scale <= 2^128/127: operand and quotient are normal, so the
+    // flushes of ftz_divide(1, scale) are identities.
+    const float reciprocal = 1.0f / bf16_to_float(scale);
 #pragma unroll
     for (int i = 0; i < (V + 3) / 4; ++i)
     {
@@ -115,8 +145,12 @@ __device__ __forceinline__ uint16_t bf8l_pack(const uint16_t (&v)[V], uint32_t (
 #pragma unroll
     for (int i = 0; i < V; ++i)
     {
-        float r = __builtin_rintf(ftz_multiply(values[i], reciprocal));
-        r = r < -128.0f ? -128.0f : (127.0f < r ? 127.0f : r);
+        // rint(ftz_multiply(value, reciprocal)): with reciprocal <= 2^117 a
+        // subnormal value gives a product below 2^-9 and a subnormal product
+        // is below 2^-126, so with or without the flushes these round to a
+        // signed zero and store 0.
+        float r = __builtin_rintf(bf16_to_float(v[i]) * reciprocal);
+        r = __builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
         packed[i / 4] |= (uint32_t(int(r)) & 0xffu) << (8 * (i % 4));
     }
     return scale;
@@ -198,8 +232,17 @@ __device__ __forceinline__ void layer_norm_values(uint16_t (&v)[V], const uint16
         squares[i] = x[i] * x[i];
     }
     constexpr int width = wave * V;
-    const float sum = row_sum<V>(values);
-    const float sum_squares = row_sum<V>(squares);
+    float sum, sum_squares;
+    if (sums_stay_normal<V>(v))
+    {
+        sum = plain_row_sum<V>(values);
+        sum_squares = plain_row_sum<V>(squares);
+    }
+    else
+    {
+        sum = row_sum<V>(values);
+        sum_squares = row_sum<V>(squares);
+    }
     const float reciprocal = 1.0f / float(width);
     const float mean = sum * reciprocal;
     float variance = __builtin_fmaf(sum_squares, reciprocal, 0.0f);

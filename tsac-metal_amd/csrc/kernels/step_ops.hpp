@@ -75,16 +75,26 @@ __device__ __forceinline__ bool build_masses(const float (&leaf)[16], int lane, 
     }
     float v = ftz_add(level[0], level[1]);
     nodes[64 + lane] = v;
-#pragma unroll
-    for (int l = 0; l < 6; ++l)
-    {
-        v = ftz_add(v, lane_xor(v, 1 << l));
+    // Level l spans 32 << l leaves (2 << l lanes); one lane per node stores it.
+    const auto store = [&](int l) {
         const int size = 32 << l;
         if ((lane * 16) % size == 0)
         {
             nodes[1024 / size + lane * 16 / size] = v;
         }
-    }
+    };
+    v = butterfly_ftz_add<1>(v);
+    store(0);
+    v = butterfly_ftz_add<2>(v);
+    store(1);
+    v = butterfly_ftz_add<4>(v);
+    store(2);
+    v = butterfly_ftz_add<8>(v);
+    store(3);
+    v = butterfly_ftz_add<16>(v);
+    store(4);
+    v = butterfly_ftz_add<32>(v);
+    store(5);
     return __all(valid);
 }
 
