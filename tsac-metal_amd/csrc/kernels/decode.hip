@@ -457,15 +457,16 @@ constexpr int sample_waves = 8;
 // 10 decisions x 2 bytes, so 256 bytes always cover a launch.
 constexpr int window = 256;
 
-// Up to `sample_waves` lanes: one wavefront each for the softmax and masses,
-// then thread 0 decodes the lanes' symbols in stream order.
+// Up to `sample_waves` lanes: one wavefront each for the softmax, masses and
+// top decisions, then wave 0 decodes the lanes' symbols in stream order.
 __global__ __launch_bounds__(sample_waves * wave) void sample_kernel(const Sample a)
 {
     __shared__ float nodes[sample_waves][1024];
     __shared__ uint16_t leaves[sample_waves][1024];
+    __shared__ uint16_t top[sample_waves][64];
     __shared__ int valid[sample_waves];
     __shared__ int rows[sample_waves];
-    __shared__ uint8_t bytes[window];
+    __shared__ __attribute__((aligned(16))) uint8_t bytes[window];
     __shared__ DecoderState shared_state;
     const int lane = threadIdx.x % wave, warp = threadIdx.x / wave;
     const int step = a.step ? *a.step : a.fixed_step;
@@ -530,14 +531,16 @@ __global__ __launch_bounds__(sample_waves * wave) void sample_kernel(const Sampl
             v[k] = float_to_bf16(e[k] * reciprocal);
             p[k] = bf16_to_float(v[k]);
         }
-        store_row<16>(&leaves[warp][lane * 16], v);
         if (a.distributions)
         {
             store_row<16>(a.distributions + std::size_t(row) * 1024 + lane * 16, v);
         }
         if (a.state)
         {
+            store_row<16>(&leaves[warp][lane * 16], v);
             const bool ok = build_masses(p, lane, nodes[warp]);
+            wait_shared_memory();
+            build_top_decisions(lane, Masses{nodes[warp], leaves[warp]}, top[warp]);
             if (lane == 0)
             {
                 valid[warp] = ok;
@@ -549,14 +552,16 @@ __global__ __launch_bounds__(sample_waves * wave) void sample_kernel(const Sampl
         bytes[threadIdx.x] = uint8_t(byte);
     }
     __syncthreads();
-    if (threadIdx.x != 0)
+    if (warp != 0)
     {
         return;
     }
+    // Wave 0 decodes the lanes' symbols in stream order.
     DecoderState s = a.state ? shared_state : DecoderState{};
+    const ByteWindow staged{bytes, window, base_offset, a.payload, a.payload_bytes};
     for (int w = 0; w < a.lanes; ++w)
     {
-        const int r = rows[w];
+        const int r = __builtin_amdgcn_readfirstlane(rows[w]);
         int token;
         if (a.known)
         {
@@ -564,55 +569,19 @@ __global__ __launch_bounds__(sample_waves * wave) void sample_kernel(const Sampl
         }
         else
         {
-            // decode_categorical + RangeDecoder::get.
-            if (!valid[w])
+            if (!__builtin_amdgcn_readfirstlane(valid[w]))
             {
                 s.failed = 1;
             }
-            int base = 0, left_count = 1024;
-            float mass = 1.0f;
-            while (left_count > 1 && !s.failed)
-            {
-                const int half = left_count / 2;
-                const float left = half == 1 ? flush(bf16_to_float(leaves[w][base]))
-                                             : nodes[w][1024 / half + base / half];
-                const uint16_t p0 = q15(left, mass);
-                const uint32_t range0 = uint32_t((uint64_t(s.range) * p0) >> 15);
-                if (s.code >= range0)
-                {
-                    s.code -= range0;
-                    s.range -= range0;
-                    base += half;
-                    left_count -= half;
-                    mass = flush(flush(mass) - flush(left));
-                }
-                else
-                {
-                    s.range = range0;
-                    left_count = half;
-                    mass = left;
-                }
-                while (s.range < 0xff01u)
-                {
-                    s.range <<= 8;
-                    const unsigned long long at = s.offset - base_offset;
-                    const uint32_t next = s.offset < a.payload_bytes
-                                              ? (at < window ? bytes[at] : a.payload[s.offset])
-                                              : 0u;
-                    s.offset += s.offset < a.payload_bytes ? 1 : 0;
-                    s.code = (s.code << 8) + next;
-                }
-                if (!(s.code < s.range))
-                {
-                    s.failed = 1;
-                }
-            }
-            token = base;
+            token = decode_symbol(top[w], Masses{nodes[w], leaves[w]}, s, staged);
         }
-        a.current[std::size_t(w) * a.books + a.book] = uint16_t(token);
-        a.tokens[r] = uint16_t(token);
+        if (lane == 0)
+        {
+            a.current[std::size_t(w) * a.books + a.book] = uint16_t(token);
+            a.tokens[r] = uint16_t(token);
+        }
     }
-    if (a.state)
+    if (a.state && lane == 0)
     {
         *a.state = s;
         if (s.failed)

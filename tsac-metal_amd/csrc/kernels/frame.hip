@@ -167,85 +167,121 @@ __device__ __forceinline__ bool keep_polling(unsigned& spins, const Exchange& x)
 }
 
 // Payloads of N words, at address(i) for word i, once each carries the epoch.
-// Every word is requested before any is waited for; only words not yet
-// current are polled again.
+// Each poll requests all N words before it waits for any (a load under a
+// per-word branch would wait for its own reply, making a poll N round trips);
+// words already current keep their first value.
 template <int N, class Address>
 __device__ __forceinline__ void take_words(const Address& address, const Exchange& x, uint32_t (&out)[N])
 {
     static_assert(N <= 64, "one pending mask");
-    unsigned long long pending = 0;
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-    {
-        const word v = __hip_atomic_load(global(address(i)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        out[i] = uint32_t(v);
-        pending |= uint32_t(v >> 32) != x.epoch ? 1ull << i : 0ull;
-    }
+    unsigned long long pending = N == 64 ? ~0ull : (1ull << N) - 1;
     unsigned spins = 0;
-    while (pending && keep_polling(spins, x))
+    do
     {
+        word v[N];
 #pragma unroll
         for (int i = 0; i < N; ++i)
         {
-            if ((pending >> i) & 1ull)
+            v[i] = __hip_atomic_load(global(address(i)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+        {
+            if (((pending >> i) & 1ull) && uint32_t(v[i] >> 32) == x.epoch)
             {
-                const word v = __hip_atomic_load(global(address(i)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (uint32_t(v >> 32) == x.epoch)
+                out[i] = uint32_t(v[i]);
+                pending &= ~(1ull << i);
+            }
+        }
+    } while (pending && keep_polling(spins, x));
+}
+
+// Device-coherent 16-byte loads of Q consecutive chunks at p (16-byte
+// aligned), all requested before the one wait for their replies. One asm
+// statement, so no instruction can read a destination before the data is in:
+// left to itself the compiler may issue such loads one at a time, each with
+// its own wait, which makes a poll of a long row many round trips. sc1 is the
+// cache policy of the compiler's own agent-scope atomic loads; each 8-byte
+// word of a chunk is read whole, as its producer wrote it.
+#define TSAC_CHUNK(n, offset) "global_load_dwordx4 %" #n ", %[at], off offset:" #offset " sc1\n"
+template <int Q> __device__ __forceinline__ void load_chunks(const word* p, u32x4 (&c)[Q])
+{
+    if constexpr (Q == 2)
+    {
+        asm volatile(TSAC_CHUNK(0, 0) TSAC_CHUNK(1, 16) "s_waitcnt vmcnt(0)"
+                     : "=&v"(c[0]), "=&v"(c[1])
+                     : [at] "v"(p)
+                     : "memory");
+    }
+    else if constexpr (Q == 4)
+    {
+        asm volatile(TSAC_CHUNK(0, 0) TSAC_CHUNK(1, 16) TSAC_CHUNK(2, 32) TSAC_CHUNK(3, 48) "s_waitcnt vmcnt(0)"
+                     : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3])
+                     : [at] "v"(p)
+                     : "memory");
+    }
+    else if constexpr (Q == 8)
+    {
+        asm volatile(TSAC_CHUNK(0, 0) TSAC_CHUNK(1, 16) TSAC_CHUNK(2, 32) TSAC_CHUNK(3, 48) TSAC_CHUNK(4, 64)
+                         TSAC_CHUNK(5, 80) TSAC_CHUNK(6, 96) TSAC_CHUNK(7, 112) "s_waitcnt vmcnt(0)"
+                     : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(c[4]), "=&v"(c[5]), "=&v"(c[6]),
+                       "=&v"(c[7])
+                     : [at] "v"(p)
+                     : "memory");
+    }
+    else
+    {
+        static_assert(Q == 16, "2, 4, 8 or 16 chunks");
+        asm volatile(TSAC_CHUNK(0, 0) TSAC_CHUNK(1, 16) TSAC_CHUNK(2, 32) TSAC_CHUNK(3, 48) TSAC_CHUNK(4, 64)
+                         TSAC_CHUNK(5, 80) TSAC_CHUNK(6, 96) TSAC_CHUNK(7, 112) TSAC_CHUNK(8, 128)
+                             TSAC_CHUNK(9, 144) TSAC_CHUNK(10, 160) TSAC_CHUNK(11, 176) TSAC_CHUNK(12, 192)
+                                 TSAC_CHUNK(13, 208) TSAC_CHUNK(14, 224) TSAC_CHUNK(15, 240) "s_waitcnt vmcnt(0)"
+                     : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(c[4]), "=&v"(c[5]), "=&v"(c[6]),
+                       "=&v"(c[7]), "=&v"(c[8]), "=&v"(c[9]), "=&v"(c[10]), "=&v"(c[11]), "=&v"(c[12]),
+                       "=&v"(c[13]), "=&v"(c[14]), "=&v"(c[15])
+                     : [at] "v"(p)
+                     : "memory");
+    }
+}
+#undef TSAC_CHUNK
+
+// This lane's V consecutive BF16 values starting at value `first` of a word
+// vector (first a multiple of 4, the vector 16-byte aligned), once every word
+// carries the epoch. Words already current keep their first value.
+template <int V>
+__device__ __forceinline__ void take_row(const word* w, std::size_t first, const Exchange& x, uint16_t (&v)[V])
+{
+    static_assert(V % 4 == 0, "whole 16-byte chunks");
+    constexpr int words = V / 2, chunks = V / 4;
+    const word* p = w + first / 2;
+    uint32_t got[words];
+    unsigned long long pending = words == 64 ? ~0ull : (1ull << words) - 1;
+    unsigned spins = 0;
+    do
+    {
+        u32x4 c[chunks];
+        load_chunks<chunks>(p, c);
+#pragma unroll
+        for (int j = 0; j < chunks; ++j)
+        {
+            const uint32_t payload[2] = {c[j].x, c[j].z}, epoch[2] = {c[j].y, c[j].w};
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+            {
+                const int i = 2 * j + h;
+                if (((pending >> i) & 1ull) && epoch[h] == x.epoch)
                 {
-                    out[i] = uint32_t(v);
+                    got[i] = payload[h];
                     pending &= ~(1ull << i);
                 }
             }
         }
-    }
-}
-
-// Called by a whole wave: returns once values [first, first + count) of a word
-// vector (first and count multiples of 64) show the epoch at one word per
-// 64-value producer tile. Polling one word per tile instead of every word
-// keeps long waits from flooding memory; the reads that follow still check
-// every word.
-constexpr bool sentinel_waits = false;
-__device__ __forceinline__ void await_tiles(const word* w, std::size_t first, int count, const Exchange& x)
-{
-    if constexpr (!sentinel_waits)
-    {
-        return;
-    }
-    const int lane = threadIdx.x % wave;
-    const int tiles = count / 64;
-    bool ready = true;
-    for (int t = lane; t < tiles; t += wave)
-    {
-        ready = ready && uint32_t(peek(w, (first + std::size_t(t) * 64) / 2) >> 32) == x.epoch;
-    }
-    unsigned spins = 0;
-    while (!__all(ready) && keep_polling(spins, x))
-    {
-        if (!ready)
-        {
-            ready = true;
-            for (int t = lane; t < tiles; t += wave)
-            {
-                ready = ready && uint32_t(peek(w, (first + std::size_t(t) * 64) / 2) >> 32) == x.epoch;
-            }
-        }
-    }
-}
-
-// This lane's V consecutive BF16 values starting at value `first` (even) of a
-// word vector.
-template <int V>
-__device__ __forceinline__ void take_row(const word* w, std::size_t first, const Exchange& x, uint16_t (&v)[V])
-{
-    static_assert(V % 2 == 0, "whole words");
-    uint32_t p[V / 2];
-    take_words<V / 2>([&](int i) { return w + first / 2 + i; }, x, p);
+    } while (pending && keep_polling(spins, x));
 #pragma unroll
-    for (int i = 0; i < V / 2; ++i)
+    for (int i = 0; i < words; ++i)
     {
-        v[2 * i] = uint16_t(p[i] & 0xffff);
-        v[2 * i + 1] = uint16_t(p[i] >> 16);
+        v[2 * i] = uint16_t(got[i] & 0xffff);
+        v[2 * i + 1] = uint16_t(got[i] >> 16);
     }
 }
 
@@ -490,7 +526,6 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
         const std::size_t first = std::size_t(warp) * K + lane * V;
         if constexpr (I == In::words || I == In::words_norm)
         {
-            await_tiles(p.x, std::size_t(warp) * K, K, x);
             take_row<V>(p.x, first, x, v);
             if constexpr (I == In::words_norm)
             {
@@ -522,7 +557,6 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
             if (p.prefix_in)
             {
                 uint16_t prev[V];
-                await_tiles(p.prefix_in, std::size_t(warp) * K, K, x);
                 take_row<V>(p.prefix_in, first, x, prev);
 #pragma unroll
                 for (int i = 0; i < V; ++i)
@@ -667,8 +701,22 @@ struct Attend
 
 template <int HW> constexpr int attend_lds()
 {
-    // partial records, query words, staged exchanged rows (keys then values)
-    return (max_blocks * (2 + HW) + HW / 2 + max_books * HW) * 4;
+    // partial records, query words, staged exchanged rows (keys then values),
+    // each wave's block weights
+    return (max_blocks * (2 + HW) + HW / 2 + max_books * HW + frame_waves * 64) * 4;
+}
+
+// Keeps a value in vector registers: a value every lane loads from one shared
+// address is otherwise kept in scalar registers, and the compiler then spills
+// such values into vector-register lanes and reads each back with readlane
+// and a wait.
+__device__ __forceinline__ void in_vgprs(uint4& u)
+{
+    asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
+}
+__device__ __forceinline__ void in_vgprs(float4& u)
+{
+    asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
 }
 
 // One (lane, head) query over all its keys (decode.hip attention_step_kernel).
@@ -696,6 +744,7 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
     float* partial = reinterpret_cast<float*>(lds); // [blocks][2 + HW]
     uint32_t* query_words = reinterpret_cast<uint32_t*>(partial + max_blocks * (2 + HW)); // [HW/2]
     uint32_t* staged = query_words + HW / 2; // [max_books][row_words]
+    float* weights = reinterpret_cast<float*>(staged + max_books * row_words); // [frame_waves][64]
     const int m = item / a.heads, head = item % a.heads;
     const int lane = threadIdx.x % wave;
     const int warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
@@ -713,11 +762,50 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
     const uint16_t* k = temporal ? a.keys + std::size_t(m) * a.lane_stride + head * HW : nullptr;
     const uint16_t* v = temporal ? a.values + std::size_t(m) * a.lane_stride + head * HW : nullptr;
 
+    // Key words and value words of one 64-key block: lane l holds key row
+    // block*64 + l, value[tt] this lane's value columns of row block*64 + tt.
+    // Temporal attention reads every row but the last (time - 1) from the
+    // cache; book attention reads all its rows (time <= max_books) from the
+    // exchange.
+    uint32_t key[HW / 2];
+    uint32_t value[64];
+    // Cache rows need nothing from this step: requested before any wait.
+    const auto load_cached = [&](int block)
+    {
+        const int start = block * 64;
+        const int count = time - start < 64 ? time - start : 64;
+        const int t = start + lane;
+        if (lane < count && t < cached)
+        {
+            const uint16_t* row = k + std::size_t(t) * width;
+#pragma unroll
+            for (int c = 0; c < HW / 8; ++c)
+            {
+                const uint4 u = load16(row + 8 * c);
+                key[4 * c] = u.x;
+                key[4 * c + 1] = u.y;
+                key[4 * c + 2] = u.z;
+                key[4 * c + 3] = u.w;
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 64; ++tt)
+        {
+            const int row = start + tt;
+            if (tt < count && row < cached)
+            {
+                const uint16_t* src = v + std::size_t(row) * width + per_lane * lane;
+                value[tt] = per_lane == 2 ? *global(reinterpret_cast<const uint32_t*>(src)) : uint32_t(*global(src));
+            }
+        }
+    };
+    if (temporal && warp < blocks)
+    {
+        load_cached(warp);
+    }
+
     // 1. Stage the query and the exchanged rows: word i of the query is i < HW/2;
     //    then row r's key words, then its value words.
-    await_tiles(row_words_of(time - 1), q_value, HW, x);
-    await_tiles(row_words_of(time - 1), q_value + width, HW, x);
-    await_tiles(row_words_of(time - 1), q_value + 2 * width, HW, x);
     __syncthreads(); // the previous job's readers of LDS are done
     {
         constexpr int per_thread = (HW / 2 + max_books * row_words + frame_threads - 1) / frame_threads;
@@ -752,95 +840,67 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
     }
     __syncthreads();
 
-    // 2. Blocks of 64 keys: wave w owns blocks w, w + waves, ... The query is
-    //    held in registers as packed BF16 pairs; block weights move between
-    //    lanes with readlane.
-    uint32_t query[HW / 2];
-#pragma unroll
-    for (int c = 0; c < HW / 8; ++c)
+    // The value word of staged row r for this lane's columns.
+    const auto staged_value = [&](int r) -> uint32_t
     {
-        const uint4 u = reinterpret_cast<const uint4*>(query_words)[c];
-        query[4 * c] = u.x;
-        query[4 * c + 1] = u.y;
-        query[4 * c + 2] = u.z;
-        query[4 * c + 3] = u.w;
-    }
-    uint32_t key[HW / 2];
-    uint32_t value[64];
-    const auto load_block = [&](int block)
-    {
-        const int start = block * 64;
-        const int count = time - start < 64 ? time - start : 64;
-        const int t = start + lane;
-        if (lane < count)
-        {
-            if (t < cached)
-            {
-                const uint16_t* row = k + std::size_t(t) * width;
-#pragma unroll
-                for (int c = 0; c < HW / 8; ++c)
-                {
-                    const uint4 u = load16(row + 8 * c);
-                    key[4 * c] = u.x;
-                    key[4 * c + 1] = u.y;
-                    key[4 * c + 2] = u.z;
-                    key[4 * c + 3] = u.w;
-                }
-            }
-            else
-            {
-                const uint32_t* row = staged + (t - cached) * row_words;
-#pragma unroll
-                for (int c = 0; c < HW / 2; ++c)
-                {
-                    key[c] = row[c];
-                }
-            }
-        }
-#pragma unroll
-        for (int tt = 0; tt < 64; ++tt)
-        {
-            const int row = start + tt;
-            uint32_t value_word = 0;
-            if (tt < count)
-            {
-                if (row < cached)
-                {
-                    const uint16_t* src = v + std::size_t(row) * width + per_lane * lane;
-                    value_word = per_lane == 2 ? *global(reinterpret_cast<const uint32_t*>(src)) : uint32_t(*global(src));
-                }
-                else
-                {
-                    const uint32_t pw = staged[(row - cached) * row_words + HW / 2 + (per_lane * lane) / 2];
-                    value_word = per_lane == 2 ? pw : ((lane & 1) ? (pw >> 16) : (pw & 0xffff));
-                }
-            }
-            value[tt] = value_word;
-        }
+        const uint32_t pw = staged[r * row_words + HW / 2 + (per_lane * lane) / 2];
+        return per_lane == 2 ? pw : ((lane & 1) ? (pw >> 16) : (pw & 0xffff));
     };
-    if (warp < blocks)
+    if (!temporal)
     {
-        load_block(warp);
+#pragma unroll
+        for (int tt = 0; tt < max_books; ++tt)
+        {
+            if (tt < time)
+            {
+                value[tt] = staged_value(tt);
+            }
+        }
     }
+
+    // 2. Blocks of 64 keys: wave w owns blocks w, w + waves, ...
+    float* block_weights = weights + warp * 64;
     for (int block = warp; block < blocks; block += frame_waves)
     {
         if (block != warp)
         {
-            load_block(block);
+            load_cached(block);
         }
         const int start = block * 64;
         const int count = time - start < 64 ? time - start : 64;
+        const int t = start + lane;
+        if (lane < count && t >= cached)
+        {
+            const uint4* row = reinterpret_cast<const uint4*>(staged + (t - cached) * row_words);
+#pragma unroll
+            for (int c = 0; c < HW / 8; ++c)
+            {
+                const uint4 u = row[c];
+                key[4 * c] = u.x;
+                key[4 * c + 1] = u.y;
+                key[4 * c + 2] = u.z;
+                key[4 * c + 3] = u.w;
+            }
+        }
         float score = -__builtin_inff();
         if (lane < count)
         {
+            // Ascending coordinates (src/scalar/attention.cpp:27-35).
             float dot = 0.0f;
 #pragma unroll
-            for (int c = 0; c < HW / 2; ++c)
+            for (int c = 0; c < HW / 8; ++c)
             {
-                dot = __builtin_fmaf(bf16_to_float(uint16_t(query[c] & 0xffff)),
-                                     bf16_to_float(uint16_t(key[c] & 0xffff)), dot);
-                dot = __builtin_fmaf(bf16_to_float(uint16_t(query[c] >> 16)), bf16_to_float(uint16_t(key[c] >> 16)),
-                                     dot);
+                uint4 q4 = reinterpret_cast<const uint4*>(query_words)[c];
+                in_vgprs(q4);
+                const uint32_t qw[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const uint32_t kw = key[4 * c + i];
+                    dot = __builtin_fmaf(__uint_as_float(qw[i] << 16), __uint_as_float(kw << 16), dot);
+                    dot = __builtin_fmaf(__uint_as_float(qw[i] & 0xffff0000u), __uint_as_float(kw & 0xffff0000u),
+                                         dot);
+                }
             }
             score = dot * a.scale;
         }
@@ -851,20 +911,62 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
             e = original_exp(score - maximum);
         }
         const float sum = tree_sum<wave>(e);
-        const int e_bits = __float_as_int(e);
-        float s0 = 0.0f, s1 = 0.0f;
+        block_weights[lane] = e;
+        wait_shared_memory();
+        // Ascending positions (src/scalar/attention.cpp:41-52); the staged
+        // last row of a temporal history comes last.
+        const int from_values = temporal ? (cached - start < count ? cached - start : count) : count;
+        // The weights needed, all requested before the first is used.
+        float4 w4[16];
 #pragma unroll
-        for (int tt = 0; tt < 64; ++tt)
+        for (int t4 = 0; t4 < 16; ++t4)
         {
-            if (tt < count)
+            if (4 * t4 < from_values)
             {
-                const float wt = __int_as_float(__builtin_amdgcn_readlane(e_bits, tt));
-                s0 = __builtin_fmaf(bf16_to_float(uint16_t(value[tt] & 0xffff)), wt, s0);
-                if (per_lane == 2)
+                w4[t4] = reinterpret_cast<const float4*>(block_weights)[t4];
+            }
+        }
+        float s0 = 0.0f, s1 = 0.0f;
+        const auto accumulate = [&](uint32_t vw, float w)
+        {
+            s0 = __builtin_fmaf(__uint_as_float(vw << 16), w, s0);
+            if (per_lane == 2)
+            {
+                s1 = __builtin_fmaf(__uint_as_float(vw & 0xffff0000u), w, s1);
+            }
+        };
+#pragma unroll
+        for (int t4 = 0; t4 < 16; ++t4)
+        {
+            if (4 * t4 >= from_values)
+            {
+                break;
+            }
+            in_vgprs(w4[t4]);
+            const float w[4] = {w4[t4].x, w4[t4].y, w4[t4].z, w4[t4].w};
+            if (4 * t4 + 4 <= from_values)
+            {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
                 {
-                    s1 = __builtin_fmaf(bf16_to_float(uint16_t(value[tt] >> 16)), wt, s1);
+                    accumulate(value[4 * t4 + i], w[i]);
                 }
             }
+            else if (4 * t4 < from_values)
+            {
+#pragma unroll
+                for (int i = 0; i < 3; ++i)
+                {
+                    if (4 * t4 + i < from_values)
+                    {
+                        accumulate(value[4 * t4 + i], w[i]);
+                    }
+                }
+            }
+        }
+        if (from_values < count)
+        {
+            accumulate(staged_value(0), block_weights[count - 1]);
         }
         float* record = partial + std::size_t(block) * (2 + HW);
         if (lane == 0)
@@ -892,23 +994,38 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
         numerator[i] = 0.0f;
     }
     float running_maximum = -__builtin_inff(), total = 0.0f;
-    for (int b = 0; b < blocks; ++b)
+    if (blocks == 1 && is_finite(partial[0]))
     {
-        const float* record = partial + std::size_t(b) * (2 + HW);
-        const float maximum = record[0];
-        const float difference = maximum - running_maximum;
-        const float factor = original_exp(-__builtin_fabsf(difference));
-        const float old_scale = running_maximum > maximum ? 1.0f : factor;
-        const float new_scale = running_maximum > maximum ? factor : 1.0f;
-        const float old_total = total * old_scale;
-        total = __builtin_fmaf(record[1], new_scale, old_total);
+        // Merging one block with a finite maximum into the empty state scales
+        // the zero totals by the finite original_exp(-88): each result is the
+        // block's value plus +0.
+        total = partial[1] + 0.0f;
 #pragma unroll
         for (int i = 0; i < per_lane; ++i)
         {
-            const float old = numerator[i] * old_scale;
-            numerator[i] = __builtin_fmaf(record[2 + per_lane * lane + i], new_scale, old);
+            numerator[i] = partial[2 + per_lane * lane + i] + 0.0f;
         }
-        running_maximum = running_maximum < maximum ? maximum : running_maximum;
+    }
+    else
+    {
+        for (int b = 0; b < blocks; ++b)
+        {
+            const float* record = partial + std::size_t(b) * (2 + HW);
+            const float maximum = record[0];
+            const float difference = maximum - running_maximum;
+            const float factor = original_exp(-__builtin_fabsf(difference));
+            const float old_scale = running_maximum > maximum ? 1.0f : factor;
+            const float new_scale = running_maximum > maximum ? factor : 1.0f;
+            const float old_total = total * old_scale;
+            total = __builtin_fmaf(record[1], new_scale, old_total);
+#pragma unroll
+            for (int i = 0; i < per_lane; ++i)
+            {
+                const float old = numerator[i] * old_scale;
+                numerator[i] = __builtin_fmaf(record[2 + per_lane * lane + i], new_scale, old);
+            }
+            running_maximum = running_maximum < maximum ? maximum : running_maximum;
+        }
     }
     const float reciprocal = 1.0f / total;
     const std::size_t at = std::size_t(m) * width + head * HW + per_lane * lane;
@@ -952,7 +1069,6 @@ __device__ __noinline__ void condition_rows(const word* in, const uint16_t* gain
         return;
     }
     uint16_t v[V];
-    await_tiles(in, std::size_t(row) * width, width, x);
     take_row<V>(in, std::size_t(row) * width + lane * V, x, v);
     layer_norm_lane<V>(v, gain, bias, lane);
     uint16_t p[V];
@@ -968,7 +1084,7 @@ __device__ __noinline__ void condition_rows(const word* in, const uint16_t* gain
 // ------------------------------------------------------------------ sampling job
 
 constexpr int window = 256;
-constexpr int draw_lds = max_lanes * 1024 * 4 + max_lanes * 1024 * 2 + window + 2 * max_lanes * 4;
+constexpr int draw_lds = max_lanes * 1024 * 4 + max_lanes * 1024 * 2 + max_lanes * 64 * 2 + window + 2 * max_lanes * 4;
 
 struct Draw
 {
@@ -985,9 +1101,9 @@ struct Draw
     unsigned long long payload_bytes = 0;
 };
 
-// Softmax and masses per lane (one wave each), then thread 0 decodes the
-// lanes' symbols in stream order with the decoder held in `state` (LDS)
-// (decode.hip sample_kernel).
+// Softmax, masses and top decisions per lane (one wave each), then wave 0
+// decodes the lanes' symbols in stream order with the decoder held in `state`
+// (LDS) (decode.hip sample_kernel).
 __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* state, const Exchange& exchange,
                                          uint32_t* error, uint8_t* lds)
 {
@@ -1008,10 +1124,11 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
     a.payload_bytes = uniform(std::size_t(job.payload_bytes));
     M = uniform(M);
     error = uniform(error);
-    float* nodes = reinterpret_cast<float*>(lds);                                  // [8][1024]
-    uint16_t* leaves = reinterpret_cast<uint16_t*>(lds + max_lanes * 1024 * 4);    // [8][1024]
-    uint8_t* bytes = lds + max_lanes * 1024 * 6;                                   // [window]
-    int* valid = reinterpret_cast<int*>(lds + max_lanes * 1024 * 6 + window);      // [8]
+    float* nodes = reinterpret_cast<float*>(lds);                                         // [8][1024]
+    uint16_t* leaves = reinterpret_cast<uint16_t*>(lds + max_lanes * 1024 * 4);           // [8][1024]
+    uint16_t* top = reinterpret_cast<uint16_t*>(lds + max_lanes * 1024 * 6);              // [8][64]
+    uint8_t* bytes = lds + max_lanes * (1024 * 6 + 128);                                  // [window]
+    int* valid = reinterpret_cast<int*>(lds + max_lanes * (1024 * 6 + 128) + window);     // [8]
     int* rows = valid + max_lanes;                                                 // [8]
     const int lane = threadIdx.x % wave, warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
     const bool active = warp < M;
@@ -1031,7 +1148,6 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
     if (active)
     {
         uint16_t v[16];
-        await_tiles(a.logits, std::size_t(warp) * 1024, 1024, x);
         take_row<16>(a.logits, std::size_t(warp) * 1024 + lane * 16, x, v);
         if (lane == 0)
         {
@@ -1067,14 +1183,16 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
             v[k] = float_to_bf16(e[k] * reciprocal);
             prob[k] = bf16_to_float(v[k]);
         }
-        store_row<16>(leaves + warp * 1024 + lane * 16, v);
         if (a.distributions)
         {
             store_row<16>(a.distributions + std::size_t(row) * 1024 + lane * 16, v);
         }
         if (decoding)
         {
+            store_row<16>(leaves + warp * 1024 + lane * 16, v);
             const bool ok = build_masses(prob, lane, nodes + warp * 1024);
+            wait_shared_memory();
+            build_top_decisions(lane, Masses{nodes + warp * 1024, leaves + warp * 1024}, top + warp * 64);
             if (lane == 0)
             {
                 valid[warp] = ok;
@@ -1086,14 +1204,16 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
         bytes[threadIdx.x] = uint8_t(byte);
     }
     __syncthreads();
-    if (threadIdx.x != 0)
+    if (warp != 0)
     {
         return;
     }
+    // Wave 0 decodes the lanes' symbols in stream order (decode.hip sample_kernel).
     DecoderState s = decoding ? *state : DecoderState{};
+    const ByteWindow staged{bytes, window, base_offset, a.payload, a.payload_bytes};
     for (int w = 0; w < M; ++w)
     {
-        const int r = rows[w];
+        const int r = __builtin_amdgcn_readfirstlane(rows[w]);
         int token;
         if (!decoding)
         {
@@ -1101,54 +1221,20 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
         }
         else
         {
-            if (!valid[w])
+            if (!__builtin_amdgcn_readfirstlane(valid[w]))
             {
                 s.failed = 1;
             }
-            int base = 0, left_count = 1024;
-            float mass = 1.0f;
-            const float* node = nodes + w * 1024;
-            while (left_count > 1 && !s.failed)
-            {
-                const int half = left_count / 2;
-                const float left = half == 1 ? flush(bf16_to_float(leaves[w * 1024 + base])) : node[1024 / half + base / half];
-                const uint16_t p0 = q15(left, mass);
-                const uint32_t range0 = uint32_t((uint64_t(s.range) * p0) >> 15);
-                if (s.code >= range0)
-                {
-                    s.code -= range0;
-                    s.range -= range0;
-                    base += half;
-                    left_count -= half;
-                    mass = flush(flush(mass) - flush(left));
-                }
-                else
-                {
-                    s.range = range0;
-                    left_count = half;
-                    mass = left;
-                }
-                while (s.range < 0xff01u)
-                {
-                    s.range <<= 8;
-                    const unsigned long long at = s.offset - base_offset;
-                    const uint32_t next =
-                        s.offset < a.payload_bytes ? (at < window ? bytes[at] : a.payload[s.offset]) : 0u;
-                    s.offset += s.offset < a.payload_bytes ? 1 : 0;
-                    s.code = (s.code << 8) + next;
-                }
-                if (!(s.code < s.range))
-                {
-                    s.failed = 1;
-                }
-            }
-            token = base;
+            token = decode_symbol(top + w * 64, Masses{nodes + w * 1024, leaves + w * 1024}, s, staged);
         }
-        a.current[std::size_t(w) * a.books + a.book] = uint16_t(token);
-        a.tokens[r] = uint16_t(token);
-        publish(a.token_words, w, uint32_t(token), x.epoch);
+        if (lane == 0)
+        {
+            a.current[std::size_t(w) * a.books + a.book] = uint16_t(token);
+            a.tokens[r] = uint16_t(token);
+            publish(a.token_words, w, uint32_t(token), x.epoch);
+        }
     }
-    if (decoding)
+    if (decoding && lane == 0)
     {
         *state = s;
     }
