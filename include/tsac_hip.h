@@ -126,7 +126,10 @@ int tsac_hip_distributions(tsac_hip_session* session, const tsac_hip_header* hea
                            const uint16_t* tokens, size_t count, int mode, uint16_t* out);
 
 /* Wall-clock split of the session's last encode/decode/distributions call
- * (seconds): [0] GPU model work, [1] host range coding, [2] total. */
+ * (seconds): [0] GPU model work, [1] host range coding, [2] total, [3] the
+ * host-to-device copy of the call's input (tokens, or the stream's payload),
+ * included in [0] and [2]. No counterpart in the reference; for callers that
+ * report throughput with inputs already in device memory. */
 int tsac_hip_session_timing(const tsac_hip_session* session, double* seconds, size_t count);
 
 /* ---- operators on device memory (hipStream_t passed as void*) -------------- */

@@ -281,6 +281,8 @@ Session::Session(std::shared_ptr<const Model> model) : model_(std::move(model))
 {
     check_hip(hipSetDevice(model_->device()), "hipSetDevice");
     check_hip(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    check_hip(hipEventCreate(&upload_start_), "hipEventCreate");
+    check_hip(hipEventCreate(&upload_stop_), "hipEventCreate");
     errors_ = DeviceBuffer(256);
     pinned_errors_.reserve(256);
 }
@@ -292,6 +294,35 @@ Session::~Session()
         (void)hipStreamSynchronize(stream_);
         (void)hipStreamDestroy(stream_);
     }
+    if (upload_start_)
+    {
+        (void)hipEventDestroy(upload_start_);
+    }
+    if (upload_stop_)
+    {
+        (void)hipEventDestroy(upload_stop_);
+    }
+}
+
+void Session::upload_input(void* device, const void* host, std::size_t bytes)
+{
+    check_hip(hipEventRecord(upload_start_, stream_), "hipEventRecord");
+    check_hip(hipMemcpyAsync(device, host, bytes, hipMemcpyHostToDevice, stream_), "upload input");
+    check_hip(hipEventRecord(upload_stop_, stream_), "hipEventRecord");
+    uploaded_ = true;
+}
+
+double Session::input_seconds()
+{
+    if (!uploaded_)
+    {
+        return 0.0;
+    }
+    uploaded_ = false;
+    float ms = 0.0f;
+    check_hip(hipEventSynchronize(upload_stop_), "hipEventSynchronize");
+    check_hip(hipEventElapsedTime(&ms, upload_start_, upload_stop_), "hipEventElapsedTime");
+    return ms / 1000.0;
 }
 
 void Session::clear()
@@ -523,8 +554,7 @@ void Session::batched(const Header& h, const uint16_t* tokens, uint16_t* distrib
     auto* conditioning = arena_.get<uint16_t>("cond", steps * w);
     temporal_rows(h, tokens, conditioning);
     auto* d_tokens = arena_.get<uint16_t>("tokens", steps * C);
-    check_hip(hipMemcpyAsync(d_tokens, tokens, steps * C * 2, hipMemcpyHostToDevice, stream_),
-              "upload tokens");
+    upload_input(d_tokens, tokens, steps * C * 2);
     const std::size_t chunk_steps = std::max<std::size_t>(1, batch_rows / C);
     // Codebook sequences: step i of a chunk is rows i*C .. i*C+C-1.
     {
@@ -634,7 +664,7 @@ std::vector<uint8_t> Session::encode(Header h, const uint16_t* tokens, std::size
     }
     const auto bytes = frame_normal(h, crc, encoder.finish());
     const double t2 = now();
-    timing_ = {t1 - t0, t2 - t1, t2 - t0};
+    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds()};
     return bytes;
 }
 
@@ -653,7 +683,7 @@ std::vector<uint16_t> Session::decode(const uint8_t* stream, std::size_t length)
     check_errors();
     require(token_crc32(tokens.data(), tokens.size()) == h.token_crc, "invalid token CRC32");
     const double t1 = now();
-    timing_ = {t1 - t0, 0.0, t1 - t0};
+    timing_ = {t1 - t0, 0.0, t1 - t0, input_seconds()};
     return tokens;
 }
 
@@ -675,6 +705,6 @@ void Session::distributions(Header h, const uint16_t* tokens, std::size_t count,
     }
     check_errors();
     const double t1 = now();
-    timing_ = {t1 - t0, 0.0, t1 - t0};
+    timing_ = {t1 - t0, 0.0, t1 - t0, input_seconds()};
 }
 } // namespace tsac_hip

@@ -188,7 +188,10 @@ public:
     // stepwise (GEMV) driver instead of the batched (GEMM) one.
     void distributions(Header header, const uint16_t* tokens, std::size_t count, bool decode_pass,
                        uint16_t* out);
-    std::array<double, 3> timing() const
+    // Seconds of the last call: GPU model work, host range coding, total, and
+    // the host-to-device copy of the call's input (tokens or payload), which
+    // the first and third include.
+    std::array<double, 4> timing() const
     {
         return timing_;
     }
@@ -197,6 +200,10 @@ private:
     struct Stepwise;
     void check_errors();
     void reset_errors();
+    // Copies the call's input to the device between two events; input_seconds()
+    // (after the stream has drained) is that copy's duration.
+    void upload_input(void* device, const void* host, std::size_t bytes);
+    double input_seconds();
     void validate(const Header& h, const uint16_t* tokens, std::size_t count) const;
     // Batched known-token pass. Writes either the BF16 distributions of every
     // token (distributions != null) or its ten Q15 splits (splits != null).
@@ -222,6 +229,8 @@ private:
     Arena arena_;
     DeviceBuffer errors_;
     PinnedBuffer pinned_errors_, staging_, staging_nodes_, staging_tokens_;
-    std::array<double, 3> timing_{};
+    std::array<double, 4> timing_{};
+    hipEvent_t upload_start_ = nullptr, upload_stop_ = nullptr;
+    bool uploaded_ = false;
 };
 } // namespace tsac_hip

@@ -184,8 +184,7 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
         d_payload = arena_.get<uint8_t>("s.payload", std::max<std::size_t>(payload_bytes, 1));
         if (payload_bytes)
         {
-            check_hip(hipMemcpyAsync(d_payload, payload, payload_bytes, hipMemcpyHostToDevice, stream_),
-                      "upload payload");
+            upload_input(d_payload, payload, payload_bytes);
         }
         // RangeDecoder construction (src/format/range.cpp:122-129): three bytes, zero-extended.
         DecoderState s{0xff0000u, 0, 0, 0, 0};

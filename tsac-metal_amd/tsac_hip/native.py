@@ -210,9 +210,9 @@ class HipSession:
         return out
 
     def timing(self):
-        t = (C.c_double * 3)()
-        check(library().tsac_hip_session_timing(self.handle, t, 3))
-        return {"model": t[0], "range_coding": t[1], "total": t[2]}
+        t = (C.c_double * 4)()
+        check(library().tsac_hip_session_timing(self.handle, t, 4))
+        return {"model": t[0], "range_coding": t[1], "total": t[2], "input_upload": t[3]}
 
 
 # ---------------------------------------------------------------- operators on torch tensors
