@@ -145,6 +145,17 @@ def model_desc(model):
     return desc, keep
 
 
+def _release(owner, destroy: str):
+    """Destroys owner.handle once. The destroy entry point is resolved while the
+    handle is created (owner._library), so a finaliser that runs during interpreter
+    shutdown, after this module's globals are cleared, still reaches it."""
+    handle = getattr(owner, "handle", None)
+    lib = getattr(owner, "_library", None)
+    if handle and lib is not None:
+        getattr(lib, destroy)(handle)
+    owner.handle = None
+
+
 class HipModel:
     """Immutable device model (MetalTransformer::from_model, src/metal/transformer.hpp:16)."""
 
@@ -155,13 +166,11 @@ class HipModel:
         handle = vp()
         check(lib.tsac_hip_model_create(C.byref(desc), C.byref(limits) if limits else None,
                                         C.byref(handle)))
-        self.handle = handle
+        self.handle, self._library = handle, lib
         del keep
 
     def __del__(self):
-        if getattr(self, "handle", None):
-            library().tsac_hip_model_destroy(self.handle)
-            self.handle = None
+        _release(self, "tsac_hip_model_destroy")
 
     def session(self) -> "HipSession":
         return HipSession(self)
@@ -174,12 +183,10 @@ class HipSession:
         self.model = model
         handle = vp()
         check(library().tsac_hip_session_create(model.handle, C.byref(handle)))
-        self.handle = handle
+        self.handle, self._library = handle, library()
 
     def __del__(self):
-        if getattr(self, "handle", None):
-            library().tsac_hip_session_destroy(self.handle)
-            self.handle = None
+        _release(self, "tsac_hip_session_destroy")
 
     def clear(self):
         check(library().tsac_hip_session_clear(self.handle))
@@ -241,12 +248,10 @@ class DeviceLinear:
         desc = Linear(_ptr(values, C.c_int8), _ptr(scales, C.c_float), _ptr(bias, C.c_float))
         handle = vp()
         check(library().tsac_hip_linear_create(C.byref(desc), k, n, C.byref(handle)))
-        self.handle = handle
+        self.handle, self._library = handle, library()
 
     def __del__(self):
-        if getattr(self, "handle", None):
-            library().tsac_hip_linear_destroy(self.handle)
-            self.handle = None
+        _release(self, "tsac_hip_linear_destroy")
 
     def apply(self, x, y, path=PATH_AUTO, stream=None):
         """x: int16/uint16 cuda tensor [M][K] of BF16 bits -> y [M][N]."""
