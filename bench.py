@@ -18,6 +18,9 @@ Also measured in the same run:
   * roofline_gemm: the encode MFMA GEMM on the codebook-stack qkv shape
     (M = 30,960 rows, K = 512, N = 1536).
   * qlinear: per-launch GB/s on the K=1024, N in {1024, 4096} shapes.
+  * attainable: this device's streaming-read rate and int8 MFMA rate, measured
+    by the library's calibration kernels; each roofline also reports its
+    fraction of these.
   * cpu_baseline: the C oracle (bit-exact restatement of the reference CPU
     path, lane-parallel like the reference's executor) on a bounded sample.
 """
@@ -103,6 +106,40 @@ def gemv_roofline(torch, native, launches):
             "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": measured, "bytes_per_launch": traffic, "avg_launch_us": round(seconds * 1e6, 2),
             "shape": {"K": K, "N": rows, "M": M, "distinct_weight_bytes": mats * rows * K}}
+
+
+def attainable_peaks(torch, native):
+    """Attainable rates on this device: a streaming read of 4 rotating 256 MiB
+    buffers with the GEMV's load pattern, and independent int8 MFMA chains."""
+    buffers = [torch.empty(256 << 20, dtype=torch.uint8, device="cuda") for _ in range(4)]
+    for b in buffers:
+        b.fill_(1)
+    stream = torch.cuda.current_stream()
+    for i in range(8):
+        native.probe_read(buffers[i % 4], stream)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    launches = 64
+    start.record(stream)
+    for i in range(launches):
+        native.probe_read(buffers[i % 4], stream)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    read = (256 << 20) * launches / (start.elapsed_time(stop) / 1000) / 1e9
+    del buffers
+    torch.cuda.empty_cache()
+    native.probe_mfma(4096, 4000, stream)
+    mfma = 0.0
+    for _ in range(3):
+        start.record(stream)
+        ops = native.probe_mfma(4096, 4000, stream)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        mfma = max(mfma, ops / (start.elapsed_time(stop) / 1000) / 1e12)
+    # A probe that beats the published peaks did not do its work.
+    assert read < 1.05 * HBM_PEAK_GBPS and mfma < 1.05 * INT8_PEAK_TOPS, (read, mfma)
+    return {"hbm_read_GBps": round(read, 1), "int8_mfma_TOPs": round(mfma, 1),
+            "method": "probe_read (16-byte nontemporal loads, 64 KiB per workgroup, 1 GiB rotating) and "
+                      "probe_mfma (4096 x 4 waves, 4 independent v_mfma_i32_32x32x32_i8 chains)"}
 
 
 def gemm_roofline(torch, native, launches=20):
@@ -268,10 +305,17 @@ def main():
         })
         del session, hip_model
         torch.cuda.synchronize()
+    if args.only in ("all", "gemv", "gemm"):
+        peaks = attainable_peaks(torch, native)
+        result["attainable"] = peaks
     if args.only in ("all", "gemv"):
-        result["roofline"] = gemv_roofline(torch, native, args.gemv_launches)
+        roof = gemv_roofline(torch, native, args.gemv_launches)
+        roof["frac_of_attainable"] = round(roof["achieved"] / peaks["hbm_read_GBps"], 4)
+        result["roofline"] = roof
     if args.only in ("all", "gemm"):
-        result["roofline_gemm"] = gemm_roofline(torch, native)
+        roof = gemm_roofline(torch, native)
+        roof["frac_of_attainable"] = round(roof["achieved"] / peaks["int8_mfma_TOPs"], 4)
+        result["roofline_gemm"] = roof
     if args.only == "all":
         result["qlinear"] = qlinear_table(torch, native)
         if not args.no_cpu:

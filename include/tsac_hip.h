@@ -217,6 +217,17 @@ int tsac_hip_attention_causal(const uint16_t* qkv, size_t heads, size_t head_wid
                               size_t sequences, size_t max_length, const uint16_t* rotations,
                               float scale, uint16_t* out, void* stream);
 
+/* ---- calibration (no counterpart in the reference) ------------------------- */
+
+/* The attainable rates roofline fractions are read against, for benchmarks on
+ * the device that runs the model. tsac_hip_probe_read launches one pass that
+ * streams `bytes` of device memory (a multiple of 64 KiB, 16-byte aligned) with
+ * the decode GEMV's load pattern; tsac_hip_probe_mfma launches `workgroups` x 4
+ * waves of independent int8 MFMA chains and returns in *ops the int8 operations
+ * that launch performs. Time them with events on `stream`. */
+int tsac_hip_probe_read(const void* data, size_t bytes, void* stream);
+int tsac_hip_probe_mfma(size_t workgroups, int iterations, double* ops, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -426,3 +426,14 @@ def test_attention_causal_matches_oracle(torch, native, oracle, heads, hw, rotar
         for t in range(length):
             expected = oracle.attention(q[t], k[:t + 1], v[:t + 1], heads, hw, scale, t < replay)
             assert np.array_equal(got[start + t], expected), (s, t)
+
+
+def test_calibration_probes(torch, native):
+    """The calibration kernels run, report their operation count, and reject
+    sizes they cannot stream."""
+    data = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    native.probe_read(data)
+    assert native.probe_mfma(8, 3) == 8 * 4 * 4 * 3 * 65536
+    torch.cuda.synchronize()
+    with pytest.raises(native.HipError, match="multiple of 64 KiB"):
+        native.probe_read(data[:1000])

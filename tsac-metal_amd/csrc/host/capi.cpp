@@ -428,4 +428,19 @@ int tsac_hip_attention_causal(const uint16_t* qkv, size_t heads, size_t head_wid
                               sequences, max_length, rotations, scale, out, as_stream(stream));
         });
 }
+
+int tsac_hip_probe_read(const void* data, size_t bytes, void* stream)
+{
+    return guarded([&] { probe_read(data, bytes, as_stream(stream)); });
+}
+
+int tsac_hip_probe_mfma(size_t workgroups, int iterations, double* ops, void* stream)
+{
+    return guarded(
+        [&]
+        {
+            require(ops != nullptr, "probe_mfma: ops must not be null");
+            *ops = probe_mfma(workgroups, iterations, as_stream(stream));
+        });
+}
 }

@@ -107,6 +107,11 @@ void add_rows(const uint16_t* a, const uint16_t* b, std::size_t rows, std::size_
 void softmax_rows(const uint16_t* x, std::size_t rows, std::size_t width, uint16_t* out,
                   uint32_t* error, hipStream_t stream);
 void gelu_values(const uint16_t* x, std::size_t count, uint16_t* out, hipStream_t stream);
+
+// Calibration (peak.hip): one streaming read of `bytes` (a multiple of 64 KiB),
+// and an MFMA loop whose launch performs the returned number of int8 operations.
+void probe_read(const void* data, std::size_t bytes, hipStream_t stream);
+double probe_mfma(std::size_t workgroups, int iterations, hipStream_t stream);
 void rotary_values(const uint16_t* x, const uint16_t* coefficients, std::size_t count,
                    uint16_t* out, hipStream_t stream);
 } // namespace tsac_hip

@@ -31,6 +31,7 @@ EXPORTS = (
     "tsac_hip_linear_apply", "tsac_hip_linear_apply_quantized", "tsac_hip_bf8l",
     "tsac_hip_layer_norm", "tsac_hip_softmax", "tsac_hip_gelu", "tsac_hip_rotary", "tsac_hip_add",
     "tsac_hip_attention", "tsac_hip_attention_causal", "tsac_hip_bf8l_tiles", "tsac_hip_tile_rows",
+    "tsac_hip_probe_read", "tsac_hip_probe_mfma",
 )
 
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_TILES = 0, 1, 2, 3
@@ -108,6 +109,8 @@ def library() -> C.CDLL:
         lib.tsac_hip_add.argtypes = [vp, vp, sz, sz, sz, vp, vp]
         lib.tsac_hip_attention.argtypes = [vp, vp, vp, sz, sz, sz, sz, sz, C.c_float, C.c_int, vp, vp]
         lib.tsac_hip_attention_causal.argtypes = [vp, sz, sz, vp, vp, vp, sz, sz, vp, C.c_float, vp, vp]
+        lib.tsac_hip_probe_read.argtypes = [vp, sz, vp]
+        lib.tsac_hip_probe_mfma.argtypes = [sz, C.c_int, C.POINTER(C.c_double), vp]
         _lib = lib
     return _lib
 
@@ -311,3 +314,15 @@ def attention_causal(qkv, heads, head_width, start, length, replay, sequences, m
     check(library().tsac_hip_attention_causal(
         _dp(qkv), heads, head_width, _dp(start), _dp(length), _dp(replay), sequences, max_length,
         _dp(rotations) if rotations is not None else None, scale, _dp(out), _stream(stream)))
+
+
+def probe_read(data, stream=None):
+    """One streaming read pass over a contiguous cuda tensor (size a multiple of 64 KiB)."""
+    check(library().tsac_hip_probe_read(_dp(data), data.numel() * data.element_size(), _stream(stream)))
+
+
+def probe_mfma(workgroups: int, iterations: int, stream=None) -> float:
+    """Launches the int8 MFMA loop; returns the operations that launch performs."""
+    ops = C.c_double()
+    check(library().tsac_hip_probe_mfma(workgroups, iterations, C.byref(ops), _stream(stream)))
+    return ops.value
