@@ -18,6 +18,8 @@ Also measured in the same run:
   * roofline_gemm: the encode MFMA GEMM on the codebook-stack qkv shape
     (M = 30,960 rows, K = 512, N = 1536).
   * qlinear: per-launch GB/s on the K=1024, N in {1024, 4096} shapes.
+  * attention: causal multi-head attention alone (16 x 64 heads, batch 3,
+    T in {256, 1290, 2580}): causal prefill TFLOP/s and one-query decode GB/s.
   * attainable: this device's streaming-read rate and int8 MFMA rate, measured
     by the library's calibration kernels; each roofline also reports its
     fraction of these.
@@ -40,6 +42,7 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+FP32_PEAK_TFLOPS = 157.3
 
 
 def parse():
@@ -50,7 +53,7 @@ def parse():
     p.add_argument("--frames", type=int, default=2580)
     p.add_argument("--batch", type=int, default=3)
     p.add_argument("--geometry", choices=["reference", "wide"], default="reference")
-    p.add_argument("--only", choices=["all", "model", "gemv", "gemm"], default="all")
+    p.add_argument("--only", choices=["all", "model", "gemv", "gemm", "attention"], default="all")
     p.add_argument("--gemv-launches", type=int, default=64)
     p.add_argument("--cpu-frames", type=int, default=660, help="CPU baseline sample (frames)")
     p.add_argument("--no-cpu", action="store_true")
@@ -215,6 +218,61 @@ def qlinear_table(torch, native):
     return table
 
 
+def attention_rates(torch, native, lengths=(256, 1290, 2580), batch=3, heads=16, head_width=64):
+    """Causal attention alone (16 heads x 64, batch 3): full causal prefill
+    (every query t over keys 0..t) and one incremental decode query over T
+    cached keys, BF16 inputs drawn from N(0, 1), scale 1/8."""
+    width = heads * head_width
+    scale = 1.0 / np.sqrt(head_width)
+    rows = []
+    for T in lengths:
+        gen = torch.Generator(device="cuda").manual_seed(T)
+        qkv = (torch.randn((batch * T, 3 * width), device="cuda", generator=gen).view(torch.int32) >> 16)
+        qkv = qkv.to(torch.int16).contiguous()
+        start = torch.arange(batch, dtype=torch.int32, device="cuda") * T
+        length = torch.full((batch,), T, dtype=torch.int32, device="cuda")
+        replay = torch.zeros(batch, dtype=torch.int32, device="cuda")
+        out = torch.empty((batch * T, width), dtype=torch.int16, device="cuda")
+        run = lambda: native.attention_causal(qkv, heads, head_width, start, length, replay, batch, T, None,
+                                              scale, out)
+        run()
+        start_e, stop_e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        start_e.record()
+        for _ in range(reps):
+            run()
+        stop_e.record()
+        torch.cuda.synchronize()
+        prefill_s = start_e.elapsed_time(stop_e) / 1000 / reps
+        flops = batch * heads * 4 * head_width * T * (T + 1) / 2
+        # Decode: the last position's query over the T cached keys/values.
+        keys = qkv[:, width:2 * width].contiguous()
+        values = qkv[:, 2 * width:].contiguous()
+        query = qkv.view(batch, T, 3 * width)[:, T - 1, :width].contiguous()
+        dout = torch.empty((batch, width), dtype=torch.int16, device="cuda")
+        step = lambda: native.attention(query, keys, values, T * width, batch, T, heads, head_width, scale,
+                                        False, dout)
+        step()
+        start_e.record()
+        reps = 50
+        for _ in range(reps):
+            step()
+        stop_e.record()
+        torch.cuda.synchronize()
+        decode_s = start_e.elapsed_time(stop_e) / 1000 / reps
+        kv_bytes = batch * 2 * T * width * 2
+        rows.append({"T": T, "prefill_us": round(prefill_s * 1e6, 1),
+                     "prefill_TFLOPs": round(flops / prefill_s / 1e12, 2),
+                     "prefill_frac_fp32_valu": round(flops / prefill_s / 1e12 / FP32_PEAK_TFLOPS, 4),
+                     "decode_us": round(decode_s * 1e6, 2), "decode_GBps": round(kv_bytes / decode_s / 1e9, 1),
+                     "decode_frac_hbm": round(kv_bytes / decode_s / 1e9 / HBM_PEAK_GBPS, 4)})
+        del qkv, keys, values, out
+    torch.cuda.empty_cache()
+    return {"heads": heads, "head_width": head_width, "batch": batch, "rows": rows,
+            "flops": "batch*heads*4*head_width*T*(T+1)/2 (causal prefill)",
+            "bytes": "batch*2*T*heads*head_width*2 (decode: the BF16 key and value cache)"}
+
+
 def cpu_baseline(model, frames, batch):
     """The C oracle on a bounded sample: pack_normal of `frames` frames (same
     geometry, batch, books), lanes prepared concurrently like the reference's
@@ -316,6 +374,8 @@ def main():
         roof = gemm_roofline(torch, native)
         roof["frac_of_attainable"] = round(roof["achieved"] / peaks["int8_mfma_TOPs"], 4)
         result["roofline_gemm"] = roof
+    if args.only in ("all", "attention"):
+        result["attention"] = attention_rates(torch, native)
     if args.only == "all":
         result["qlinear"] = qlinear_table(torch, native)
         if not args.no_cpu:
