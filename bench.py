@@ -24,7 +24,8 @@ Also measured in the same run:
     by the library's calibration kernels; each roofline also reports its
     fraction of these.
   * cpu_baseline: the C oracle (bit-exact restatement of the reference CPU
-    path, lane-parallel like the reference's executor) on a bounded sample.
+    path, lane-parallel like the reference's executor): encode + decode round
+    trip of a bounded sample (1290 frames, 15 s of audio), same rate definition.
 """
 import argparse
 import json
@@ -55,7 +56,7 @@ def parse():
     p.add_argument("--geometry", choices=["reference", "wide"], default="reference")
     p.add_argument("--only", choices=["all", "model", "gemv", "gemm", "attention"], default="all")
     p.add_argument("--gemv-launches", type=int, default=64)
-    p.add_argument("--cpu-frames", type=int, default=660, help="CPU baseline sample (frames)")
+    p.add_argument("--cpu-frames", type=int, default=1290, help="CPU baseline sample (frames)")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
 
@@ -274,9 +275,11 @@ def attention_rates(torch, native, lengths=(256, 1290, 2580), batch=3, heads=16,
 
 
 def cpu_baseline(model, frames, batch):
-    """The C oracle on a bounded sample: pack_normal of `frames` frames (same
-    geometry, batch, books), lanes prepared concurrently like the reference's
-    executor (src/common/transformer.cpp:70-90)."""
+    """The C oracle on a bounded sample of the same workload: a pack_normal +
+    unpack_normal round trip of `frames` frames (same geometry, batch, books),
+    lanes run concurrently like the reference's executor
+    (src/common/transformer.cpp:70-90). Same rate definition as `value`:
+    tokens / (encode seconds + decode seconds)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     from oracle import Oracle, header
     from tsac_hip.synthetic import random_tokens
@@ -285,13 +288,17 @@ def cpu_baseline(model, frames, batch):
     tokens = random_tokens(frames, 1, 12, seed=99)
     om = Oracle().model(model)
     t0 = time.perf_counter()
-    om.pack_normal(header(frames, batch, 1, 12), tokens, threads=threads)
-    seconds = time.perf_counter() - t0
+    stream = om.pack_normal(header(frames, batch, 1, 12), tokens, threads=threads)
+    t1 = time.perf_counter()
+    decoded = om.unpack_normal(stream, threads=threads)
+    t2 = time.perf_counter()
+    assert np.array_equal(decoded, tokens.ravel()), "oracle round trip failed"
+    seconds = t2 - t0
     return {"value": round(tokens.size / seconds, 1), "unit": "tokens/s", "cores": threads,
             "kind": "port",
-            "sample": f"oracle pack_normal of {frames} frames x 12 codebooks (batch {batch}, "
-                      f"{tokens.size} tokens) in {seconds:.1f} s; host has "
-                      f"{len(os.sched_getaffinity(0))} cores, lane parallelism caps threads at {threads}"}
+            "sample": f"oracle pack_normal + unpack_normal round trip of {frames} frames x 12 codebooks "
+                      f"(batch {batch}, {tokens.size} tokens): encode {t1 - t0:.1f} s + decode {t2 - t1:.1f} s; "
+                      f"host has {len(os.sched_getaffinity(0))} cores, lane parallelism caps threads at {threads}"}
 
 
 def main():

@@ -217,6 +217,45 @@ def test_gemm_many_tiles_per_workgroup(torch, native, k, n, with_residual):
         assert np.array_equal(host(y), want)
 
 
+def test_gemm_output_beyond_32bit_byte_range(torch, native, oracle):
+    """Outputs are addressed through 32-bit buffer ranges, so an output matrix
+    past 2^31 bytes takes several launches of row chunks (K=256, N=8192: 130,944
+    rows per launch); rows on both sides of the chunk boundary, in both
+    activation layouts and with a residual, must match the oracle."""
+    rng = np.random.default_rng(31)
+    k, n = 256, 8192
+    m = 131072 + 300
+    assert m * n * 2 > 2 ** 31
+    values, scales, bias = random_linear(rng, k, n, bias_std=0.1)
+    linear = native.DeviceLinear(values, scales, bias)
+    x = _activations(rng, m, k)
+    dx = dev(torch, x)
+    rows = np.unique(np.r_[0, 1, 130943, 130944, 130945, 131071, 131072, m - 1, rng.integers(0, m, 24)])
+    expected = oracle.qlinear(values, scales, bias, x[rows])
+    index = torch.from_numpy(rows).cuda()
+    padded = native.tile_rows(m)
+    q_tiles = empty(torch, (padded * k,), torch.int8)
+    s_tiles = empty(torch, (k // 256 * padded,), torch.float32)
+    native.bf8l_tiles(dx, m, k, q_tiles, s_tiles)
+    q_rows = empty(torch, (m, k), torch.int8)
+    s_rows = empty(torch, (m, k // 256), torch.float32)
+    native.bf8l(dx, m, k, q_rows, s_rows)
+    y = empty(torch, (m, n), torch.int16)
+    for q, s, path in ((q_tiles, s_tiles, native.PATH_GEMM_TILES), (q_rows, s_rows, native.PATH_GEMM)):
+        y.zero_()
+        linear.apply_quantized(q, s, m, y, path=path)
+        assert np.array_equal(host(y.index_select(0, index)), expected)
+    skip = bf16_bits(rng.standard_normal((rows.size, n)).astype(np.float32))
+    y.zero_()
+    y.index_copy_(0, index, dev(torch, skip))
+    linear.apply_quantized(q_tiles, s_tiles, m, y, residual=y, path=native.PATH_GEMM_TILES)
+    with_skip = np.array([[oracle.add_bf16(int(a), int(b)) for a, b in zip(r1, r2)]
+                          for r1, r2 in zip(skip, expected)], np.uint16)
+    assert np.array_equal(host(y.index_select(0, index)), with_skip)
+    del y, q_tiles, q_rows
+    torch.cuda.empty_cache()
+
+
 def test_gemm_repeatable(torch, native):
     """Two launches of the persistent GEMM give identical bytes."""
     rng = np.random.default_rng(8)
