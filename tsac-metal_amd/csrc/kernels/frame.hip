@@ -28,6 +28,21 @@ constexpr int max_books = 16;  // codebook positions of one frame
 // clocks and makes one device-scope load): seconds, far beyond any real wait.
 constexpr unsigned spin_limit = 1u << 22;
 
+// Workgroup barrier for hand-offs between this workgroup's waves through LDS.
+// __syncthreads() would also wait for the wave's outstanding global loads and
+// stores (s_waitcnt vmcnt(0)): the next job's weight prefetch and the words
+// just published would then delay every barrier by a memory round trip. Jobs
+// pass nothing between their waves through global memory, so waiting for the
+// wave's LDS accesses (lgkmcnt(0)) is all a barrier needs; the empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("" ::: "memory");
+    wait_shared_memory();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ------------------------------------------------------------------ exchange words
 
 struct Exchange
@@ -425,7 +440,7 @@ template <int V> constexpr int projection_lds()
 }
 
 // One 64-row tile of a projection for M lanes (decode.hip fused_linear_kernel).
-template <int V, In I, Out O>
+template <int V, In I, Out O, bool Pipelined = true>
 __device__ __noinline__ void project_tile(const Projection& job, int M, int tile, const Exchange& exchange, uint32_t* error,
                                           uint8_t* lds)
 {
@@ -465,6 +480,7 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
     constexpr int waves_per_block = blocks >= frame_waves ? 1 : frame_waves / blocks;
     constexpr int wave_segments = segments / waves_per_block;
     constexpr int rounds = blocks > frame_waves ? blocks / frame_waves : 1;
+    constexpr bool pipelined = Pipelined && rounds == 1;
     int8_t* q = reinterpret_cast<int8_t*>(lds);
     float* scales = reinterpret_cast<float*>(lds + max_lanes * K);
     int* dots = reinterpret_cast<int*>(lds + max_lanes * K + max_lanes * blocks * 4);
@@ -517,168 +533,187 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
             load_values<V>(p.beta + lane * V, norm_bias);
         }
     }
-    __syncthreads(); // the previous job's readers of LDS are done
+    lds_barrier(); // the previous job's readers of LDS are done
 
-    // 2. Inputs: one row per wave, quantised into LDS.
-    if (warp < M)
+    // Phases 2-4 for lanes [m0, m1). Pipelined tiles run them one lane at a
+    // time in lane order, so lane m's output is published as soon as lane m's
+    // input is in, without waiting for the later lanes (whose inputs come
+    // later when they follow the range decoder's stream order); the weights
+    // stay in registers across the lanes, so this needs a single round.
+    const auto run_lanes = [&](int m0, int m1)
     {
-        uint16_t v[V];
-        const std::size_t first = std::size_t(warp) * K + lane * V;
-        if constexpr (I == In::words || I == In::words_norm)
+        // 2. Inputs: one row per wave (wave m reads lane m), quantised into LDS.
+        if (warp >= m0 && warp < m1)
         {
-            take_row<V>(p.x, first, x, v);
-            if constexpr (I == In::words_norm)
+            uint16_t v[V];
+            const std::size_t first = std::size_t(warp) * K + lane * V;
+            if constexpr (I == In::words || I == In::words_norm)
             {
-                layer_norm_values<V>(v, norm_gain, norm_bias);
-            }
-        }
-        else if constexpr (I == In::embed_sum)
-        {
-            // src/common/cpu_transformer.tpp:205-224: copy book 0, add later books in order.
-            const uint16_t* t = p.tokens + std::size_t(warp) * p.token_stride;
-            const int t0 = min(int(t[0]), p.alphabet - 1);
-            load_row<V>(p.embeddings + std::size_t(t0) * K + lane * V, v);
-            for (int b = 1; b < p.books; ++b)
-            {
-                const int tb = min(int(t[b]), p.alphabet - 1);
-                uint16_t e[V];
-                load_row<V>(p.embeddings + (std::size_t(b) * p.alphabet + tb) * K + lane * V, e);
-#pragma unroll
-                for (int i = 0; i < V; ++i)
+                take_row<V>(p.x, first, x, v);
+                if constexpr (I == In::words_norm)
                 {
-                    v[i] = float_to_bf16(bf16_to_float(v[i]) + bf16_to_float(e[i]));
+                    layer_norm_values<V>(v, norm_gain, norm_bias);
                 }
             }
-        }
-        else
-        {
-            const int token = min(int(take(p.token_words, warp, x) & 0xffffu), p.alphabet - 1);
-            load_row<V>(p.embeddings + (std::size_t(p.book) * p.alphabet + token) * K + lane * V, v);
-            if (p.prefix_in)
+            else if constexpr (I == In::embed_sum)
             {
-                uint16_t prev[V];
-                take_row<V>(p.prefix_in, first, x, prev);
-#pragma unroll
-                for (int i = 0; i < V; ++i)
+                // src/common/cpu_transformer.tpp:205-224: copy book 0, add later books in order.
+                const uint16_t* t = p.tokens + std::size_t(warp) * p.token_stride;
+                const int t0 = min(int(t[0]), p.alphabet - 1);
+                load_row<V>(p.embeddings + std::size_t(t0) * K + lane * V, v);
+                for (int b = 1; b < p.books; ++b)
                 {
-                    v[i] = float_to_bf16(bf16_to_float(prev[i]) + bf16_to_float(v[i]));
+                    const int tb = min(int(t[b]), p.alphabet - 1);
+                    uint16_t e[V];
+                    load_row<V>(p.embeddings + (std::size_t(b) * p.alphabet + tb) * K + lane * V, e);
+#pragma unroll
+                    for (int i = 0; i < V; ++i)
+                    {
+                        v[i] = float_to_bf16(bf16_to_float(v[i]) + bf16_to_float(e[i]));
+                    }
                 }
             }
-            if (tile == 0)
+            else
             {
-                give_row<V>(p.prefix_out, first, x, v);
+                const int token = min(int(take(p.token_words, warp, x) & 0xffffu), p.alphabet - 1);
+                load_row<V>(p.embeddings + (std::size_t(p.book) * p.alphabet + token) * K + lane * V, v);
+                if (p.prefix_in)
+                {
+                    uint16_t prev[V];
+                    take_row<V>(p.prefix_in, first, x, prev);
+#pragma unroll
+                    for (int i = 0; i < V; ++i)
+                    {
+                        v[i] = float_to_bf16(bf16_to_float(prev[i]) + bf16_to_float(v[i]));
+                    }
+                }
+                if (tile == 0)
+                {
+                    give_row<V>(p.prefix_out, first, x, v);
+                }
+            }
+            bf8l_lane<V>(v, lane, q + warp * K, scales + warp * blocks, error);
+        }
+        // The residual rows come from an earlier job than the inputs just read, so
+        // requesting them now costs no wait of its own.
+        word residual_seen = 0;
+        if constexpr (O == Out::residual_words)
+        {
+            if (column >= m0 && column < m1)
+            {
+                residual_seen = peek(p.residual, out_word);
             }
         }
-        bf8l_lane<V>(v, lane, q + warp * K, scales + warp * blocks, error);
-    }
-    // The residual rows come from an earlier job than the inputs just read, so
-    // requesting them now costs no wait of its own.
-    word residual_seen = 0;
-    if constexpr (O == Out::residual_words)
-    {
-        if (column < M)
-        {
-            residual_seen = peek(p.residual, out_word);
-        }
-    }
-    __syncthreads();
+        lds_barrier();
 
-    // 3. Exact partial dots.
+        // 3. Exact partial dots.
 #pragma unroll
-    for (int r = 0; r < rounds; ++r)
-    {
-        const int b = rounds > 1 ? warp + r * frame_waves : first_block;
-        if (r > 0)
+        for (int r = 0; r < rounds; ++r)
         {
-            const int8_t* base = p.w.values + tile_offset(tile, b, 0, blocks) + lane * 16;
-#pragma unroll
-            for (int s = 0; s < wave_segments; ++s)
+            const int b = rounds > 1 ? warp + r * frame_waves : first_block;
+            if (r > 0)
             {
-                w[s] = load16(base + s * tile_rows * 16);
+                const int8_t* base = p.w.values + tile_offset(tile, b, 0, blocks) + lane * 16;
+#pragma unroll
+                for (int s = 0; s < wave_segments; ++s)
+                {
+                    w[s] = load16(base + s * tile_rows * 16);
+                }
+            }
+            const int slot = b * waves_per_block + (rounds > 1 ? 0 : warp % waves_per_block);
+            for (int m = m0; m < m1; ++m)
+            {
+                const uint4* xq = reinterpret_cast<const uint4*>(q + m * K + b * 256 + first_segment * 16);
+                int dot = 0;
+#pragma unroll
+                for (int s = 0; s < wave_segments; ++s)
+                {
+                    const uint4 u = xq[s];
+                    dot = __builtin_amdgcn_sdot4(int(w[s].x), int(u.x), dot, false);
+                    dot = __builtin_amdgcn_sdot4(int(w[s].y), int(u.y), dot, false);
+                    dot = __builtin_amdgcn_sdot4(int(w[s].z), int(u.z), dot, false);
+                    dot = __builtin_amdgcn_sdot4(int(w[s].w), int(u.w), dot, false);
+                }
+                dots[(slot * max_lanes + m) * tile_rows + lane] = dot;
             }
         }
-        const int slot = b * waves_per_block + (rounds > 1 ? 0 : warp % waves_per_block);
+        lds_barrier();
+
+        // 4. Ordered chain per (row pair, column), then the output.
+        if (column < m0 || column >= m1)
+        {
+            return;
+        }
+        const int m = column;
+        float sum0 = 0.0f, sum1 = 0.0f;
+#pragma unroll
+        for (int b = 0; b < blocks; ++b)
+        {
+            int d0 = 0, d1 = 0;
+#pragma unroll
+            for (int s = 0; s < waves_per_block; ++s)
+            {
+                const int* d = dots + ((b * waves_per_block + s) * max_lanes + m) * tile_rows + 2 * pair;
+                d0 += d[0];
+                d1 += d[1];
+            }
+            const float as = scales[m * blocks + b];
+            const float scale0 = ws0[b] * as;
+            const float scale1 = ws1[b] * as;
+            sum0 = __builtin_fmaf(float(d0), scale0, sum0);
+            sum1 = __builtin_fmaf(float(d1), scale1, sum1);
+        }
+        uint16_t y0 = float_to_bf16(sum0 + bias0);
+        uint16_t y1 = float_to_bf16(sum1 + bias1);
+        if constexpr (O == Out::residual_words)
+        {
+            const uint32_t r = settle(p.residual, out_word, residual_seen, x);
+            y0 = float_to_bf16(bf16_to_float(uint16_t(r & 0xffff)) + bf16_to_float(y0));
+            y1 = float_to_bf16(bf16_to_float(uint16_t(r >> 16)) + bf16_to_float(y1));
+        }
+        else if constexpr (O == Out::residual_row)
+        {
+            y0 = float_to_bf16(bf16_to_float(p.residual_row[n0]) + bf16_to_float(y0));
+            y1 = float_to_bf16(bf16_to_float(p.residual_row[n0 + 1]) + bf16_to_float(y1));
+        }
+        else if constexpr (O == Out::gelu)
+        {
+            y0 = gelu_bf16(y0);
+            y1 = gelu_bf16(y1);
+        }
+        else if constexpr (O == Out::qkv)
+        {
+            const int width = p.width;
+            if (n0 < 2 * width && p.rotations)
+            {
+                // rotate() of step_ops.hpp on the prefetched coefficients.
+                const float cosine = bf16_to_float(uint16_t(rotation & 0xffff)), sine = bf16_to_float(uint16_t(rotation >> 16));
+                const float re = bf16_to_float(y0), im = bf16_to_float(y1);
+                const float im_sine = im * sine;
+                const float re_sine = re * sine;
+                y0 = float_to_bf16(__builtin_fmaf(re, cosine, -im_sine));
+                y1 = float_to_bf16(__builtin_fmaf(im, cosine, re_sine));
+            }
+            if (p.keys && n0 >= width)
+            {
+                uint16_t* cache = n0 < 2 * width ? p.keys + (n0 - width) : p.values + (n0 - 2 * width);
+                *reinterpret_cast<uint32_t*>(cache + std::size_t(m) * p.lane_stride + std::size_t(p.position) * width) =
+                    y0 | (uint32_t(y1) << 16);
+            }
+        }
+        publish(p.y, out_word, y0 | (uint32_t(y1) << 16), x.epoch);
+    };
+    if constexpr (pipelined)
+    {
         for (int m = 0; m < M; ++m)
         {
-            const uint4* xq = reinterpret_cast<const uint4*>(q + m * K + b * 256 + first_segment * 16);
-            int dot = 0;
-#pragma unroll
-            for (int s = 0; s < wave_segments; ++s)
-            {
-                const uint4 u = xq[s];
-                dot = __builtin_amdgcn_sdot4(int(w[s].x), int(u.x), dot, false);
-                dot = __builtin_amdgcn_sdot4(int(w[s].y), int(u.y), dot, false);
-                dot = __builtin_amdgcn_sdot4(int(w[s].z), int(u.z), dot, false);
-                dot = __builtin_amdgcn_sdot4(int(w[s].w), int(u.w), dot, false);
-            }
-            dots[(slot * max_lanes + m) * tile_rows + lane] = dot;
+            run_lanes(m, m + 1);
         }
     }
-    __syncthreads();
-
-    // 4. Ordered chain per (row pair, column), then the output.
-    if (column >= M)
+    else
     {
-        return;
+        run_lanes(0, M);
     }
-    const int m = column;
-    float sum0 = 0.0f, sum1 = 0.0f;
-#pragma unroll
-    for (int b = 0; b < blocks; ++b)
-    {
-        int d0 = 0, d1 = 0;
-#pragma unroll
-        for (int s = 0; s < waves_per_block; ++s)
-        {
-            const int* d = dots + ((b * waves_per_block + s) * max_lanes + m) * tile_rows + 2 * pair;
-            d0 += d[0];
-            d1 += d[1];
-        }
-        const float as = scales[m * blocks + b];
-        const float scale0 = ws0[b] * as;
-        const float scale1 = ws1[b] * as;
-        sum0 = __builtin_fmaf(float(d0), scale0, sum0);
-        sum1 = __builtin_fmaf(float(d1), scale1, sum1);
-    }
-    uint16_t y0 = float_to_bf16(sum0 + bias0);
-    uint16_t y1 = float_to_bf16(sum1 + bias1);
-    if constexpr (O == Out::residual_words)
-    {
-        const uint32_t r = settle(p.residual, out_word, residual_seen, x);
-        y0 = float_to_bf16(bf16_to_float(uint16_t(r & 0xffff)) + bf16_to_float(y0));
-        y1 = float_to_bf16(bf16_to_float(uint16_t(r >> 16)) + bf16_to_float(y1));
-    }
-    else if constexpr (O == Out::residual_row)
-    {
-        y0 = float_to_bf16(bf16_to_float(p.residual_row[n0]) + bf16_to_float(y0));
-        y1 = float_to_bf16(bf16_to_float(p.residual_row[n0 + 1]) + bf16_to_float(y1));
-    }
-    else if constexpr (O == Out::gelu)
-    {
-        y0 = gelu_bf16(y0);
-        y1 = gelu_bf16(y1);
-    }
-    else if constexpr (O == Out::qkv)
-    {
-        const int width = p.width;
-        if (n0 < 2 * width && p.rotations)
-        {
-            // rotate() of step_ops.hpp on the prefetched coefficients.
-            const float cosine = bf16_to_float(uint16_t(rotation & 0xffff)), sine = bf16_to_float(uint16_t(rotation >> 16));
-            const float re = bf16_to_float(y0), im = bf16_to_float(y1);
-            const float im_sine = im * sine;
-            const float re_sine = re * sine;
-            y0 = float_to_bf16(__builtin_fmaf(re, cosine, -im_sine));
-            y1 = float_to_bf16(__builtin_fmaf(im, cosine, re_sine));
-        }
-        if (p.keys && n0 >= width)
-        {
-            uint16_t* cache = n0 < 2 * width ? p.keys + (n0 - width) : p.values + (n0 - 2 * width);
-            *reinterpret_cast<uint32_t*>(cache + std::size_t(m) * p.lane_stride + std::size_t(p.position) * width) =
-                y0 | (uint32_t(y1) << 16);
-        }
-    }
-    publish(p.y, out_word, y0 | (uint32_t(y1) << 16), x.epoch);
 }
 
 // ------------------------------------------------------------------ attention job
@@ -806,7 +841,7 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
 
     // 1. Stage the query and the exchanged rows: word i of the query is i < HW/2;
     //    then row r's key words, then its value words.
-    __syncthreads(); // the previous job's readers of LDS are done
+    lds_barrier(); // the previous job's readers of LDS are done
     {
         constexpr int per_thread = (HW / 2 + max_books * row_words + frame_threads - 1) / frame_threads;
         const int total = HW / 2 + exchanged * row_words;
@@ -838,7 +873,7 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // The value word of staged row r for this lane's columns.
     const auto staged_value = [&](int r) -> uint32_t
@@ -981,7 +1016,7 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
         }
         __builtin_amdgcn_wave_barrier();
     }
-    __syncthreads();
+    lds_barrier();
     if (warp != 0)
     {
         return;
@@ -1084,7 +1119,7 @@ __device__ __noinline__ void condition_rows(const word* in, const uint16_t* gain
 // ------------------------------------------------------------------ sampling job
 
 constexpr int window = 256;
-constexpr int draw_lds = max_lanes * 1024 * 4 + max_lanes * 1024 * 2 + max_lanes * 64 * 2 + window + 2 * max_lanes * 4;
+constexpr int draw_lds = max_lanes * 1024 * 4 + max_lanes * 1024 * 2 + max_lanes * 64 * 2 + window + 3 * max_lanes * 4;
 
 struct Draw
 {
@@ -1101,9 +1136,9 @@ struct Draw
     unsigned long long payload_bytes = 0;
 };
 
-// Softmax, masses and top decisions per lane (one wave each), then wave 0
-// decodes the lanes' symbols in stream order with the decoder held in `state`
-// (LDS) (decode.hip sample_kernel).
+// Softmax, masses and top decisions per lane (one wave each); wave 0 decodes
+// the lanes' symbols in stream order with the decoder held in `state` (LDS)
+// (decode.hip sample_kernel), each once its lane's wave has released it.
 __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* state, const Exchange& exchange,
                                          uint32_t* error, uint8_t* lds)
 {
@@ -1130,6 +1165,7 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
     uint8_t* bytes = lds + max_lanes * (1024 * 6 + 128);                                  // [window]
     int* valid = reinterpret_cast<int*>(lds + max_lanes * (1024 * 6 + 128) + window);     // [8]
     int* rows = valid + max_lanes;                                                 // [8]
+    int* ready = rows + max_lanes;                                                  // [8]
     const int lane = threadIdx.x % wave, warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
     const bool active = warp < M;
     const bool decoding = a.known == nullptr;
@@ -1138,12 +1174,27 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
     {
         row = a.row_base[warp] + a.step * a.step_stride + a.book;
     }
-    __syncthreads(); // the previous job's readers of LDS are done; `state` is current
-    uint32_t byte = 0;
-    const unsigned long long base_offset = decoding ? state->offset : 0;
-    if (decoding && threadIdx.x < window && base_offset + threadIdx.x < a.payload_bytes)
+    lds_barrier(); // the previous job's readers of LDS are done; `state` is current
+    if (threadIdx.x < max_lanes)
     {
-        byte = a.payload[base_offset + threadIdx.x];
+        ready[threadIdx.x] = 0;
+    }
+    lds_barrier();
+    // Wave 0 decodes, so it stages the payload window itself (zeros past the end).
+    const unsigned long long base_offset = decoding ? state->offset : 0;
+    if (warp == 0)
+    {
+        uint32_t four = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const unsigned long long at = base_offset + uint32_t(lane * 4 + i);
+            if (decoding && at < a.payload_bytes)
+            {
+                four |= uint32_t(a.payload[at]) << (8 * i);
+            }
+        }
+        reinterpret_cast<uint32_t*>(bytes)[lane] = four;
     }
     if (active)
     {
@@ -1198,21 +1249,27 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
                 valid[warp] = ok;
             }
         }
+        // Lane `warp`'s row, masses and decisions are in LDS: release them to wave 0.
+        if (lane == 0)
+        {
+            __hip_atomic_store(ready + warp, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
     }
-    if (threadIdx.x < window)
-    {
-        bytes[threadIdx.x] = uint8_t(byte);
-    }
-    __syncthreads();
     if (warp != 0)
     {
         return;
     }
-    // Wave 0 decodes the lanes' symbols in stream order (decode.hip sample_kernel).
+    // Wave 0 decodes the lanes' symbols in stream order (decode.hip sample_kernel),
+    // each as soon as its lane's masses are in, and publishes each token at once,
+    // so the next book of lane w can start while the later lanes are decoded.
     DecoderState s = decoding ? *state : DecoderState{};
     const ByteWindow staged{bytes, window, base_offset, a.payload, a.payload_bytes};
     for (int w = 0; w < M; ++w)
     {
+        while (__hip_atomic_load(ready + w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+        {
+            __builtin_amdgcn_s_sleep(1);
+        }
         const int r = __builtin_amdgcn_readfirstlane(rows[w]);
         int token;
         if (!decoding)
@@ -1309,6 +1366,10 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
         const int member = me - group_base[kind];
         return member >= 0 && member < group_size[kind] ? member : G * max_lanes * 64;
     };
+    // Whether this workgroup takes tiles of `kind`. A job block is skipped whole
+    // when it does not: building a job reads the model tables from memory, which
+    // would put a round trip between every two jobs of the workgroup's own kind.
+    const auto member = [&](int kind) { return first_tile(kind) < kind_tiles[kind]; };
     const auto linear = [&](bool temporal, int layer, int op) -> const DeviceLinear&
     { return model.linears[(temporal ? 0 : 4 * TL) + 4 * layer + op]; };
     const auto norm = [&](bool temporal, int layer, bool mlp) { return (temporal ? 0 : 2 * TL + 1) + 2 * layer + (mlp ? 1 : 0); };
@@ -1322,6 +1383,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
     const auto run_layer = [&](bool temporal, int layer, std::size_t in, std::size_t qkv, std::size_t att,
                                std::size_t mid, std::size_t hid, std::size_t output, const Attend& attention)
     {
+        if (member(Kind::qkv))
         {
             Projection p;
             p.w = linear(temporal, layer, 0);
@@ -1348,6 +1410,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
         {
             attend_item<HW>(attention, t, x, lds);
         }
+        if (member(Kind::out))
         {
             Projection p;
             p.w = linear(temporal, layer, 1);
@@ -1359,6 +1422,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
                 project_tile<VW, In::words, Out::residual_words>(p, M, t, x, a.error, lds);
             }
         }
+        if (member(Kind::up))
         {
             Projection p;
             p.w = linear(temporal, layer, 2);
@@ -1371,6 +1435,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
                 project_tile<VW, In::words_norm, Out::gelu>(p, M, t, x, a.error, lds);
             }
         }
+        if (member(Kind::down))
         {
             Projection p;
             p.w = linear(temporal, layer, 3);
@@ -1385,6 +1450,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
     };
 
     // Temporal stack: feedback embeddings of the previous frame, then layers.
+    if (member(Kind::embed))
     {
         Projection p;
         p.w = temporal_projection;
@@ -1421,7 +1487,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
     }
     for (int b = 0; b < C; ++b)
     {
-        if (b > 0)
+        if (b > 0 && member(Kind::prefix))
         {
             Projection p;
             p.w = codebook_projection;
@@ -1451,6 +1517,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
             run_layer(false, l, L.c_x(b, l), L.c_qkv(b, l), L.c_att(b, l), L.c_mid(b, l), L.c_hid(b, l),
                       L.c_x(b, l + 1), at);
         }
+        if (member(Kind::head))
         {
             Projection p;
             p.w = output_projection;
@@ -1484,7 +1551,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
     }
     if (me == sampler && a.known == nullptr)
     {
-        __syncthreads();
+        lds_barrier();
         if (threadIdx.x == 0)
         {
             *a.state = decoder;
