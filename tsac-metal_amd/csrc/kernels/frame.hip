@@ -440,7 +440,7 @@ template <int V> constexpr int projection_lds()
 }
 
 // One 64-row tile of a projection for M lanes (decode.hip fused_linear_kernel).
-template <int V, In I, Out O, bool Pipelined = true>
+template <int V, In I, Out O>
 __device__ __noinline__ void project_tile(const Projection& job, int M, int tile, const Exchange& exchange, uint32_t* error,
                                           uint8_t* lds)
 {
@@ -480,7 +480,8 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
     constexpr int waves_per_block = blocks >= frame_waves ? 1 : frame_waves / blocks;
     constexpr int wave_segments = segments / waves_per_block;
     constexpr int rounds = blocks > frame_waves ? blocks / frame_waves : 1;
-    constexpr bool pipelined = Pipelined && rounds == 1;
+    // Lanes one at a time whenever the weights fit registers for all of them.
+    constexpr bool pipelined = rounds == 1;
     int8_t* q = reinterpret_cast<int8_t*>(lds);
     float* scales = reinterpret_cast<float*>(lds + max_lanes * K);
     int* dots = reinterpret_cast<int*>(lds + max_lanes * K + max_lanes * blocks * 4);

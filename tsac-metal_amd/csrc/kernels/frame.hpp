@@ -10,6 +10,10 @@
 // invalidation) is needed, and every workgroup issues its next job's weight
 // loads before it waits for that job's inputs.
 //
+// Jobs take the lanes one at a time in lane order, the order in which the range
+// decoder produces their tokens, so a lane's next codebook starts as soon as its
+// own token is known.
+//
 // Key/value rows of earlier steps come from the temporal cache (written by
 // earlier launches); the current step's rows and the whole codebook stack come
 // from exchange words. Every wait is bounded: a stalled wait raises the abort
