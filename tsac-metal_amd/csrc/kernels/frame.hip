@@ -1566,8 +1566,8 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
 
 template <int VW, int VF, int VL, int HW> void launch_frame(const FrameArgs& a, hipStream_t stream)
 {
-    static int grid = 0;
-    if (!grid)
+    static int resident = 0;
+    if (!resident)
     {
         int device = 0, units = 0, per_unit = 0;
         check_hip(hipGetDevice(&device), "hipGetDevice");
@@ -1576,8 +1576,13 @@ template <int VW, int VF, int VL, int HW> void launch_frame(const FrameArgs& a, 
                                                                frame_threads, 0),
                   "hipOccupancyMaxActiveBlocksPerMultiprocessor");
         require(units > 0 && per_unit > 0, "frame step: kernel does not fit a compute unit");
-        grid = std::min(128, units * per_unit);
+        resident = units * per_unit;
     }
+    // One workgroup per tile of every job kind (frame_kernel's groups) plus the
+    // sampler when the device holds that many; otherwise the groups shrink and
+    // workgroups take several tiles of a job.
+    const int tiles = a.width / tile_rows * 7 + a.ffn / tile_rows + a.alphabet / tile_rows + a.lanes * a.heads + 2;
+    const int grid = std::min(resident, tiles);
     FrameArgs args = a;
     void* params[] = {&args};
     // Cooperative: every workgroup waits on others, so all must be resident at
