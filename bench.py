@@ -18,6 +18,8 @@ Also measured in the same run:
   * roofline_gemm: the encode MFMA GEMM on the codebook-stack qkv shape
     (M = 30,960 rows, K = 512, N = 1536).
   * qlinear: per-launch GB/s on the K=1024, N in {1024, 4096} shapes.
+  * wide_geometry: throughput of the same round trip on the 1024-wide
+    geometry (16 x 64 heads, FFN 4096), 300 frames.
   * attention: causal multi-head attention alone (16 x 64 heads, batch 3,
     T in {256, 1290, 2580}): causal prefill TFLOP/s and one-query decode GB/s.
   * attainable: this device's streaming-read rate and int8 MFMA rate, measured
@@ -276,6 +278,29 @@ def attention_rates(torch, native, lengths=(256, 1290, 2580), batch=3, heads=16,
             "bytes": "batch*2*T*heads*head_width*2 (decode: the BF16 key and value cache)"}
 
 
+def wide_geometry(native, frames=300, batch=3):
+    """Throughput only: the same round trip on the 1024-wide geometry (width
+    1024, 16 x 64 heads, FFN 4096, 12 + 3 layers), random-init weights, on a
+    bounded sample of `frames` frames."""
+    from tsac_hip.synthetic import WIDE, random_model, random_tokens
+
+    session = native.HipModel(random_model(WIDE, seed=2)).session()
+    h = native.header(frames, batch, 1, 12)
+    tokens = random_tokens(frames, 1, 12, seed=6)
+    assert np.array_equal(session.decode(session.encode(h, tokens)), tokens)
+    t0 = time.perf_counter()
+    stream = session.encode(h, tokens)
+    t1 = time.perf_counter()
+    decoded = session.decode(stream)
+    t2 = time.perf_counter()
+    assert np.array_equal(decoded, tokens), "wide round trip failed"
+    return {"tokens_per_s": round(tokens.size / (t2 - t0), 1), "encode_s": round(t1 - t0, 4),
+            "decode_s": round(t2 - t1, 4),
+            "sample": f"encode + decode of {frames} frames x 12 codebooks, batch {batch}",
+            "geometry": {"width": WIDE.width, "heads": WIDE.heads, "head_width": WIDE.head_width,
+                         "ffn": WIDE.ffn, "layers": [WIDE.temporal_layers, WIDE.codebook_layers]}}
+
+
 def cpu_baseline(model, frames, batch):
     """The C oracle on a bounded sample of the same workload: a pack_normal +
     unpack_normal round trip of `frames` frames (same geometry, batch, books),
@@ -385,6 +410,8 @@ def main():
         result["roofline_gemm"] = roof
     if args.only in ("all", "attention"):
         result["attention"] = attention_rates(torch, native)
+    if args.only == "all" and args.geometry == "reference":
+        result["wide_geometry"] = wide_geometry(native)
     if args.only == "all":
         result["qlinear"] = qlinear_table(torch, native)
         if not args.no_cpu:
