@@ -735,11 +735,16 @@ struct Attend
     word* out = nullptr;
 };
 
+// Row stride (floats) of the codebook keys staged in fp32: 16 bytes of padding
+// move consecutive rows four banks apart, so lane r reading row r at the same
+// column hits distinct banks.
+template <int HW> constexpr int staged_key_stride = HW + 4;
+
 template <int HW> constexpr int attend_lds()
 {
-    // partial records, query words, staged exchanged rows (keys then values),
-    // each wave's block weights
-    return (max_blocks * (2 + HW) + HW / 2 + max_books * HW + frame_waves * 64) * 4;
+    // partial records, the fp32 query, staged exchanged rows (key words then
+    // value words), codebook keys in fp32, each wave's block weights
+    return (max_blocks * (2 + HW) + HW + max_books * HW + max_books * staged_key_stride<HW> + frame_waves * 64) * 4;
 }
 
 // Keeps a value in vector registers: a value every lane loads from one shared
@@ -777,10 +782,12 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
     item = uniform(item);
     constexpr int per_lane = HW / 64; // value columns per lane (adjacent)
     constexpr int row_words = HW;     // staged row: HW/2 key words, then HW/2 value words
-    float* partial = reinterpret_cast<float*>(lds); // [blocks][2 + HW]
-    uint32_t* query_words = reinterpret_cast<uint32_t*>(partial + max_blocks * (2 + HW)); // [HW/2]
-    uint32_t* staged = query_words + HW / 2; // [max_books][row_words]
-    float* weights = reinterpret_cast<float*>(staged + max_books * row_words); // [frame_waves][64]
+    constexpr int key_stride = staged_key_stride<HW>;
+    float* partial = reinterpret_cast<float*>(lds);        // [blocks][2 + HW]
+    float* query = partial + max_blocks * (2 + HW);         // [HW]
+    uint32_t* staged = reinterpret_cast<uint32_t*>(query + HW); // [max_books][row_words]
+    float* staged_keys = reinterpret_cast<float*>(staged + max_books * row_words); // [max_books][key_stride]
+    float* weights = staged_keys + max_books * key_stride; // [frame_waves][64]
     const int m = item / a.heads, head = item % a.heads;
     const int lane = threadIdx.x % wave;
     const int warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
@@ -841,7 +848,9 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
     }
 
     // 1. Stage the query and the exchanged rows: word i of the query is i < HW/2;
-    //    then row r's key words, then its value words.
+    //    then row r's key words, then its value words. The query and the keys
+    //    of codebook rows are stored as fp32 (exact: BF16 is the top half of
+    //    an fp32), so the score chains read operands without unpacking them.
     lds_barrier(); // the previous job's readers of LDS are done
     {
         constexpr int per_thread = (HW / 2 + max_books * row_words + frame_threads - 1) / frame_threads;
@@ -864,13 +873,22 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
         for (int i = 0; i < per_thread; ++i)
         {
             const int index = int(threadIdx.x) + i * frame_threads;
+            const float2 pair = make_float2(__uint_as_float(got[i] << 16), __uint_as_float(got[i] & 0xffff0000u));
             if (index < HW / 2)
             {
-                query_words[index] = got[i];
+                reinterpret_cast<float2*>(query)[index] = pair;
             }
             else if (index < total)
             {
-                staged[index - HW / 2] = got[i];
+                const int r = (index - HW / 2) / row_words, c = (index - HW / 2) % row_words;
+                if (!temporal && c < HW / 2)
+                {
+                    reinterpret_cast<float2*>(staged_keys + r * key_stride)[c] = pair;
+                }
+                else
+                {
+                    staged[index - HW / 2] = got[i];
+                }
             }
         }
     }
@@ -896,6 +914,7 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
 
     // 2. Blocks of 64 keys: wave w owns blocks w, w + waves, ...
     float* block_weights = weights + warp * 64;
+    float kept[2 + per_lane]; // the last block's maximum, total and value sums
     for (int block = warp; block < blocks; block += frame_waves)
     {
         if (block != warp)
@@ -905,7 +924,7 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
         const int start = block * 64;
         const int count = time - start < 64 ? time - start : 64;
         const int t = start + lane;
-        if (lane < count && t >= cached)
+        if (temporal && lane < count && t >= cached)
         {
             const uint4* row = reinterpret_cast<const uint4*>(staged + (t - cached) * row_words);
 #pragma unroll
@@ -923,19 +942,40 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
         {
             // Ascending coordinates (src/scalar/attention.cpp:27-35).
             float dot = 0.0f;
-#pragma unroll
-            for (int c = 0; c < HW / 8; ++c)
+            if (temporal)
             {
-                uint4 q4 = reinterpret_cast<const uint4*>(query_words)[c];
-                in_vgprs(q4);
-                const uint32_t qw[4] = {q4.x, q4.y, q4.z, q4.w};
+                // Key words in registers (cache rows and the staged last row).
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int c = 0; c < HW / 8; ++c)
                 {
-                    const uint32_t kw = key[4 * c + i];
-                    dot = __builtin_fmaf(__uint_as_float(qw[i] << 16), __uint_as_float(kw << 16), dot);
-                    dot = __builtin_fmaf(__uint_as_float(qw[i] & 0xffff0000u), __uint_as_float(kw & 0xffff0000u),
-                                         dot);
+                    float4 qa = reinterpret_cast<const float4*>(query)[2 * c];
+                    float4 qb = reinterpret_cast<const float4*>(query)[2 * c + 1];
+                    in_vgprs(qa);
+                    in_vgprs(qb);
+                    const float q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        const uint32_t kw = key[4 * c + i];
+                        dot = __builtin_fmaf(q[2 * i], __uint_as_float(kw << 16), dot);
+                        dot = __builtin_fmaf(q[2 * i + 1], __uint_as_float(kw & 0xffff0000u), dot);
+                    }
+                }
+            }
+            else
+            {
+                // Codebook keys in fp32 in LDS, row t per lane.
+                const float4* row = reinterpret_cast<const float4*>(staged_keys + t * key_stride);
+#pragma unroll
+                for (int c = 0; c < HW / 4; ++c)
+                {
+                    float4 q4 = reinterpret_cast<const float4*>(query)[c];
+                    in_vgprs(q4);
+                    const float4 k4 = row[c];
+                    dot = __builtin_fmaf(q4.x, k4.x, dot);
+                    dot = __builtin_fmaf(q4.y, k4.y, dot);
+                    dot = __builtin_fmaf(q4.z, k4.z, dot);
+                    dot = __builtin_fmaf(q4.w, k4.w, dot);
                 }
             }
             score = dot * a.scale;
@@ -1004,20 +1044,36 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
         {
             accumulate(staged_value(0), block_weights[count - 1]);
         }
-        float* record = partial + std::size_t(block) * (2 + HW);
-        if (lane == 0)
+        // The block's record: lane 0's maximum and total, this lane's value sums.
+        kept[0] = uniform(maximum);
+        kept[1] = uniform(sum);
+        kept[2] = round_values ? round_bf16(s0) : s0;
+        if constexpr (per_lane == 2)
         {
-            record[0] = maximum;
-            record[1] = sum;
+            kept[3] = round_values ? round_bf16(s1) : s1;
         }
-        record[2 + per_lane * lane] = round_values ? round_bf16(s0) : s0;
-        if (per_lane == 2)
+        if (blocks > 1)
         {
-            record[3 + per_lane * lane] = round_values ? round_bf16(s1) : s1;
+            float* record = partial + std::size_t(block) * (2 + HW);
+            if (lane == 0)
+            {
+                record[0] = kept[0];
+                record[1] = kept[1];
+            }
+#pragma unroll
+            for (int i = 0; i < per_lane; ++i)
+            {
+                record[2 + per_lane * lane + i] = kept[2 + i];
+            }
+            __builtin_amdgcn_wave_barrier();
         }
-        __builtin_amdgcn_wave_barrier();
     }
-    lds_barrier();
+    // A single block (every codebook query, and temporal ones up to 64 keys)
+    // is wave 0's own: its record stays in registers, with no barrier.
+    if (blocks > 1)
+    {
+        lds_barrier();
+    }
     if (warp != 0)
     {
         return;
@@ -1030,37 +1086,44 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
         numerator[i] = 0.0f;
     }
     float running_maximum = -__builtin_inff(), total = 0.0f;
-    if (blocks == 1 && is_finite(partial[0]))
+    const auto merge = [&](float maximum, float block_total, const float* values)
+    {
+        const float difference = maximum - running_maximum;
+        const float factor = original_exp(-__builtin_fabsf(difference));
+        const float old_scale = running_maximum > maximum ? 1.0f : factor;
+        const float new_scale = running_maximum > maximum ? factor : 1.0f;
+        const float old_total = total * old_scale;
+        total = __builtin_fmaf(block_total, new_scale, old_total);
+#pragma unroll
+        for (int i = 0; i < per_lane; ++i)
+        {
+            const float old = numerator[i] * old_scale;
+            numerator[i] = __builtin_fmaf(values[i], new_scale, old);
+        }
+        running_maximum = running_maximum < maximum ? maximum : running_maximum;
+    };
+    if (blocks == 1 && is_finite(kept[0]))
     {
         // Merging one block with a finite maximum into the empty state scales
         // the zero totals by the finite original_exp(-88): each result is the
         // block's value plus +0.
-        total = partial[1] + 0.0f;
+        total = kept[1] + 0.0f;
 #pragma unroll
         for (int i = 0; i < per_lane; ++i)
         {
-            numerator[i] = partial[2 + per_lane * lane + i] + 0.0f;
+            numerator[i] = kept[2 + i] + 0.0f;
         }
+    }
+    else if (blocks == 1)
+    {
+        merge(kept[0], kept[1], kept + 2);
     }
     else
     {
         for (int b = 0; b < blocks; ++b)
         {
             const float* record = partial + std::size_t(b) * (2 + HW);
-            const float maximum = record[0];
-            const float difference = maximum - running_maximum;
-            const float factor = original_exp(-__builtin_fabsf(difference));
-            const float old_scale = running_maximum > maximum ? 1.0f : factor;
-            const float new_scale = running_maximum > maximum ? factor : 1.0f;
-            const float old_total = total * old_scale;
-            total = __builtin_fmaf(record[1], new_scale, old_total);
-#pragma unroll
-            for (int i = 0; i < per_lane; ++i)
-            {
-                const float old = numerator[i] * old_scale;
-                numerator[i] = __builtin_fmaf(record[2 + per_lane * lane + i], new_scale, old);
-            }
-            running_maximum = running_maximum < maximum ? maximum : running_maximum;
+            merge(record[0], record[1], record + 2 + per_lane * lane);
         }
     }
     const float reciprocal = 1.0f / total;
