@@ -942,21 +942,33 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
         {
             // Ascending coordinates (src/scalar/attention.cpp:27-35).
             float dot = 0.0f;
+            // LDS operands are requested `ahead` chunks before their use: one
+            // chunk's FMAs take far less time than an LDS round trip.
+            const float4* q4 = reinterpret_cast<const float4*>(query);
             if (temporal)
             {
                 // Key words in registers (cache rows and the staged last row).
+                constexpr int chunks = HW / 4, ahead = 2;
+                float4 qs[ahead];
 #pragma unroll
-                for (int c = 0; c < HW / 8; ++c)
+                for (int c = 0; c < ahead; ++c)
                 {
-                    float4 qa = reinterpret_cast<const float4*>(query)[2 * c];
-                    float4 qb = reinterpret_cast<const float4*>(query)[2 * c + 1];
-                    in_vgprs(qa);
-                    in_vgprs(qb);
-                    const float q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+                    qs[c] = q4[c];
+                }
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
+                for (int c = 0; c < chunks; ++c)
+                {
+                    float4 qc = qs[c % ahead];
+                    if (c + ahead < chunks)
                     {
-                        const uint32_t kw = key[4 * c + i];
+                        qs[c % ahead] = q4[c + ahead];
+                    }
+                    in_vgprs(qc);
+                    const float q[4] = {qc.x, qc.y, qc.z, qc.w};
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                    {
+                        const uint32_t kw = key[2 * c + i];
                         dot = __builtin_fmaf(q[2 * i], __uint_as_float(kw << 16), dot);
                         dot = __builtin_fmaf(q[2 * i + 1], __uint_as_float(kw & 0xffff0000u), dot);
                     }
@@ -966,16 +978,29 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
             {
                 // Codebook keys in fp32 in LDS, row t per lane.
                 const float4* row = reinterpret_cast<const float4*>(staged_keys + t * key_stride);
+                constexpr int chunks = HW / 4, ahead = 4;
+                float4 qs[ahead], ks[ahead];
 #pragma unroll
-                for (int c = 0; c < HW / 4; ++c)
+                for (int c = 0; c < ahead; ++c)
                 {
-                    float4 q4 = reinterpret_cast<const float4*>(query)[c];
-                    in_vgprs(q4);
-                    const float4 k4 = row[c];
-                    dot = __builtin_fmaf(q4.x, k4.x, dot);
-                    dot = __builtin_fmaf(q4.y, k4.y, dot);
-                    dot = __builtin_fmaf(q4.z, k4.z, dot);
-                    dot = __builtin_fmaf(q4.w, k4.w, dot);
+                    qs[c] = q4[c];
+                    ks[c] = row[c];
+                }
+#pragma unroll
+                for (int c = 0; c < chunks; ++c)
+                {
+                    float4 qc = qs[c % ahead];
+                    const float4 kc = ks[c % ahead];
+                    if (c + ahead < chunks)
+                    {
+                        qs[c % ahead] = q4[c + ahead];
+                        ks[c % ahead] = row[c + ahead];
+                    }
+                    in_vgprs(qc);
+                    dot = __builtin_fmaf(qc.x, kc.x, dot);
+                    dot = __builtin_fmaf(qc.y, kc.y, dot);
+                    dot = __builtin_fmaf(qc.z, kc.z, dot);
+                    dot = __builtin_fmaf(qc.w, kc.w, dot);
                 }
             }
             score = dot * a.scale;
