@@ -108,6 +108,27 @@ def test_reference_geometry(native, oracle, reference_model):
     assert np.array_equal(session.decode(stream), tokens)
 
 
+@pytest.mark.parametrize("frames,batch", [(5, 1), (4, 2), (8, 8)])
+def test_reference_geometry_lane_counts(native, oracle, reference_model, frames, batch):
+    """The decode step's workgroup layouts at 1, 2 and 8 lanes (with 8 lanes
+    the codebook attention runs inside the out projection but the layer sets
+    are not paired; with 1 and 2 lanes both apply)."""
+    model, hip_model = reference_model
+    h = native.header(frames, batch, 1, 12)
+    tokens = random_tokens(frames, 1, 12, seed=frames + batch)
+    encode, decode = _both_passes(native, hip_model, h, tokens)
+    from oracle import header
+
+    oh = header(frames, batch, 1, 12)
+    expected = oracle.model(model).distributions(oh, tokens, threads=4)
+    assert np.array_equal(encode, decode)
+    assert np.array_equal(encode, expected)
+    session = hip_model.session()
+    stream = session.encode(h, tokens)
+    assert stream == oracle.model(model).pack_normal(oh, tokens, threads=4)
+    assert np.array_equal(session.decode(stream), tokens)
+
+
 def test_wide_geometry(native, oracle):
     """Width 1024, FFN 4096, 16 x 64 heads."""
     model = random_model(WIDE, seed=2)

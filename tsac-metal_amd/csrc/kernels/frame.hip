@@ -88,6 +88,20 @@ template <class T> __device__ __forceinline__ T* uniform(T* p)
     return reinterpret_cast<T*>(uniform(reinterpret_cast<std::size_t>(p)));
 }
 
+// Keeps a value in vector registers: a value every lane loads from one shared
+// address is otherwise kept in scalar registers, and the compiler then spills
+// such values into vector-register lanes and reads each back with readlane
+// and a wait.
+__device__ __forceinline__ void in_vgprs(float4& u)
+{
+    asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
+}
+
+// Row stride (floats) of the codebook keys staged in fp32: 16 bytes of padding
+// move consecutive rows four banks apart, so lane r reading row r at the same
+// column hits distinct banks.
+template <int HW> constexpr int staged_key_stride = HW + 4;
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -398,6 +412,7 @@ enum class In
     words_norm,       // LayerNorm of those rows
     embed_sum,        // sum of the previous frame's feedback embeddings (memory tokens)
     embed_accumulate, // prefix (words) + embedding of the previous book's token (words)
+    attention,        // codebook attention of the lane over its books (from the qkv words)
 };
 
 enum class Out
@@ -433,16 +448,245 @@ struct Projection
     int width = 0, head_width = 0;
 };
 
+// In::attention: the layer's qkv words of book 0 (book t at + t*book_words),
+// keys 0 .. time-1, and the one lane whose row the tile computes.
+struct BookAttention
+{
+    const word* qkv = nullptr;
+    std::size_t book_words = 0;
+    int time = 0, lane = 0;
+    float scale = 0.0f;
+};
+
 template <int V> constexpr int projection_lds()
 {
     constexpr int K = wave * V, blocks = K / 256, slots = blocks > frame_waves ? blocks : frame_waves;
     return max_lanes * K + max_lanes * blocks * 4 + slots * max_lanes * tile_rows * 4;
 }
 
+// ------------------------------------------------------------------ codebook attention in a projection
+
+// LDS (floats) of one wave's codebook attention head: the fp32 query, the
+// fp32 keys (padded rows), the value words and the query's weights.
+template <int HW> constexpr int book_head_floats = HW + max_books * staged_key_stride<HW> + max_books * HW / 2 + wave;
+
+// A projection computes codebook attention rows when every head has a wave of
+// its own (width / HW <= frame_waves): per-wave head regions, then the lane's
+// BF16 attention row, after the projection's own LDS.
+template <int V, int HW> constexpr bool book_attention_fits = HW > 0 && wave * V / HW <= frame_waves;
+template <int V, int HW> constexpr int book_attention_lds()
+{
+    return book_attention_fits<V, HW> ? (wave * V / HW) * book_head_floats<HW> * 4 + wave * V * 2 : 0;
+}
+
+// One codebook attention head of lane m over keys 0 .. time-1 (time <=
+// max_books: one block of attend_item, which computes the same values in the
+// same order) by one wave; the head's BF16 outputs go to row[head*HW ...].
+// The books before the current one were published long before this job, so
+// their key and value words are requested first, and only the current book's
+// query, key and value words are polled for.
+template <int HW>
+__device__ __forceinline__ void book_head(const word* qkv, std::size_t book_words, int time, int width, float scale,
+                                          int m, int head, const Exchange& x, float* scratch, uint16_t* row)
+{
+    constexpr int per_lane = HW / 64, key_stride = staged_key_stride<HW>;
+    float* query = scratch;                                                          // [HW]
+    float* keys = query + HW;                                                        // [max_books][key_stride]
+    uint32_t* values = reinterpret_cast<uint32_t*>(keys + max_books * key_stride);  // [max_books][HW/2]
+    float* weights = reinterpret_cast<float*>(values + max_books * HW / 2);         // [wave]
+    const int lane = threadIdx.x % wave;
+    const std::size_t query_word = (std::size_t(m) * 3 * width + head * HW) / 2;
+    const std::size_t key_word = query_word + width / 2, value_word = query_word + width;
+    const auto pair = [](uint32_t w) { return make_float2(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)); };
+
+    // 1. Earlier books, four at a time (one request of all their words each):
+    //    word i of book r is key word i for i < HW/2, else value word i - HW/2.
+    const int older = (time - 1) * HW;
+    constexpr int chunk_books = 4, per_thread = chunk_books * HW / wave;
+    for (int first = 0; first < older; first += chunk_books * HW)
+    {
+        uint32_t got[per_thread];
+        const auto address = [&](int i) -> const word*
+        {
+            int w = first + lane + i * wave;
+            w = w < older ? w : older - 1;
+            const int r = w / HW, c = w % HW;
+            return qkv + std::size_t(r) * book_words + (c < HW / 2 ? key_word + c : value_word + (c - HW / 2));
+        };
+        take_words<per_thread>(address, x, got);
+#pragma unroll
+        for (int i = 0; i < per_thread; ++i)
+        {
+            const int w = first + lane + i * wave;
+            const int r = w / HW, c = w % HW;
+            if (w < older)
+            {
+                if (c < HW / 2)
+                {
+                    reinterpret_cast<float2*>(keys + r * key_stride)[c] = pair(got[i]);
+                }
+                else
+                {
+                    values[r * (HW / 2) + c - HW / 2] = got[i];
+                }
+            }
+        }
+    }
+    // 2. The current book: query words, then key words, then value words.
+    {
+        constexpr int count = 3 * HW / 2, per_thread = (count + wave - 1) / wave;
+        const int r = time - 1;
+        const word* base = qkv + std::size_t(r) * book_words;
+        uint32_t got[per_thread];
+        const auto address = [&](int i) -> const word*
+        {
+            int w = lane + i * wave;
+            w = w < count ? w : count - 1;
+            return base + (w < HW / 2 ? query_word + w : w < HW ? key_word + (w - HW / 2) : value_word + (w - HW));
+        };
+        take_words<per_thread>(address, x, got);
+#pragma unroll
+        for (int i = 0; i < per_thread; ++i)
+        {
+            const int w = lane + i * wave;
+            if (w < HW / 2)
+            {
+                reinterpret_cast<float2*>(query)[w] = pair(got[i]);
+            }
+            else if (w < HW)
+            {
+                reinterpret_cast<float2*>(keys + r * key_stride)[w - HW / 2] = pair(got[i]);
+            }
+            else if (w < count)
+            {
+                values[r * (HW / 2) + w - HW] = got[i];
+            }
+        }
+    }
+    // The staged rows are read by other lanes of this wave only.
+    asm volatile("" ::: "memory");
+    wait_shared_memory();
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+
+    // 3. Scores (src/scalar/attention.cpp:27-35): lane t dots key row t with
+    //    the query in ascending coordinates; operands requested `ahead`
+    //    chunks before their use.
+    float score = -__builtin_inff();
+    if (lane < time)
+    {
+        const float4* q4 = reinterpret_cast<const float4*>(query);
+        const float4* k4 = reinterpret_cast<const float4*>(keys + lane * key_stride);
+        constexpr int chunks = HW / 4, ahead = 4;
+        float4 qs[ahead], ks[ahead];
+#pragma unroll
+        for (int c = 0; c < ahead; ++c)
+        {
+            qs[c] = q4[c];
+            ks[c] = k4[c];
+        }
+        float dot = 0.0f;
+#pragma unroll
+        for (int c = 0; c < chunks; ++c)
+        {
+            float4 qc = qs[c % ahead];
+            const float4 kc = ks[c % ahead];
+            if (c + ahead < chunks)
+            {
+                qs[c % ahead] = q4[c + ahead];
+                ks[c % ahead] = k4[c + ahead];
+            }
+            in_vgprs(qc);
+            dot = __builtin_fmaf(qc.x, kc.x, dot);
+            dot = __builtin_fmaf(qc.y, kc.y, dot);
+            dot = __builtin_fmaf(qc.z, kc.z, dot);
+            dot = __builtin_fmaf(qc.w, kc.w, dot);
+        }
+        score = dot * scale;
+    }
+    const float maximum = group_max<wave>(score);
+    float e = 0.0f;
+    if (lane < time)
+    {
+        e = original_exp(score - maximum);
+    }
+    const float sum = tree_sum<wave>(e);
+    weights[lane] = e;
+    asm volatile("" ::: "memory");
+    wait_shared_memory();
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+
+    // 4. Value sums in ascending positions (src/scalar/attention.cpp:41-52).
+    float s[per_lane];
+#pragma unroll
+    for (int i = 0; i < per_lane; ++i)
+    {
+        s[i] = 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < max_books; ++t)
+    {
+        if (t < time)
+        {
+            const float w = weights[t];
+            const uint32_t pw = values[t * (HW / 2) + (per_lane * lane) / 2];
+            if constexpr (per_lane == 2)
+            {
+                s[0] = __builtin_fmaf(__uint_as_float(pw << 16), w, s[0]);
+                s[1] = __builtin_fmaf(__uint_as_float(pw & 0xffff0000u), w, s[1]);
+            }
+            else
+            {
+                const uint32_t v = (lane & 1) ? (pw >> 16) : (pw & 0xffffu);
+                s[0] = __builtin_fmaf(__uint_as_float(v << 16), w, s[0]);
+            }
+        }
+    }
+
+    // 5. The one block merged into the empty state (src/scalar/attention.cpp:86-101).
+    const float block_maximum = uniform(maximum), block_total = uniform(sum);
+    float total, numerator[per_lane];
+    if (is_finite(block_maximum))
+    {
+        // The finite original_exp(-88) scales the zero totals: each result is
+        // the block's value plus +0.
+        total = block_total + 0.0f;
+#pragma unroll
+        for (int i = 0; i < per_lane; ++i)
+        {
+            numerator[i] = s[i] + 0.0f;
+        }
+    }
+    else
+    {
+        const float running_maximum = -__builtin_inff();
+        const float factor = original_exp(-__builtin_fabsf(block_maximum - running_maximum));
+        const float old_scale = running_maximum > block_maximum ? 1.0f : factor;
+        const float new_scale = running_maximum > block_maximum ? factor : 1.0f;
+        total = __builtin_fmaf(block_total, new_scale, 0.0f * old_scale);
+#pragma unroll
+        for (int i = 0; i < per_lane; ++i)
+        {
+            numerator[i] = __builtin_fmaf(s[i], new_scale, 0.0f * old_scale);
+        }
+    }
+    const float reciprocal = 1.0f / total;
+    if constexpr (per_lane == 2)
+    {
+        *reinterpret_cast<uint32_t*>(row + head * HW + 2 * lane) =
+            float_to_bf16(numerator[0] * reciprocal) | (uint32_t(float_to_bf16(numerator[1] * reciprocal)) << 16);
+    }
+    else
+    {
+        row[head * HW + lane] = float_to_bf16(numerator[0] * reciprocal);
+    }
+}
+
 // One 64-row tile of a projection for M lanes (decode.hip fused_linear_kernel).
-template <int V, In I, Out O>
+template <int V, In I, Out O, int HW = 0>
 __device__ __noinline__ void project_tile(const Projection& job, int M, int tile, const Exchange& exchange, uint32_t* error,
-                                          uint8_t* lds)
+                                          uint8_t* lds, const BookAttention* book_job = nullptr)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
     Projection p;
@@ -473,6 +717,15 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
     p.rotations = uniform(job.rotations);
     p.width = uniform(job.width);
     p.head_width = uniform(job.head_width);
+    BookAttention book;
+    if constexpr (I == In::attention)
+    {
+        book.qkv = uniform(book_job->qkv);
+        book.book_words = uniform(book_job->book_words);
+        book.time = uniform(book_job->time);
+        book.lane = uniform(book_job->lane);
+        book.scale = uniform(book_job->scale);
+    }
     M = uniform(M);
     tile = uniform(tile);
     error = uniform(error);
@@ -482,6 +735,8 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
     constexpr int rounds = blocks > frame_waves ? blocks / frame_waves : 1;
     // Lanes one at a time whenever the weights fit registers for all of them.
     constexpr bool pipelined = rounds == 1;
+    static_assert(I != In::attention || (pipelined && book_attention_fits<V, HW>),
+                  "attention rows: one lane at a time, a wave per head");
     int8_t* q = reinterpret_cast<int8_t*>(lds);
     float* scales = reinterpret_cast<float*>(lds + max_lanes * K);
     int* dots = reinterpret_cast<int*>(lds + max_lanes * K + max_lanes * blocks * 4);
@@ -543,8 +798,39 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
     // stay in registers across the lanes, so this needs a single round.
     const auto run_lanes = [&](int m0, int m1)
     {
-        // 2. Inputs: one row per wave (wave m reads lane m), quantised into LDS.
-        if (warp >= m0 && warp < m1)
+        // 2. Inputs: one row per wave (wave m reads lane m), quantised into LDS;
+        //    an attention row is computed by the waves together (wave h takes
+        //    head h) and quantised by wave 0.
+        if constexpr (I == In::attention)
+        {
+            constexpr int heads = K / HW;
+            float* regions = reinterpret_cast<float*>(lds + projection_lds<V>());
+            uint16_t* row = reinterpret_cast<uint16_t*>(regions + heads * book_head_floats<HW>);
+            if (warp < heads)
+            {
+                book_head<HW>(book.qkv, book.book_words, book.time, K, book.scale, m0, warp, x,
+                              regions + warp * book_head_floats<HW>, row);
+            }
+            lds_barrier();
+            if (warp == 0)
+            {
+                uint16_t v[V];
+#pragma unroll
+                for (int c = 0; c < V / 8; ++c)
+                {
+                    const uint4 u = reinterpret_cast<const uint4*>(row + lane * V)[c];
+                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        v[8 * c + 2 * i] = uint16_t(w[i] & 0xffff);
+                        v[8 * c + 2 * i + 1] = uint16_t(w[i] >> 16);
+                    }
+                }
+                bf8l_lane<V>(v, lane, q + m0 * K, scales + m0 * blocks, error);
+            }
+        }
+        else if (warp >= m0 && warp < m1)
         {
             uint16_t v[V];
             const std::size_t first = std::size_t(warp) * K + lane * V;
@@ -706,9 +992,16 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
     };
     if constexpr (pipelined)
     {
-        for (int m = 0; m < M; ++m)
+        if constexpr (I == In::attention)
         {
-            run_lanes(m, m + 1);
+            run_lanes(book.lane, book.lane + 1);
+        }
+        else
+        {
+            for (int m = 0; m < M; ++m)
+            {
+                run_lanes(m, m + 1);
+            }
         }
     }
     else
@@ -735,29 +1028,11 @@ struct Attend
     word* out = nullptr;
 };
 
-// Row stride (floats) of the codebook keys staged in fp32: 16 bytes of padding
-// move consecutive rows four banks apart, so lane r reading row r at the same
-// column hits distinct banks.
-template <int HW> constexpr int staged_key_stride = HW + 4;
-
 template <int HW> constexpr int attend_lds()
 {
     // partial records, the fp32 query, staged exchanged rows (key words then
     // value words), codebook keys in fp32, each wave's block weights
     return (max_blocks * (2 + HW) + HW + max_books * HW + max_books * staged_key_stride<HW> + frame_waves * 64) * 4;
-}
-
-// Keeps a value in vector registers: a value every lane loads from one shared
-// address is otherwise kept in scalar registers, and the compiler then spills
-// such values into vector-register lanes and reads each back with readlane
-// and a wait.
-__device__ __forceinline__ void in_vgprs(uint4& u)
-{
-    asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
-}
-__device__ __forceinline__ void in_vgprs(float4& u)
-{
-    asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
 }
 
 // One (lane, head) query over all its keys (decode.hip attention_step_kernel).
@@ -1391,7 +1666,50 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
 // V* = K/64 of the width, FFN and latent rows; HW the head width.
 template <int VW, int VF, int VL, int HW> constexpr int frame_lds()
 {
-    return std::max({projection_lds<VW>(), projection_lds<VF>(), projection_lds<VL>(), attend_lds<HW>(), draw_lds});
+    return std::max({projection_lds<VW>() + book_attention_lds<VW, HW>(), projection_lds<VF>(), projection_lds<VL>(),
+                     attend_lds<HW>(), draw_lds});
+}
+
+// How a frame step's jobs map onto `workers` workgroups (besides the sampler).
+// Every kind of job owns a group of workgroups, one per tile when they fit.
+// Two refinements, taken when the device holds their extra workgroups:
+//  * fused: a codebook layer's attention (at most max_books keys) is computed
+//    by its out-projection tiles, one workgroup per (tile, lane), instead of
+//    by a job of its own followed by a hand-off;
+//  * paired: qkv, up and down tiles (which take every lane in turn) get two
+//    sets of workgroups that alternate between consecutive layers, so a
+//    workgroup has two layers' time to finish its last lane and load the next
+//    layer's weights before that layer's first input arrives.
+struct FrameLayout
+{
+    bool fused = false, paired = false;
+    int out_tiles = 0; // tiles of an out job: one per lane when fused
+    int workgroups = 0; // workers the layout asks for
+};
+
+__host__ __device__ inline FrameLayout frame_layout(int width, int heads, int ffn, int alphabet, int lanes, int workers)
+{
+    const bool fusable = heads <= frame_waves; // a wave per head (book_attention_fits)
+    const int w = width / tile_rows, f = ffn / tile_rows;
+    // embed, qkv, attend, out, up, down, condition, prefix, head
+    const int base = w + 3 * w + lanes * heads + w + f + w + 1 + w + alphabet / tile_rows;
+    const int fused_extra = (lanes - 1) * w, paired_extra = 3 * w + f + w;
+    FrameLayout l;
+    if (fusable && base + fused_extra + paired_extra <= workers)
+    {
+        l.fused = l.paired = true;
+    }
+    else if (fusable && base + fused_extra <= workers)
+    {
+        l.fused = true;
+    }
+    else if (base + paired_extra <= workers)
+    {
+        l.paired = true;
+    }
+    l.out_tiles = l.fused ? lanes * w : w;
+    l.workgroups = base + (l.fused ? fused_extra : 0) + (l.paired ? paired_extra : 0);
+    return l;
 }
 
 template <int VW, int VF, int VL, int HW>
@@ -1430,35 +1748,51 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
         head,
         kinds
     };
-    const int kind_tiles[kinds] = {width / tile_rows, 3 * width / tile_rows, M * a.heads, width / tile_rows,
+    const FrameLayout layout = frame_layout(width, a.heads, a.ffn, a.alphabet, M, G - 1);
+    const int kind_tiles[kinds] = {width / tile_rows, 3 * width / tile_rows, M * a.heads, layout.out_tiles,
                                    a.ffn / tile_rows, width / tile_rows, 1, width / tile_rows,
                                    a.alphabet / tile_rows};
+    const auto sets = [&](int kind)
+    { return layout.paired && (kind == Kind::qkv || kind == Kind::up || kind == Kind::down) ? 2 : 1; };
     int group_size[kinds], group_base[kinds];
     {
         const int workers = G - 1;
         int total = 0;
         for (int k = 0; k < kinds; ++k)
         {
-            total += kind_tiles[k];
+            total += kind_tiles[k] * sets(k);
         }
         int base = 1;
         for (int k = 0; k < kinds; ++k)
         {
-            group_size[k] = total <= workers ? kind_tiles[k] : max(1, kind_tiles[k] * (workers - kinds) / total);
+            group_size[k] = total <= workers ? kind_tiles[k] * sets(k)
+                                             : max(1, kind_tiles[k] * (workers - kinds) / total);
             group_base[k] = base;
             base += group_size[k];
         }
     }
-    // This workgroup's first tile of a job of `kind` (>= any tile count if none).
-    const auto first_tile = [&](int kind)
+    // This workgroup's first tile of a job of `kind` (>= any tile count if
+    // none); `parity` picks the set of a paired kind (the layer's parity).
+    const auto first_tile = [&](int kind, int parity = 0)
     {
+        const int none = G * max_lanes * 64;
         const int member = me - group_base[kind];
-        return member >= 0 && member < group_size[kind] ? member : G * max_lanes * 64;
+        if (member < 0 || member >= group_size[kind])
+        {
+            return none;
+        }
+        if (sets(kind) == 1)
+        {
+            return member;
+        }
+        return member / kind_tiles[kind] == parity ? member % kind_tiles[kind] : none;
     };
+    // Distance between a workgroup's tiles of one job.
+    const auto step = [&](int kind) { return group_size[kind] / sets(kind); };
     // Whether this workgroup takes tiles of `kind`. A job block is skipped whole
     // when it does not: building a job reads the model tables from memory, which
     // would put a round trip between every two jobs of the workgroup's own kind.
-    const auto member = [&](int kind) { return first_tile(kind) < kind_tiles[kind]; };
+    const auto member = [&](int kind, int parity = 0) { return first_tile(kind, parity) < kind_tiles[kind]; };
     const auto linear = [&](bool temporal, int layer, int op) -> const DeviceLinear&
     { return model.linears[(temporal ? 0 : 4 * TL) + 4 * layer + op]; };
     const auto norm = [&](bool temporal, int layer, bool mlp) { return (temporal ? 0 : 2 * TL + 1) + 2 * layer + (mlp ? 1 : 0); };
@@ -1469,10 +1803,10 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
 
     // One stack layer; `x_of`... words of the layer's input, qkv, attention,
     // mid residual, hidden and output.
-    const auto run_layer = [&](bool temporal, int layer, std::size_t in, std::size_t qkv, std::size_t att,
+    const auto run_layer = [&](bool temporal, int layer, int parity, std::size_t in, std::size_t qkv, std::size_t att,
                                std::size_t mid, std::size_t hid, std::size_t output, const Attend& attention)
     {
-        if (member(Kind::qkv))
+        if (member(Kind::qkv, parity))
         {
             Projection p;
             p.w = linear(temporal, layer, 0);
@@ -1490,14 +1824,21 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
                 p.position = a.position;
                 p.rotations = model.rotations;
             }
-            for (int t = first_tile(Kind::qkv); t < int(p.w.N) / tile_rows; t += group_size[Kind::qkv])
+            for (int t = first_tile(Kind::qkv, parity); t < int(p.w.N) / tile_rows; t += step(Kind::qkv))
             {
                 project_tile<VW, In::words_norm, Out::qkv>(p, M, t, x, a.error, lds);
             }
         }
-        for (int t = first_tile(Kind::attend); t < M * a.heads; t += group_size[Kind::attend])
+        // Temporal attention is a job of its own; with the fused layout a
+        // codebook layer's (at most max_books keys) is computed by each
+        // out-projection tile itself.
+        const bool fused = !temporal && layout.fused;
+        if (!fused)
         {
-            attend_item<HW>(attention, t, x, lds);
+            for (int t = first_tile(Kind::attend); t < M * a.heads; t += group_size[Kind::attend])
+            {
+                attend_item<HW>(attention, t, x, lds);
+            }
         }
         if (member(Kind::out))
         {
@@ -1506,12 +1847,31 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
             p.x = words + att;
             p.residual = words + in;
             p.y = words + mid;
-            for (int t = first_tile(Kind::out); t < int(p.w.N) / tile_rows; t += group_size[Kind::out])
+            if (!fused)
             {
-                project_tile<VW, In::words, Out::residual_words>(p, M, t, x, a.error, lds);
+                for (int t = first_tile(Kind::out); t < int(p.w.N) / tile_rows; t += group_size[Kind::out])
+                {
+                    project_tile<VW, In::words, Out::residual_words>(p, M, t, x, a.error, lds);
+                }
+            }
+            else if constexpr (book_attention_fits<VW, HW>)
+            {
+                // One lane per workgroup: each stages its lane's earlier books
+                // while it waits, and no lane waits for another's attention.
+                BookAttention book;
+                book.qkv = attention.qkv;
+                book.book_words = attention.book_words;
+                book.time = attention.time;
+                book.scale = attention.scale;
+                const int tiles = int(p.w.N) / tile_rows;
+                for (int t = first_tile(Kind::out); t < M * tiles; t += group_size[Kind::out])
+                {
+                    book.lane = t / tiles;
+                    project_tile<VW, In::attention, Out::residual_words, HW>(p, M, t % tiles, x, a.error, lds, &book);
+                }
             }
         }
-        if (member(Kind::up))
+        if (member(Kind::up, parity))
         {
             Projection p;
             p.w = linear(temporal, layer, 2);
@@ -1519,19 +1879,19 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
             p.gain = model.gain[norm(temporal, layer, true)];
             p.beta = model.bias[norm(temporal, layer, true)];
             p.y = words + hid;
-            for (int t = first_tile(Kind::up); t < int(p.w.N) / tile_rows; t += group_size[Kind::up])
+            for (int t = first_tile(Kind::up, parity); t < int(p.w.N) / tile_rows; t += step(Kind::up))
             {
                 project_tile<VW, In::words_norm, Out::gelu>(p, M, t, x, a.error, lds);
             }
         }
-        if (member(Kind::down))
+        if (member(Kind::down, parity))
         {
             Projection p;
             p.w = linear(temporal, layer, 3);
             p.x = words + hid;
             p.residual = words + mid;
             p.y = words + output;
-            for (int t = first_tile(Kind::down); t < int(p.w.N) / tile_rows; t += group_size[Kind::down])
+            for (int t = first_tile(Kind::down, parity); t < int(p.w.N) / tile_rows; t += step(Kind::down))
             {
                 project_tile<VF, In::words, Out::residual_words>(p, M, t, x, a.error, lds);
             }
@@ -1566,7 +1926,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
         at.lane_stride = a.lane_stride;
         at.qkv = words + L.t_qkv(l);
         at.out = words + L.t_att(l);
-        run_layer(true, l, L.t_x(l), L.t_qkv(l), L.t_att(l), L.t_mid(l), L.t_hid(l), L.t_x(l + 1), at);
+        run_layer(true, l, l % 2, L.t_x(l), L.t_qkv(l), L.t_att(l), L.t_mid(l), L.t_hid(l), L.t_x(l + 1), at);
     }
     // Book 0's input.
     if (first_tile(Kind::condition) == 0)
@@ -1603,8 +1963,8 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
             at.qkv = words + L.c_qkv(0, l);
             at.book_words = L.book;
             at.out = words + L.c_att(b, l);
-            run_layer(false, l, L.c_x(b, l), L.c_qkv(b, l), L.c_att(b, l), L.c_mid(b, l), L.c_hid(b, l),
-                      L.c_x(b, l + 1), at);
+            run_layer(false, l, (TL + b * CL + l) % 2, L.c_x(b, l), L.c_qkv(b, l), L.c_att(b, l), L.c_mid(b, l),
+                      L.c_hid(b, l), L.c_x(b, l + 1), at);
         }
         if (member(Kind::head))
         {
@@ -1666,11 +2026,11 @@ template <int VW, int VF, int VL, int HW> void launch_frame(const FrameArgs& a, 
         require(units > 0 && per_unit > 0, "frame step: kernel does not fit a compute unit");
         resident = units * per_unit;
     }
-    // One workgroup per tile of every job kind (frame_kernel's groups) plus the
-    // sampler when the device holds that many; otherwise the groups shrink and
-    // workgroups take several tiles of a job.
-    const int tiles = a.width / tile_rows * 7 + a.ffn / tile_rows + a.alphabet / tile_rows + a.lanes * a.heads + 2;
-    const int grid = std::min(resident, tiles);
+    // The workgroups of the richest layout the device holds (frame_kernel
+    // derives the same layout from the grid), plus the sampler; when not even
+    // the plain one fits, the groups shrink and workgroups take several tiles.
+    const FrameLayout layout = frame_layout(a.width, a.heads, a.ffn, a.alphabet, a.lanes, resident - 1);
+    const int grid = std::min(resident, layout.workgroups + 1);
     FrameArgs args = a;
     void* params[] = {&args};
     // Cooperative: every workgroup waits on others, so all must be resident at
