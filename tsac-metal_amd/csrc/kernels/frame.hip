@@ -485,9 +485,13 @@ template <int V, int HW> constexpr int book_attention_lds()
 // The books before the current one were published long before this job, so
 // their key and value words are requested first, and only the current book's
 // query, key and value words are polled for.
+// A thread given `residual` also requests that word as soon as the current
+// book's words are in (the residual row is the layer's input, which the qkv
+// job consumed before it published them), into `residual_seen`.
 template <int HW>
 __device__ __forceinline__ void book_head(const word* qkv, std::size_t book_words, int time, int width, float scale,
-                                          int m, int head, const Exchange& x, float* scratch, uint16_t* row)
+                                          int m, int head, const Exchange& x, float* scratch, uint16_t* row,
+                                          const word* residual, word& residual_seen)
 {
     constexpr int per_lane = HW / 64, key_stride = staged_key_stride<HW>;
     float* query = scratch;                                                          // [HW]
@@ -545,6 +549,10 @@ __device__ __forceinline__ void book_head(const word* qkv, std::size_t book_word
             return base + (w < HW / 2 ? query_word + w : w < HW ? key_word + (w - HW / 2) : value_word + (w - HW));
         };
         take_words<per_thread>(address, x, got);
+        if (residual)
+        {
+            residual_seen = peek(residual, 0);
+        }
 #pragma unroll
         for (int i = 0; i < per_thread; ++i)
         {
@@ -798,6 +806,8 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
     // stay in registers across the lanes, so this needs a single round.
     const auto run_lanes = [&](int m0, int m1)
     {
+        word residual_seen = 0;
+        bool residual_requested = false;
         // 2. Inputs: one row per wave (wave m reads lane m), quantised into LDS;
         //    an attention row is computed by the waves together (wave h takes
         //    head h) and quantised by wave 0.
@@ -808,8 +818,10 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
             uint16_t* row = reinterpret_cast<uint16_t*>(regions + heads * book_head_floats<HW>);
             if (warp < heads)
             {
+                residual_requested = O == Out::residual_words && column == m0;
                 book_head<HW>(book.qkv, book.book_words, book.time, K, book.scale, m0, warp, x,
-                              regions + warp * book_head_floats<HW>, row);
+                              regions + warp * book_head_floats<HW>, row,
+                              residual_requested ? p.residual + out_word : nullptr, residual_seen);
             }
             lds_barrier();
             if (warp == 0)
@@ -883,10 +895,9 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
         }
         // The residual rows come from an earlier job than the inputs just read, so
         // requesting them now costs no wait of its own.
-        word residual_seen = 0;
         if constexpr (O == Out::residual_words)
         {
-            if (column >= m0 && column < m1)
+            if (column >= m0 && column < m1 && !residual_requested)
             {
                 residual_seen = peek(p.residual, out_word);
             }
