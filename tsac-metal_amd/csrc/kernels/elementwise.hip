@@ -1,5 +1,5 @@
-// Row-wise LayerNorm and softmax (one wavefront per row), BF16 residual adds,
-// GELU and rotary helpers.
+// Row-wise LayerNorm (one row per workgroup, spread over its waves) and
+// softmax (one wavefront per row), BF16 residual adds, GELU and rotary helpers.
 #include "kernels.hpp"
 #include "row_ops.hpp"
 
@@ -9,23 +9,24 @@ namespace
 {
 constexpr int rows_per_block = 4;
 
-template <int V>
-__global__ __launch_bounds__(256) void layer_norm_kernel(const uint16_t* x, int rows,
-                                                         const uint16_t* __restrict__ gain,
-                                                         const uint16_t* __restrict__ bias,
-                                                         uint16_t* out)
+// One row per workgroup of Waves waves (the row layout of layer_norm_spread,
+// which the decode frame step's projections use).
+template <int Vw, int Waves>
+__global__ __launch_bounds__(Waves * 64) void layer_norm_kernel(const uint16_t* x,
+                                                                const uint16_t* __restrict__ gain,
+                                                                const uint16_t* __restrict__ bias,
+                                                                uint16_t* out)
 {
-    constexpr int width = wave * V;
-    const int lane = threadIdx.x % wave;
-    const int row = blockIdx.x * rows_per_block + threadIdx.x / wave;
-    if (row >= rows)
-    {
-        return;
-    }
-    uint16_t v[V];
-    load_row<V>(x + std::size_t(row) * width + lane * V, v);
-    layer_norm_lane<V>(v, gain, bias, lane);
-    store_row<V>(out + std::size_t(row) * width + lane * V, v);
+    constexpr int width = Waves * wave * Vw;
+    __shared__ float exchange[2 * Waves];
+    const int warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
+    const std::size_t at = std::size_t(blockIdx.x) * width + threadIdx.x * Vw;
+    uint16_t v[Vw], g[Vw], b[Vw];
+    load_row<Vw>(x + at, v);
+    load_row<Vw>(gain + threadIdx.x * Vw, g);
+    load_row<Vw>(bias + threadIdx.x * Vw, b);
+    layer_norm_spread<Vw, Waves>(v, g, b, warp, exchange);
+    store_row<Vw>(out + at, v);
 }
 
 // src/common/probability.cpp:96-122
@@ -126,20 +127,20 @@ void layer_norm_rows(const uint16_t* x, std::size_t rows, std::size_t width, con
         return;
     }
     require(rows < (std::size_t(1) << 31), "too many rows");
-    const dim3 grid(unsigned((rows + rows_per_block - 1) / rows_per_block));
+    const dim3 grid(static_cast<unsigned>(rows));
     switch (width)
     {
     case 256:
-        layer_norm_kernel<4><<<grid, 256, 0, stream>>>(x, int(rows), gain, bias, out);
+        layer_norm_kernel<1, 4><<<grid, 256, 0, stream>>>(x, gain, bias, out);
         break;
     case 512:
-        layer_norm_kernel<8><<<grid, 256, 0, stream>>>(x, int(rows), gain, bias, out);
+        layer_norm_kernel<1, 8><<<grid, 512, 0, stream>>>(x, gain, bias, out);
         break;
     case 1024:
-        layer_norm_kernel<16><<<grid, 256, 0, stream>>>(x, int(rows), gain, bias, out);
+        layer_norm_kernel<2, 8><<<grid, 512, 0, stream>>>(x, gain, bias, out);
         break;
     case 2048:
-        layer_norm_kernel<32><<<grid, 256, 0, stream>>>(x, int(rows), gain, bias, out);
+        layer_norm_kernel<4, 8><<<grid, 512, 0, stream>>>(x, gain, bias, out);
         break;
     default:
         throw Error("layer norm: width must be one of 256, 512, 1024, 2048");

@@ -28,20 +28,9 @@ constexpr int max_books = 16;  // codebook positions of one frame
 // clocks and makes one device-scope load): seconds, far beyond any real wait.
 constexpr unsigned spin_limit = 1u << 22;
 
-// Workgroup barrier for hand-offs between this workgroup's waves through LDS.
-// __syncthreads() would also wait for the wave's outstanding global loads and
-// stores (s_waitcnt vmcnt(0)): the next job's weight prefetch and the words
-// just published would then delay every barrier by a memory round trip. Jobs
-// pass nothing between their waves through global memory, so waiting for the
-// wave's LDS accesses (lgkmcnt(0)) is all a barrier needs; the empty asm
-// statements keep the compiler from moving memory accesses across it.
-__device__ __forceinline__ void lds_barrier()
-{
-    asm volatile("" ::: "memory");
-    wait_shared_memory();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
+// Jobs pass nothing between their waves through global memory, so their
+// barriers are lds_barrier() (row_ops.hpp): the next job's weight prefetch and
+// the words just published are not waited for.
 
 // ------------------------------------------------------------------ exchange words
 
@@ -314,6 +303,29 @@ __device__ __forceinline__ void take_row(const word* w, std::size_t first, const
     }
 }
 
+// This lane's Vw consecutive BF16 values from value `first` (a multiple of Vw)
+// of a word vector, once current; with Vw == 1 neighbouring lanes share a word.
+template <int Vw>
+__device__ __forceinline__ void take_values(const word* w, std::size_t first, const Exchange& x, uint16_t (&v)[Vw])
+{
+    constexpr int words = Vw < 2 ? 1 : Vw / 2;
+    uint32_t got[words];
+    take_words<words>([&](int i) -> const word* { return w + first / 2 + i; }, x, got);
+    if constexpr (Vw == 1)
+    {
+        v[0] = uint16_t((first & 1) ? got[0] >> 16 : got[0] & 0xffffu);
+    }
+    else
+    {
+#pragma unroll
+        for (int i = 0; i < words; ++i)
+        {
+            v[2 * i] = uint16_t(got[i] & 0xffffu);
+            v[2 * i + 1] = uint16_t(got[i] >> 16);
+        }
+    }
+}
+
 template <int V>
 __device__ __forceinline__ void give_row(word* w, std::size_t first, const Exchange& x, const uint16_t (&v)[V])
 {
@@ -458,10 +470,17 @@ struct BookAttention
     float scale = 0.0f;
 };
 
-template <int V> constexpr int projection_lds()
+// A projection's LDS: quantised rows, their block scales, the partial dots,
+// then the exchange words of the spread LayerNorm (2 per wave) and BF8L (1 per
+// wave).
+template <int V> constexpr int projection_exchange()
 {
     constexpr int K = wave * V, blocks = K / 256, slots = blocks > frame_waves ? blocks : frame_waves;
     return max_lanes * K + max_lanes * blocks * 4 + slots * max_lanes * tile_rows * 4;
+}
+template <int V> constexpr int projection_lds()
+{
+    return projection_exchange<V>() + 3 * frame_waves * 4;
 }
 
 // ------------------------------------------------------------------ codebook attention in a projection
@@ -745,6 +764,13 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
     constexpr bool pipelined = rounds == 1;
     static_assert(I != In::attention || (pipelined && book_attention_fits<V, HW>),
                   "attention rows: one lane at a time, a wave per head");
+    // A pipelined tile spreads each input row over its waves (row_ops.hpp), so
+    // LayerNorm and BF8L run on V / frame_waves values per lane of every wave
+    // instead of V values per lane of one.
+    constexpr int Vw = V / frame_waves;
+    constexpr bool spread = pipelined && V % frame_waves == 0 &&
+                            (I == In::words || I == In::words_norm || I == In::attention);
+    static_assert(I != In::attention || spread, "attention rows are spread");
     int8_t* q = reinterpret_cast<int8_t*>(lds);
     float* scales = reinterpret_cast<float*>(lds + max_lanes * K);
     int* dots = reinterpret_cast<int*>(lds + max_lanes * K + max_lanes * blocks * 4);
@@ -788,8 +814,13 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
         }
     }
     // LayerNorm constants of this lane's input values, before any wait.
-    uint16_t norm_gain[V], norm_bias[V];
-    if constexpr (I == In::words_norm)
+    uint16_t norm_gain[V], norm_bias[V], spread_gain[Vw > 0 ? Vw : 1], spread_bias[Vw > 0 ? Vw : 1];
+    if constexpr (I == In::words_norm && spread)
+    {
+        load_row<Vw>(p.gain + (warp * wave + lane) * Vw, spread_gain);
+        load_row<Vw>(p.beta + (warp * wave + lane) * Vw, spread_bias);
+    }
+    else if constexpr (I == In::words_norm)
     {
         if (warp < M)
         {
@@ -797,6 +828,8 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
             load_values<V>(p.beta + lane * V, norm_bias);
         }
     }
+    float* norm_exchange = reinterpret_cast<float*>(lds + projection_exchange<V>()); // [2 * frame_waves]
+    uint32_t* scale_exchange = reinterpret_cast<uint32_t*>(norm_exchange + 2 * frame_waves); // [frame_waves]
     lds_barrier(); // the previous job's readers of LDS are done
 
     // Phases 2-4 for lanes [m0, m1). Pipelined tiles run them one lane at a
@@ -808,9 +841,10 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
     {
         word residual_seen = 0;
         bool residual_requested = false;
-        // 2. Inputs: one row per wave (wave m reads lane m), quantised into LDS;
-        //    an attention row is computed by the waves together (wave h takes
-        //    head h) and quantised by wave 0.
+        // 2. Inputs, quantised into LDS: a spread row is taken, normalised and
+        //    quantised by all waves together; an attention row is computed by
+        //    them (wave h takes head h) and then quantised the same way; other
+        //    inputs take one row per wave (wave m reads lane m).
         if constexpr (I == In::attention)
         {
             constexpr int heads = K / HW;
@@ -824,23 +858,19 @@ __device__ __noinline__ void project_tile(const Projection& job, int M, int tile
                               residual_requested ? p.residual + out_word : nullptr, residual_seen);
             }
             lds_barrier();
-            if (warp == 0)
+            uint16_t v[Vw];
+            load_row<Vw>(row + (warp * wave + lane) * Vw, v);
+            bf8l_spread<Vw, frame_waves>(v, warp, q + m0 * K, scales + m0 * blocks, error, scale_exchange);
+        }
+        else if constexpr (spread)
+        {
+            uint16_t v[Vw];
+            take_values<Vw>(p.x, std::size_t(m0) * K + (warp * wave + lane) * Vw, x, v);
+            if constexpr (I == In::words_norm)
             {
-                uint16_t v[V];
-#pragma unroll
-                for (int c = 0; c < V / 8; ++c)
-                {
-                    const uint4 u = reinterpret_cast<const uint4*>(row + lane * V)[c];
-                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                    {
-                        v[8 * c + 2 * i] = uint16_t(w[i] & 0xffff);
-                        v[8 * c + 2 * i + 1] = uint16_t(w[i] >> 16);
-                    }
-                }
-                bf8l_lane<V>(v, lane, q + m0 * K, scales + m0 * blocks, error);
+                layer_norm_spread<Vw, frame_waves>(v, spread_gain, spread_bias, warp, norm_exchange);
             }
+            bf8l_spread<Vw, frame_waves>(v, warp, q + m0 * K, scales + m0 * blocks, error, scale_exchange);
         }
         else if (warp >= m0 && warp < m1)
         {

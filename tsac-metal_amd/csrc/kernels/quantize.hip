@@ -59,6 +59,31 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restric
     }
 }
 
+// BF8L of row-major rows without a prologue: one row per workgroup of Waves
+// waves (the row layout of bf8l_spread, which the decode frame step's
+// projections use).
+template <int Vw, int Waves>
+__global__ __launch_bounds__(Waves * 64) void bf8l_rows_kernel(const uint16_t* __restrict__ x,
+                                                               int8_t* __restrict__ q,
+                                                               float* __restrict__ scales,
+                                                               uint32_t* __restrict__ error)
+{
+    constexpr int K = Waves * wave * Vw;
+    __shared__ uint32_t exchange[Waves];
+    const int warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
+    uint16_t v[Vw];
+    load_row<Vw>(x + std::size_t(blockIdx.x) * K + threadIdx.x * Vw, v);
+    bf8l_spread<Vw, Waves>(v, warp, q + std::size_t(blockIdx.x) * K, scales + std::size_t(blockIdx.x) * (K / 256),
+                           error, exchange);
+}
+
+template <int Vw, int Waves>
+void launch_bf8l_rows(const uint16_t* x, std::size_t rows, int8_t* q, float* scales, uint32_t* error,
+                      hipStream_t stream)
+{
+    bf8l_rows_kernel<Vw, Waves><<<unsigned(rows), Waves * 64, 0, stream>>>(x, q, scales, error);
+}
+
 template <int V>
 void launch_quantize(const uint16_t* x, std::size_t rows, Prologue prologue, const uint16_t* gain,
                      const uint16_t* bias, int8_t* q, float* scales, uint16_t* normalized,
@@ -99,6 +124,31 @@ void quantize_rows(const uint16_t* x, std::size_t rows, std::size_t K, Prologue 
         return;
     }
     const std::size_t padded = layout == Layout::tiles ? tile_padded_rows(rows) : 0;
+    if (prologue == Prologue::none && layout == Layout::rows)
+    {
+        switch (K)
+        {
+        case 256:
+            launch_bf8l_rows<1, 4>(x, rows, q, scales, error, stream);
+            break;
+        case 512:
+            launch_bf8l_rows<1, 8>(x, rows, q, scales, error, stream);
+            break;
+        case 1024:
+            launch_bf8l_rows<2, 8>(x, rows, q, scales, error, stream);
+            break;
+        case 2048:
+            launch_bf8l_rows<4, 8>(x, rows, q, scales, error, stream);
+            break;
+        case 4096:
+            launch_bf8l_rows<8, 8>(x, rows, q, scales, error, stream);
+            break;
+        default:
+            throw Error("quantize: K must be one of 256, 512, 1024, 2048, 4096");
+        }
+        check_hip(hipGetLastError(), "bf8l launch");
+        return;
+    }
     switch (K)
     {
     case 256:

@@ -6,6 +6,25 @@
 
 namespace tsac_hip
 {
+__device__ __forceinline__ void wait_shared_memory()
+{
+    __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
+}
+
+// Workgroup barrier for hand-offs between a workgroup's waves through LDS.
+// __syncthreads() would also wait for the wave's outstanding global loads and
+// stores (s_waitcnt vmcnt(0)), such as weight prefetches and words just
+// published; waiting for the wave's LDS accesses (lgkmcnt(0)) is all an LDS
+// hand-off needs. The empty asm statements keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("" ::: "memory");
+    wait_shared_memory();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <int V> __device__ __forceinline__ void load_row(const uint16_t* p, uint16_t (&v)[V])
 {
     if constexpr (V == 1)
@@ -104,16 +123,11 @@ template <int V> __device__ __forceinline__ bool sums_stay_normal(const uint16_t
     return !__any(tiny);
 }
 
-// BF8L quantisation of one row held V-per-lane (src/scalar/probability.cpp:20-38):
-// packs this lane's V int8 values four to a word and returns the BF16 scale of
-// its 256-value block. Sets error[0] when a value is not finite.
-template <int V>
-__device__ __forceinline__ uint16_t bf8l_pack(const uint16_t (&v)[V], uint32_t (&packed)[(V + 3) / 4],
-                                              uint32_t* error)
+// Largest magnitude of this lane's values as BF16 bits: on non-negative BF16
+// patterns integer order is numeric order, and patterns from 0x7f80 up are
+// not finite.
+template <int V> __device__ __forceinline__ uint32_t bf8l_lane_top(const uint16_t (&v)[V])
 {
-    constexpr int lanes_per_block = 256 / V;
-    // Largest magnitude as BF16 bits: on non-negative BF16 patterns integer
-    // order is numeric order, and patterns from 0x7f80 up are not finite.
     uint32_t top = 0;
 #pragma unroll
     for (int i = 0; i < V; ++i)
@@ -121,7 +135,29 @@ __device__ __forceinline__ uint16_t bf8l_pack(const uint16_t (&v)[V], uint32_t (
         const uint32_t magnitude = uint32_t(v[i]) & 0x7fffu;
         top = top < magnitude ? magnitude : top;
     }
-    top = group_umax<lanes_per_block>(top);
+    return top;
+}
+
+template <int V>
+__device__ __forceinline__ uint16_t bf8l_with_top(const uint16_t (&v)[V], uint32_t top,
+                                                  uint32_t (&packed)[(V + 3) / 4], uint32_t* error);
+
+// BF8L quantisation of one row held V-per-lane (src/scalar/probability.cpp:20-38):
+// packs this lane's V int8 values four to a word and returns the BF16 scale of
+// its 256-value block. Sets error[0] when a value is not finite.
+template <int V>
+__device__ __forceinline__ uint16_t bf8l_pack(const uint16_t (&v)[V], uint32_t (&packed)[(V + 3) / 4],
+                                              uint32_t* error)
+{
+    return bf8l_with_top<V>(v, group_umax<256 / V>(bf8l_lane_top<V>(v)), packed, error);
+}
+
+// The block's scale from its largest magnitude `top`, and this lane's values
+// quantised with it.
+template <int V>
+__device__ __forceinline__ uint16_t bf8l_with_top(const uint16_t (&v)[V], uint32_t top,
+                                                  uint32_t (&packed)[(V + 3) / 4], uint32_t* error)
+{
     if (top >= 0x7f80u)
     {
         error[0] = 1u;
@@ -267,5 +303,149 @@ __device__ __forceinline__ void layer_norm_lane(uint16_t (&v)[V], const uint16_t
     load_row<V>(gain + lane * V, g);
     load_row<V>(bias + lane * V, b);
     layer_norm_values<V>(v, g, b);
+}
+
+// ---- rows spread over a workgroup ----------------------------------------------
+// A row of K = Waves*64*Vw values held by the Waves wavefronts of a workgroup:
+// wave w holds the 64*Vw consecutive values from w*64*Vw, and lane l of it the
+// Vw consecutive values from (w*64 + l)*Vw. Leaves are in row order, so each
+// wave's in-lane and cross-lane trees are the reference's pair tree over its
+// part of the row, and the waves' results join as the tree's top levels. Every
+// wave of the workgroup calls these helpers (they contain barriers).
+
+// FTZ pair tree over `count` (a power of two) flushed values.
+template <int count> __device__ __forceinline__ float flushed_tree(float (&t)[count])
+{
+#pragma unroll
+    for (int width = count; width > 1; width /= 2)
+    {
+#pragma unroll
+        for (int i = 0; i < width / 2; ++i)
+        {
+            t[i] = flushed_add(t[2 * i], t[2 * i + 1]);
+        }
+    }
+    return t[0];
+}
+
+// LayerNorm of a spread row, in place; `exchange` is 2*Waves floats of LDS.
+// A wave whose values are all zero or at least 2^-56 in magnitude sums its part
+// with plain additions: every partial sum inside its subtree is then zero or at
+// least 2^-126 (sums_stay_normal), so the FTZ tree's flushes are identities
+// there. The waves' sums always join with FTZ additions, as the reference's
+// tree does, whatever the other waves' parts hold.
+template <int Vw, int Waves>
+__device__ __forceinline__ void layer_norm_spread(uint16_t (&v)[Vw], const uint16_t (&g)[Vw], const uint16_t (&b)[Vw],
+                                                  int warp, float* exchange)
+{
+    float values[Vw], squares[Vw], x[Vw];
+#pragma unroll
+    for (int i = 0; i < Vw; ++i)
+    {
+        x[i] = bf16_to_float(v[i]);
+        values[i] = x[i];
+        squares[i] = x[i] * x[i];
+    }
+    float sum, sum_squares;
+    if (sums_stay_normal<Vw>(v))
+    {
+        sum = plain_tree_sum<wave>(register_tree<Vw, false>(values));
+        sum_squares = plain_tree_sum<wave>(register_tree<Vw, false>(squares));
+    }
+    else
+    {
+        sum = tree_sum<wave>(register_tree<Vw>(values));
+        sum_squares = tree_sum<wave>(register_tree<Vw>(squares));
+    }
+    if (threadIdx.x % wave == 0)
+    {
+        exchange[warp] = sum;
+        exchange[Waves + warp] = sum_squares;
+    }
+    lds_barrier();
+    float sums[Waves], square_sums[Waves];
+#pragma unroll
+    for (int w = 0; w < Waves; ++w)
+    {
+        sums[w] = exchange[w];
+        square_sums[w] = exchange[Waves + w];
+    }
+    // The row's probability_sum ends with add(+0, S) (src/format/categorical.cpp:44-74).
+    sum = flushed_add(0.0f, flushed_tree<Waves>(sums));
+    sum_squares = flushed_add(0.0f, flushed_tree<Waves>(square_sums));
+    constexpr int width = Waves * wave * Vw;
+    const float reciprocal = 1.0f / float(width);
+    const float mean = sum * reciprocal;
+    float variance = __builtin_fmaf(sum_squares, reciprocal, 0.0f);
+    variance = __builtin_fmaf(mean, -mean, variance);
+    variance += 1e-5f;
+    const float inverse = 1.0f / __builtin_sqrtf(variance);
+    const float offset = -mean * inverse;
+#pragma unroll
+    for (int i = 0; i < Vw; ++i)
+    {
+        const float normalized = __builtin_fmaf(x[i], inverse, offset);
+        v[i] = float_to_bf16(__builtin_fmaf(normalized, bf16_to_float(g[i]), bf16_to_float(b[i])));
+    }
+}
+
+// BF8L of a spread row into row-major storage (q_row [K], s_row [K/256]);
+// `exchange` is Waves words of LDS, used when a 256-value block spans waves.
+template <int Vw, int Waves>
+__device__ __forceinline__ void bf8l_spread(const uint16_t (&v)[Vw], int warp, int8_t* q_row, float* s_row,
+                                            uint32_t* error, uint32_t* exchange)
+{
+    constexpr int block_lanes = 256 / Vw; // lanes holding one 256-value block
+    const int lane = threadIdx.x % wave, position = warp * wave + lane;
+    uint32_t top = bf8l_lane_top<Vw>(v);
+    if constexpr (block_lanes <= wave)
+    {
+        top = group_umax<block_lanes>(top);
+    }
+    else
+    {
+        constexpr int block_waves = block_lanes / wave;
+        top = group_umax<wave>(top);
+        if (lane == 0)
+        {
+            exchange[warp] = top;
+        }
+        lds_barrier();
+        const int first = warp / block_waves * block_waves;
+        top = 0;
+#pragma unroll
+        for (int i = 0; i < block_waves; ++i)
+        {
+            const uint32_t t = exchange[first + i];
+            top = top < t ? t : top;
+        }
+    }
+    uint32_t packed[(Vw + 3) / 4];
+    const uint16_t scale = bf8l_with_top<Vw>(v, top, packed, error);
+    int8_t* q = q_row + position * Vw;
+    if constexpr (Vw == 1)
+    {
+        *q = int8_t(packed[0] & 0xffu);
+    }
+    else if constexpr (Vw == 2)
+    {
+        *reinterpret_cast<uint16_t*>(q) = uint16_t(packed[0] & 0xffffu);
+    }
+    else if constexpr (Vw == 4)
+    {
+        *reinterpret_cast<uint32_t*>(q) = packed[0];
+    }
+    else
+    {
+#pragma unroll
+        for (int c = 0; c < Vw / 8; ++c)
+        {
+            *reinterpret_cast<uint2*>(q + 8 * c) = make_uint2(packed[2 * c], packed[2 * c + 1]);
+        }
+    }
+    if (position % block_lanes == 0)
+    {
+        s_row[position / block_lanes] = bf16_to_float(scale);
+    }
 }
 } // namespace tsac_hip

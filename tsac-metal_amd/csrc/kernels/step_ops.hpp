@@ -101,11 +101,6 @@ __device__ __forceinline__ bool build_masses(const float (&leaf)[16], int lane, 
     return __all(valid);
 }
 
-__device__ __forceinline__ void wait_shared_memory()
-{
-    __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
-}
-
 // Explicit shared-memory views: a generic pointer whose address space the
 // compiler cannot see turns shared-memory reads into flat loads.
 template <class T> using Shared = const __attribute__((address_space(3))) T*;
