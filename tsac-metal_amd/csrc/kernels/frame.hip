@@ -1524,7 +1524,8 @@ __device__ __noinline__ void condition_rows(const word* in, const uint16_t* gain
 // ------------------------------------------------------------------ sampling job
 
 constexpr int window = 256;
-constexpr int draw_lds = max_lanes * 1024 * 4 + max_lanes * 1024 * 2 + max_lanes * 64 * 2 + window + 3 * max_lanes * 4;
+constexpr int draw_lds =
+    max_lanes * 1024 * 4 + max_lanes * 1024 * 2 + max_lanes * 64 * 2 + window + 3 * max_lanes * 4 + 3 * frame_waves * 4;
 
 struct Draw
 {
@@ -1541,9 +1542,146 @@ struct Draw
     unsigned long long payload_bytes = 0;
 };
 
-// Softmax, masses and top decisions per lane (one wave each); wave 0 decodes
-// the lanes' symbols in stream order with the decoder held in `state` (LDS)
-// (decode.hip sample_kernel), each once its lane's wave has released it.
+// Lane 0's softmax (src/common/probability.cpp:96-122) and subtree masses
+// (build_masses' nodes) by all waves: its logits arrive first, as the lanes
+// follow the range decoder's stream order, while the other waves would wait.
+// Wave w takes symbols [128w, 128w + 128), two per lane, so each wave's trees
+// are the reference's pair trees over its part and the waves' results join as
+// the trees' top levels. `exchange` is 3 * frame_waves words of LDS. Returns
+// (in wave 0) whether every probability is finite and non-negative.
+__device__ __forceinline__ bool first_lane_masses(const word* logits, uint16_t* distributions, bool decoding,
+                                                  const Exchange& x, uint32_t* error, float* nodes, uint16_t* leaves,
+                                                  float* exchange)
+{
+    const int lane = threadIdx.x % wave, warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
+    const int position = warp * wave + lane; // symbols 2 * position and 2 * position + 1
+    uint16_t v[2];
+    take_values<2>(logits, std::size_t(position) * 2, x, v);
+    float maximum = -__builtin_inff();
+    bool finite = true;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+    {
+        const float value = bf16_to_float(v[k]);
+        finite = finite && is_finite(value);
+        maximum = maximum < value ? value : maximum;
+    }
+    if (!finite)
+    {
+        error[0] = 1u;
+    }
+    maximum = group_max<wave>(maximum);
+    if (lane == 0)
+    {
+        exchange[warp] = maximum;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int w = 0; w < frame_waves; ++w)
+    {
+        const float m = exchange[w];
+        maximum = maximum < m ? m : maximum;
+    }
+    float e[2], sum[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+    {
+        e[k] = original_exp(bf16_to_float(v[k]) - maximum);
+        sum[k] = e[k];
+    }
+    const float part = tree_sum<wave>(register_tree<2>(sum));
+    if (lane == 0)
+    {
+        exchange[frame_waves + warp] = part;
+    }
+    lds_barrier();
+    float parts[frame_waves];
+#pragma unroll
+    for (int w = 0; w < frame_waves; ++w)
+    {
+        parts[w] = exchange[frame_waves + w];
+    }
+    // probability_sum ends with add(+0, S) (src/format/categorical.cpp:44-74).
+    const float total = flushed_add(0.0f, flushed_tree<frame_waves>(parts));
+    const float reciprocal = 1.0f / total;
+    float prob[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+    {
+        v[k] = float_to_bf16(e[k] * reciprocal);
+        prob[k] = bf16_to_float(v[k]);
+    }
+    const uint32_t pair = v[0] | (uint32_t(v[1]) << 16);
+    if (distributions)
+    {
+        *reinterpret_cast<uint32_t*>(distributions + 2 * position) = pair;
+    }
+    if (!decoding)
+    {
+        return true;
+    }
+    *reinterpret_cast<uint32_t*>(leaves + 2 * position) = pair;
+    bool valid = is_finite(prob[0]) && prob[0] >= 0.0f && is_finite(prob[1]) && prob[1] >= 0.0f;
+    // Node n covers 1024 >> floor(log2 n) symbols; after the butterfly at
+    // stride s a lane's value covers 4s symbols from 2 * position.
+    float m = flushed_add(flush(prob[0]), flush(prob[1]));
+    nodes[512 + position] = m;
+    const auto store = [&](int s) {
+        if (position % (2 * s) == 0)
+        {
+            nodes[256 / s + position / (2 * s)] = m;
+        }
+    };
+    m = butterfly_ftz_add<1>(m);
+    store(1);
+    m = butterfly_ftz_add<2>(m);
+    store(2);
+    m = butterfly_ftz_add<4>(m);
+    store(4);
+    m = butterfly_ftz_add<8>(m);
+    store(8);
+    m = butterfly_ftz_add<16>(m);
+    store(16);
+    m = butterfly_ftz_add<32>(m);
+    store(32); // node 8 + warp
+    if (lane == 0)
+    {
+        exchange[2 * frame_waves + warp] = __all(valid) ? 1.0f : 0.0f;
+    }
+    lds_barrier();
+    if (warp != 0)
+    {
+        return true;
+    }
+    // Nodes 1..7 from the waves' nodes 8..15.
+    float level[frame_waves];
+    valid = true;
+#pragma unroll
+    for (int w = 0; w < frame_waves; ++w)
+    {
+        level[w] = nodes[frame_waves + w];
+        valid = valid && exchange[2 * frame_waves + w] != 0.0f;
+    }
+#pragma unroll
+    for (int width = frame_waves / 2; width >= 1; width /= 2)
+    {
+#pragma unroll
+        for (int i = 0; i < width; ++i)
+        {
+            level[i] = flushed_add(level[2 * i], level[2 * i + 1]);
+            if (lane == 0)
+            {
+                nodes[width + i] = level[i];
+            }
+        }
+    }
+    return valid;
+}
+
+// Softmax, masses and top decisions per lane: lane 0's by all waves
+// (first_lane_masses), every later lane's by one wave; wave 0 decodes the
+// lanes' symbols in stream order with the decoder held in `state` (LDS)
+// (decode.hip sample_kernel), each once its lane's masses are released.
 __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* state, const Exchange& exchange,
                                          uint32_t* error, uint8_t* lds)
 {
@@ -1571,6 +1709,7 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
     int* valid = reinterpret_cast<int*>(lds + max_lanes * (1024 * 6 + 128) + window);     // [8]
     int* rows = valid + max_lanes;                                                 // [8]
     int* ready = rows + max_lanes;                                                  // [8]
+    float* partials = reinterpret_cast<float*>(ready + max_lanes);                  // [3 * waves]
     const int lane = threadIdx.x % wave, warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
     const bool active = warp < M;
     const bool decoding = a.known == nullptr;
@@ -1601,7 +1740,28 @@ __device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* s
         }
         reinterpret_cast<uint32_t*>(bytes)[lane] = four;
     }
-    if (active)
+    {
+        const int first_row = a.row_base[0] + a.step * a.step_stride + a.book;
+        const bool ok = first_lane_masses(a.logits, a.distributions ? a.distributions + std::size_t(first_row) * 1024
+                                                                    : nullptr,
+                                          decoding, x, error, nodes, leaves, partials);
+        if (warp == 0)
+        {
+            if (decoding)
+            {
+                wait_shared_memory();
+                build_top_decisions(lane, Masses{nodes, leaves}, top);
+            }
+            // Lane 0's row, masses and decisions are in LDS: release them.
+            if (lane == 0)
+            {
+                valid[0] = ok;
+                rows[0] = first_row;
+                __hip_atomic_store(ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+    }
+    if (active && warp > 0)
     {
         uint16_t v[16];
         take_row<16>(a.logits, std::size_t(warp) * 1024 + lane * 16, x, v);
