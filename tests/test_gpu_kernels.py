@@ -418,6 +418,28 @@ def test_attention_decode_matches_oracle(torch, native, oracle, heads, hw):
                     (frames, pattern, prefill)
 
 
+@pytest.mark.parametrize("heads,hw", [(1, 128), (2, 64)])
+def test_attention_decode_long_histories(torch, native, oracle, heads, hw):
+    """Histories past 64 blocks (the merge's running-maximum scan carried from
+    one chunk of 64 blocks to the next), the longest one workgroup's LDS holds
+    (256 blocks), one block more (partials in scratch and a merge launch), and
+    a block whose scores are all NaN (the merge's plain sequential loop)."""
+    rng = np.random.default_rng(21 + hw)
+    scale = np.float32(1 / np.sqrt(hw))
+    w = heads * hw
+    cases = [(frames, False) for frames in (4097, 8191, 16384, 16385)] + [(5000, True)]
+    for frames, poisoned in cases:
+        q = bf16_bits(rng.standard_normal(w).astype(np.float32) * 2)
+        k = bf16_bits(rng.standard_normal(frames * w).astype(np.float32) * 2)
+        v = bf16_bits(rng.standard_normal(frames * w).astype(np.float32))
+        if poisoned:
+            q[3] = 0  # 0 * inf = NaN in every score of block 70
+            k.reshape(frames, w)[70 * 64:71 * 64, 3] = 0x7F80
+        out = empty(torch, w, torch.int16)
+        native.attention(dev(torch, q), dev(torch, k), dev(torch, v), 0, 1, frames, heads, hw, scale, False, out)
+        assert np.array_equal(host(out), oracle.attention(q, k, v, heads, hw, scale, False)), (frames, poisoned)
+
+
 def test_attention_decode_batched_sequences(torch, native, oracle):
     """Three lanes with their own caches, as the decode step runs them."""
     rng = np.random.default_rng(11)

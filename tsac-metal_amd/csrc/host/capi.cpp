@@ -410,7 +410,14 @@ int tsac_hip_attention(const uint16_t* query, const uint16_t* keys, const uint16
         [&]
         {
             const auto s = as_stream(stream);
-            AsyncScratch scratch(decode_partial_floats(sequences, heads, head_width, time) * 4, s);
+            const std::size_t floats = decode_partial_floats(sequences, heads, head_width, time);
+            if (floats == 0)
+            {
+                attention_decode(query, keys, values, sequence_stride, sequences, time, heads, head_width, scale,
+                                 prefill != 0, nullptr, out, s);
+                return;
+            }
+            AsyncScratch scratch(floats * 4, s);
             attention_decode(query, keys, values, sequence_stride, sequences, time, heads, head_width,
                              scale, prefill != 0, static_cast<float*>(scratch.pointer), out, s);
         });

@@ -7,8 +7,10 @@
 //   * blocks merged in ascending order with the online-softmax recurrence.
 // Matrix cores would reorder those sums, so everything runs on the VALU.
 //
-// Decode (one query per sequence): block partials are computed in parallel,
-// one wavefront per (sequence, head, 64-key block), then merged in order.
+// Decode (one query per sequence): one workgroup per (sequence, head) computes
+// the block partials into LDS and merges them in order; histories beyond what
+// its LDS holds use one wavefront per (sequence, head, block) and a second
+// launch for the merge.
 // Prefill (encode, all queries known): one workgroup per (sequence, head,
 // 64-query tile) walks the causal key blocks with Q/K/V tiles in LDS.
 #include "attention.hpp"
@@ -136,6 +138,211 @@ __global__ __launch_bounds__(64) void decode_blocks_kernel(
             s = round_bf16(s);
         }
         record[2 + j] = s;
+    }
+}
+
+// Waves per workgroup: 16 for 64-wide heads; 8 for 128-wide ones, whose key
+// rows and value words need twice the registers.
+template <int HW> constexpr int decode_waves = HW == 64 ? 16 : 8;
+constexpr int decode_lds_blocks = 256; // blocks whose records one workgroup's LDS holds
+
+// Records [max, block sum, value sums[HW]] of one (sequence, head) in LDS, wave
+// w computing blocks w, w + decode_waves<HW>, ...; then wave 0 merges them in
+// ascending order. The merge's running maxima are a scan with the recurrence's
+// own update (keep the running maximum unless it is smaller: the first of
+// equal values wins), which is associative without NaNs, so every block's
+// factors come at once and only the two-operation total/numerator recurrence
+// stays sequential; with a NaN maximum the merge runs the plain loop.
+template <int HW>
+__global__ __launch_bounds__(decode_waves<HW> * 64) void decode_attention_kernel(
+    const uint16_t* __restrict__ query, const uint16_t* __restrict__ keys,
+    const uint16_t* __restrict__ values, std::size_t sequence_stride, int width, int time,
+    int heads, float scale, int round_values, uint16_t* __restrict__ out)
+{
+    extern __shared__ float records[]; // [blocks][2 + HW]
+    __shared__ float qf[HW];
+    __shared__ float weights[decode_waves<HW>][64];
+    const int sequence = blockIdx.x / heads, head = blockIdx.x % heads;
+    const int lane = threadIdx.x % wave, warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
+    const int blocks = (time + 63) / 64;
+    const uint16_t* q = query + std::size_t(sequence) * width + head * HW;
+    const uint16_t* k = keys + std::size_t(sequence) * sequence_stride + head * HW;
+    const uint16_t* v = values + std::size_t(sequence) * sequence_stride + head * HW;
+    for (int j = threadIdx.x; j < HW; j += blockDim.x)
+    {
+        qf[j] = bf16_to_float(q[j]);
+    }
+    __syncthreads();
+    // Lane l sums value column l (HW = 64) or columns 2l and 2l + 1 (HW = 128).
+    constexpr int per_lane = HW / 64;
+    for (int block = warp; block < blocks; block += decode_waves<HW>)
+    {
+        const int start = block * 64;
+        const int count = time - start < 64 ? time - start : 64;
+        // This lane's key row, then every row's values, requested before any
+        // is used (rows past the history repeat its last row and are not
+        // used): a load under a per-row branch would be waited for on its own,
+        // and keys requested after the values would wait for all of them.
+        uint4 key[HW / 8];
+        {
+            const uint16_t* row = k + std::size_t(start + lane < time ? start + lane : time - 1) * width;
+#pragma unroll
+            for (int c = 0; c < HW / 8; ++c)
+            {
+                key[c] = reinterpret_cast<const uint4*>(row)[c];
+            }
+        }
+        uint32_t value[64];
+#pragma unroll
+        for (int t = 0; t < 64; ++t)
+        {
+            const int row = start + t < time ? start + t : time - 1;
+            const uint16_t* at = v + std::size_t(row) * width + per_lane * lane;
+            value[t] = per_lane == 2 ? *reinterpret_cast<const uint32_t*>(at) : uint32_t(*at);
+        }
+        float score = -__builtin_inff();
+        if (lane < count)
+        {
+            float dot = 0.0f;
+#pragma unroll
+            for (int c = 0; c < HW / 8; ++c)
+            {
+                const uint4 u = key[c];
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    dot = __builtin_fmaf(qf[8 * c + 2 * i], bf16_to_float(uint16_t(w[i] & 0xffff)), dot);
+                    dot = __builtin_fmaf(qf[8 * c + 2 * i + 1], bf16_to_float(uint16_t(w[i] >> 16)), dot);
+                }
+            }
+            score = dot * scale;
+        }
+        const float maximum = group_max<wave>(score);
+        float e = 0.0f;
+        if (lane < count)
+        {
+            e = original_exp(score - maximum);
+        }
+        const float sum = tree_sum<wave>(e);
+        weights[warp][lane] = e;
+        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the wave's weights are in
+        __builtin_amdgcn_wave_barrier();
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 64; ++t)
+        {
+            if (t < count)
+            {
+                const float w = weights[warp][t];
+                if constexpr (per_lane == 2)
+                {
+                    s0 = __builtin_fmaf(__uint_as_float(value[t] << 16), w, s0);
+                    s1 = __builtin_fmaf(__uint_as_float(value[t] & 0xffff0000u), w, s1);
+                }
+                else
+                {
+                    s0 = __builtin_fmaf(__uint_as_float(value[t] << 16), w, s0);
+                }
+            }
+        }
+        float* record = records + std::size_t(block) * (2 + HW);
+        if (lane == 0)
+        {
+            record[0] = maximum;
+            record[1] = sum;
+        }
+        record[2 + per_lane * lane] = round_values ? round_bf16(s0) : s0;
+        if constexpr (per_lane == 2)
+        {
+            record[3 + per_lane * lane] = round_values ? round_bf16(s1) : s1;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    if (warp != 0)
+    {
+        return;
+    }
+    // Ordered merge (src/scalar/attention.cpp:86-101).
+    float numerator[2] = {0.0f, 0.0f};
+    float total = 0.0f;
+    bool nan = false;
+    for (int b = lane; b < blocks; b += wave)
+    {
+        nan = nan || __builtin_isnan(records[std::size_t(b) * (2 + HW)]);
+    }
+    const auto step = [&](const float* record, float old_scale, float new_scale)
+    {
+        total = __builtin_fmaf(record[1], new_scale, total * old_scale);
+#pragma unroll
+        for (int i = 0; i < per_lane; ++i)
+        {
+            numerator[i] = __builtin_fmaf(record[2 + per_lane * lane + i], new_scale, numerator[i] * old_scale);
+        }
+    };
+    const auto scales_of = [](float running, float maximum, float& old_scale, float& new_scale)
+    {
+        const float factor = original_exp(-__builtin_fabsf(maximum - running));
+        old_scale = running > maximum ? 1.0f : factor;
+        new_scale = running > maximum ? factor : 1.0f;
+    };
+    if (__any(nan))
+    {
+        float running = -__builtin_inff();
+        for (int b = 0; b < blocks; ++b)
+        {
+            const float* record = records + std::size_t(b) * (2 + HW);
+            const float maximum = record[0];
+            float old_scale, new_scale;
+            scales_of(running, maximum, old_scale, new_scale);
+            step(record, old_scale, new_scale);
+            running = running < maximum ? maximum : running;
+        }
+    }
+    else
+    {
+        float carry = -__builtin_inff();
+        for (int chunk = 0; chunk < blocks; chunk += wave)
+        {
+            const int b = chunk + lane;
+            const float maximum = b < blocks ? records[std::size_t(b) * (2 + HW)] : -__builtin_inff();
+            // Inclusive scan of the running maximum over this chunk, from `carry`.
+            float inclusive = maximum;
+#pragma unroll
+            for (int stride = 1; stride < wave; stride *= 2)
+            {
+                const float left = __shfl_up(inclusive, stride, wave);
+                if (lane >= stride)
+                {
+                    inclusive = left < inclusive ? inclusive : left;
+                }
+            }
+            inclusive = carry < inclusive ? inclusive : carry;
+            const float before = __shfl_up(inclusive, 1, wave);
+            const float running = lane == 0 ? carry : before;
+            float old_scale, new_scale;
+            scales_of(running, maximum, old_scale, new_scale);
+            const int here = blocks - chunk < wave ? blocks - chunk : wave;
+            for (int i = 0; i < here; ++i)
+            {
+                step(records + std::size_t(chunk + i) * (2 + HW),
+                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(old_scale), i)),
+                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(new_scale), i)));
+            }
+            carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inclusive), here - 1));
+        }
+    }
+    const float reciprocal = 1.0f / total;
+    uint16_t* o = out + std::size_t(sequence) * width + head * HW + per_lane * lane;
+    if constexpr (per_lane == 2)
+    {
+        *reinterpret_cast<uint32_t*>(o) =
+            float_to_bf16(numerator[0] * reciprocal) | (uint32_t(float_to_bf16(numerator[1] * reciprocal)) << 16);
+    }
+    else
+    {
+        *o = float_to_bf16(numerator[0] * reciprocal);
     }
 }
 
@@ -458,7 +665,8 @@ void append_qkv(const uint16_t* qkv, std::size_t rows, std::size_t width, std::s
 std::size_t decode_partial_floats(std::size_t sequences, std::size_t heads, std::size_t head_width,
                                   std::size_t time)
 {
-    return sequences * heads * ((time + 63) / 64) * (2 + head_width);
+    const std::size_t blocks = (time + 63) / 64;
+    return blocks <= std::size_t(decode_lds_blocks) ? 0 : sequences * heads * blocks * (2 + head_width);
 }
 
 void attention_decode(const uint16_t* query, const uint16_t* keys, const uint16_t* values,
@@ -467,9 +675,37 @@ void attention_decode(const uint16_t* query, const uint16_t* keys, const uint16_
                       float* partial, uint16_t* out, hipStream_t stream)
 {
     require(time > 0 && sequences > 0, "attention: empty shape");
+    require(time < (std::size_t(1) << 30) && sequences * heads < (std::size_t(1) << 31), "attention: shape too large");
     const int max_blocks = int((time + 63) / 64);
     const int width = int(heads * head_width);
     const int round_values = time > 64 || replay;
+    if (max_blocks <= decode_lds_blocks)
+    {
+        const std::size_t lds = std::size_t(max_blocks) * (2 + head_width) * 4;
+        const unsigned grid = unsigned(sequences * heads);
+        switch (head_width)
+        {
+        case 64:
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attention_kernel<64>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)),
+                      "attention decode LDS");
+            decode_attention_kernel<64><<<grid, decode_waves<64> * 64, lds, stream>>>(
+                query, keys, values, sequence_stride, width, int(time), int(heads), scale, round_values, out);
+            break;
+        case 128:
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attention_kernel<128>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)),
+                      "attention decode LDS");
+            decode_attention_kernel<128><<<grid, decode_waves<128> * 64, lds, stream>>>(
+                query, keys, values, sequence_stride, width, int(time), int(heads), scale, round_values, out);
+            break;
+        default:
+            throw Error("attention: head width must be 64 or 128");
+        }
+        check_hip(hipGetLastError(), "attention decode launch");
+        return;
+    }
+    require(partial != nullptr, "attention: long histories need the partial scratch");
     const dim3 grid(unsigned(sequences * heads), unsigned(max_blocks));
     switch (head_width)
     {

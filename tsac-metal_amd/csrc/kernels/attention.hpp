@@ -12,7 +12,8 @@ void append_qkv(const uint16_t* qkv, std::size_t rows, std::size_t width, std::s
                 const uint16_t* rotation, uint16_t* query, uint16_t* keys, uint16_t* values,
                 std::size_t row_stride, hipStream_t stream);
 
-// Floats of block-partial scratch that attention_decode needs.
+// Floats of block-partial scratch that attention_decode needs (0 when one
+// workgroup per (sequence, head) holds every block's record in LDS).
 std::size_t decode_partial_floats(std::size_t sequences, std::size_t heads, std::size_t head_width,
                                   std::size_t time);
 
