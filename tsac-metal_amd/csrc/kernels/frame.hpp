@@ -1,7 +1,7 @@
 // One decode frame step (temporal stack, then every codebook with its range
 // decoding) in a single persistent launch.
 //
-// The step's ~280 dependent operations (projections, attention, sampling) run
+// The step's ~240 dependent operations (projections, attention, sampling) run
 // as jobs of a fixed set of co-resident workgroups. Activations pass between
 // jobs through "exchange words": 8-byte words holding two BF16 values (or a
 // token) in the low half and the step's epoch in the high half, written and
@@ -12,7 +12,11 @@
 //
 // Jobs take the lanes one at a time in lane order, the order in which the range
 // decoder produces their tokens, so a lane's next codebook starts as soon as its
-// own token is known.
+// own token is known. A projection normalises and quantises each lane's input
+// with all of its waves. When the device holds the extra workgroups, each
+// codebook layer's attention (at most one key per book) is computed inside its
+// out-projection tiles, one workgroup per (tile, lane), and the qkv/up/down
+// tiles alternate between two sets of workgroups from layer to layer.
 //
 // Key/value rows of earlier steps come from the temporal cache (written by
 // earlier launches); the current step's rows and the whole codebook stack come
