@@ -17,6 +17,9 @@ Also measured in the same run:
     MALL) rotated across launches; HIP events on the launch stream.
   * roofline_gemm: the encode MFMA GEMM on the codebook-stack qkv shape
     (M = 30,960 rows, K = 512, N = 1536).
+  * roofline_frame: the timed round trip's dominant kernel, the decode frame
+    step: algorithmic bytes per step over the session's decode-model time per
+    step. It is bound by the latency of its dependent jobs, not by HBM.
   * qlinear: per-launch GB/s on the K=1024, N in {1024, 4096} shapes.
   * wide_geometry: throughput of the same round trip on the 1024-wide
     geometry (16 x 64 heads, FFN 4096), 300 frames.
@@ -278,6 +281,35 @@ def attention_rates(torch, native, lengths=(256, 1290, 2580), batch=3, heads=16,
             "bytes": "batch*2*T*heads*head_width*2 (decode: the BF16 key and value cache)"}
 
 
+def frame_roofline(geometry, frames, batch, decode_model_s):
+    """The timed region's dominant kernel, one decode frame step per launch:
+    algorithmic bytes per step (every projection's int8 weights, block scales
+    and bias read once per step for all lanes, plus each lane's temporal
+    key/value cache rows at the average context position) over the average
+    step time. It is bound by its ~240 dependent jobs on lane 0's chain, not
+    by memory; the fraction shows how far from HBM-bound that is."""
+    g = geometry
+
+    def linear(k, n):
+        return k * n + 4 * (k // 256) * n + 4 * n
+
+    layer = (linear(g.width, 3 * g.width) + linear(g.width, g.width) + linear(g.width, g.ffn) +
+             linear(g.ffn, g.width))
+    lanes = min(batch, frames)
+    steps = -(-frames // lanes)
+    weights = (g.temporal_layers * layer + g.books * g.codebook_layers * layer + g.books * linear(g.width, g.alphabet)
+               + (g.books - 1) * linear(g.latent, g.width) + linear(g.latent, g.width))
+    cache = lanes * g.temporal_layers * ((steps - 1) / 2) * g.width * 2 * 2
+    step_s = decode_model_s / steps
+    achieved = (weights + cache) / step_s / 1e9
+    kernel = "frame_kernel<8, 32, 16, 128>" if g.width == 512 else "frame_kernel<16, 64, 16, 64>"
+    return {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "limited_by": "dependent-job latency (~240 jobs per step in order on lane 0's chain)",
+            "bytes_per_step": int(weights + cache), "avg_step_us": round(step_s * 1e6, 1), "steps": steps,
+            "step_time": "session decode-model time (HIP events on its stream) / steps"}
+
+
 def wide_geometry(native, frames=300, batch=3):
     """Throughput only: the same round trip on the 1024-wide geometry (width
     1024, 16 x 64 heads, FFN 4096, 12 + 3 layers), random-init weights, on a
@@ -394,6 +426,7 @@ def main():
                         "encode_range_coding": round(encode_split[1] / args.steps, 4),
                         "decode_model": round(decode_split[0] / args.steps, 4),
                         "decode_range_coding": round(decode_split[1] / args.steps, 4)},
+            "roofline_frame": frame_roofline(geometry, args.frames, args.batch, decode_split[0] / args.steps),
         })
         del session, hip_model
         torch.cuda.synchronize()
