@@ -287,8 +287,16 @@ def frame_roofline(geometry, frames, batch, decode_model_s):
     and bias read once per step for all lanes, plus each lane's temporal
     key/value cache rows at the average context position) over the average
     step time. It is bound by its ~240 dependent jobs on lane 0's chain, not
-    by memory; the fraction shows how far from HBM-bound that is."""
+    by memory; the fraction shows how far from HBM-bound that is. `traffic`
+    is the HBM bytes per step from the two calibrated PMC runs of the
+    2580-frame, batch-3 reference workload recorded in profiles/ (null for
+    other workloads)."""
     g = geometry
+    measured = None
+    record = ROOT / "profiles" / "frame_step_decode_reference_2580frames.traffic.txt"
+    if g.width == 512 and frames == 2580 and batch == 3 and record.exists():
+        fields = dict(line.split("=", 1) for line in record.read_text().split() if "=" in line)
+        measured = int(float(fields["bytes_per_step"]))
 
     def linear(k, n):
         return k * n + 4 * (k // 256) * n + 4 * n
@@ -304,7 +312,7 @@ def frame_roofline(geometry, frames, batch, decode_model_s):
     achieved = (weights + cache) / step_s / 1e9
     kernel = "frame_kernel<8, 32, 16, 128>" if g.width == 512 else "frame_kernel<16, 64, 16, 64>"
     return {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured,
             "limited_by": "dependent-job latency (~240 jobs per step in order on lane 0's chain)",
             "bytes_per_step": int(weights + cache), "avg_step_us": round(step_s * 1e6, 1), "steps": steps,
             "step_time": "session decode-model time (HIP events on its stream) / steps"}
