@@ -175,6 +175,17 @@ class HipModel:
     def __del__(self):
         _release(self, "tsac_hip_model_destroy")
 
+    def close(self):
+        """Destroys the device model now (every session of it must be closed
+        first); later calls are no-ops."""
+        _release(self, "tsac_hip_model_destroy")
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
     def session(self) -> "HipSession":
         return HipSession(self)
 
@@ -190,6 +201,17 @@ class HipSession:
 
     def __del__(self):
         _release(self, "tsac_hip_session_destroy")
+
+    def close(self):
+        """Destroys the session (its stream, caches and scratch) now; later
+        calls are no-ops."""
+        _release(self, "tsac_hip_session_destroy")
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
     def clear(self):
         check(library().tsac_hip_session_clear(self.handle))
