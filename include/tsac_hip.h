@@ -114,6 +114,37 @@ int tsac_hip_decode(tsac_hip_session* session, const uint8_t* stream, size_t len
 
 void tsac_hip_free(void* pointer);
 
+/* EntropyPosition (include/tsac/observer.hpp:7-10): token_offset indexes the
+ * [frame][group][book] token array. */
+typedef struct tsac_hip_position
+{
+    uint64_t frame, group, codebook, lane, step, token_offset;
+} tsac_hip_position;
+
+/* EntropyObserver (include/tsac/observer.hpp:12-16) as C callbacks; either may
+ * be NULL. They run on the calling thread, once per symbol in stream order
+ * (step, book, lane, group), after the call's GPU work has completed, as
+ * MetalTransformer runs its observers (src/metal/transformer.hpp:9-12).
+ * after_symbol receives the bits the range encoder spent on the symbol
+ * (RangeEncoder::bit_position() before and after it, src/format/entropy.cpp:86-100)
+ * when encoding and 0 when decoding (src/format/entropy.cpp:137-149). A nonzero
+ * return stops the call, which then fails with "stopped by the observer". */
+typedef struct tsac_hip_observer
+{
+    void* context;
+    int (*before_symbol)(void* context, const tsac_hip_position* position);
+    int (*after_symbol)(void* context, const tsac_hip_position* position, uint64_t bits);
+} tsac_hip_observer;
+
+/* MetalTransformer::encode / decode with their EntropyObserver argument
+ * (src/metal/transformer.hpp:30-33); observer may be NULL. tsac_hip_encode and
+ * tsac_hip_decode are these with no observer. */
+int tsac_hip_encode_observed(tsac_hip_session* session, const tsac_hip_header* header,
+                             const uint16_t* tokens, size_t count, const tsac_hip_observer* observer,
+                             uint8_t** stream, size_t* length);
+int tsac_hip_decode_observed(tsac_hip_session* session, const uint8_t* stream, size_t length,
+                             const tsac_hip_observer* observer, uint16_t** tokens, size_t* count);
+
 /* Teacher-forced probability-model outputs: the BF16 distribution the model
  * assigns to every token position (out: host [count][alphabet]), i.e. what
  * TransformerPredictor::predict returns (src/common/transformer.cpp:137-182).

@@ -137,6 +137,18 @@ int orc_encoder_put(orc_encoder* e, uint16_t probability_zero, int bit)
     return 0;
 }
 
+/* src/format/range.cpp:81-87: whole bytes (emitted and pending) times 8 plus the
+ * bits the range has consumed below 24. */
+size_t orc_encoder_bit_position(const orc_encoder* e)
+{
+    unsigned width = 0;
+    for (uint32_t r = e->range; r; r >>= 1)
+    {
+        ++width;
+    }
+    return (e->pending_count + e->size) * 8 + (size_t)(24 - width);
+}
+
 /* src/format/range.cpp:83-110 */
 int orc_encoder_finish(orc_encoder* e)
 {

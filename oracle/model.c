@@ -842,6 +842,9 @@ typedef struct
 {
     orc_encoder encoder;
     const uint16_t* tokens;
+    uint32_t* bits;       /* per symbol in stream order, or NULL */
+    uint64_t* positions;  /* 6 per symbol in stream order, or NULL */
+    size_t visited;
     float probabilities[4096];
 } pack_context;
 
@@ -856,15 +859,39 @@ static int pack_visit(void* context, predictor* p, const position_t* q)
     }
     widen(distribution, alphabet, c->probabilities);
     const uint16_t token = c->tokens[q->token_offset];
+    const size_t before = orc_encoder_bit_position(&c->encoder);
     if (orc_encode_categorical(&c->encoder, c->probabilities, alphabet, token))
     {
         return 1;
     }
+    /* pack_normal's after_symbol(position, bits) (src/format/entropy.cpp:86-100). */
+    if (c->bits)
+    {
+        c->bits[c->visited] = (uint32_t)(orc_encoder_bit_position(&c->encoder) - before);
+    }
+    if (c->positions)
+    {
+        uint64_t* r = c->positions + 6 * c->visited;
+        r[0] = q->frame;
+        r[1] = q->group;
+        r[2] = q->codebook;
+        r[3] = q->lane;
+        r[4] = q->step;
+        r[5] = q->token_offset;
+    }
+    ++c->visited;
     return commit(p, q, token);
 }
 
 int orc_pack_normal(orc_model* m, const orc_header* header, const uint16_t* tokens, size_t count,
                     unsigned threads, uint8_t** out, size_t* length)
+{
+    return orc_pack_normal_observed(m, header, tokens, count, threads, out, length, NULL, NULL);
+}
+
+int orc_pack_normal_observed(orc_model* m, const orc_header* header, const uint16_t* tokens,
+                             size_t count, unsigned threads, uint8_t** out, size_t* length,
+                             uint32_t* bits, uint64_t* positions)
 {
     orc_header h = *header;
     h.method = 1;
@@ -895,6 +922,9 @@ int orc_pack_normal(orc_model* m, const orc_header* header, const uint16_t* toke
     pack_context* c = orc_alloc(sizeof *c);
     orc_encoder_init(&c->encoder, (size_t)512 * 1024 * 1024 - 18);
     c->tokens = tokens;
+    c->bits = bits;
+    c->positions = positions;
+    c->visited = 0;
     predictor p;
     int status = predictor_reset(&p, m, &h, threads);
     if (!status)

@@ -220,6 +220,9 @@ class Oracle(_Kernels):
                                         C.POINTER(u8p), C.POINTER(sz)]
         lib.orc_unpack_normal.argtypes = [C.c_void_p, u8p, sz, C.c_uint, C.POINTER(u16p),
                                           C.POINTER(sz)]
+        lib.orc_pack_normal_observed.argtypes = [C.c_void_p, C.POINTER(Header), u16p, sz, C.c_uint,
+                                                 C.POINTER(u8p), C.POINTER(sz), C.POINTER(C.c_uint32),
+                                                 C.POINTER(C.c_uint64)]
         lib.orc_distributions_prefix.argtypes = [C.c_void_p, C.POINTER(Header), u16p, sz, C.c_uint,
                                                  sz, u16p]
         lib.orc_free.argtypes = [C.c_void_p]
@@ -292,6 +295,21 @@ class OracleModel:
         self.lib.orc_free(out)
         return data
 
+    def pack_normal_observed(self, h: Header, tokens, threads=1):
+        """pack_normal plus what an EntropyObserver sees: per symbol in stream
+        order, after_symbol's bit count and the position (frame, group,
+        codebook, lane, step, token_offset)."""
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out, n = u8p(), sz()
+        bits = np.zeros(max(t.size, 1), np.uint32)
+        positions = np.zeros((max(t.size, 1), 6), np.uint64)
+        self.oracle._check(self.lib.orc_pack_normal_observed(
+            self.handle, C.byref(h), ptr(t, C.c_uint16), t.size, threads, C.byref(out), C.byref(n),
+            ptr(bits, C.c_uint32), ptr(positions, C.c_uint64)))
+        data = C.string_at(out, n.value)
+        self.lib.orc_free(out)
+        return data, bits[:t.size], positions[:t.size]
+
     def unpack_normal(self, data: bytes, threads=1) -> np.ndarray:
         b = np.frombuffer(data, np.uint8).copy()
         out, n = u16p(), sz()
@@ -344,6 +362,8 @@ class Reference(_Kernels):
         lib.ref_pack_normal.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u8p, sz,
                                         C.POINTER(sz)]
         lib.ref_unpack_normal.argtypes = [C.POINTER(ModelDesc), u8p, sz, u16p, sz, C.POINTER(sz)]
+        lib.ref_pack_normal_observed.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u8p, sz,
+                                                 C.POINTER(sz), C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]
         lib.ref_distributions.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u16p]
 
     @staticmethod
@@ -381,6 +401,20 @@ class Reference(_Kernels):
         self._check(self.lib.ref_pack_normal(C.byref(desc), C.byref(h), ptr(t, C.c_uint16), t.size,
                                              ptr(out, C.c_uint8), out.size, C.byref(n)))
         return out[:n.value].tobytes()
+
+    def pack_normal_observed(self, model, h: Header, tokens):
+        """The reference's pack_normal with an EntropyObserver recording each
+        symbol's position and after_symbol bit count in the order it sees them."""
+        desc, keep = model_desc(model)
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out = np.zeros(1 << 22, np.uint8)
+        n = sz()
+        bits = np.zeros(max(t.size, 1), np.uint32)
+        positions = np.zeros((max(t.size, 1), 6), np.uint64)
+        self._check(self.lib.ref_pack_normal_observed(C.byref(desc), C.byref(h), ptr(t, C.c_uint16), t.size,
+                                                      ptr(out, C.c_uint8), out.size, C.byref(n),
+                                                      ptr(bits, C.c_uint32), ptr(positions, C.c_uint64)))
+        return out[:n.value].tobytes(), bits[:t.size], positions[:t.size]
 
     def unpack_normal(self, model, data: bytes, capacity: int) -> np.ndarray:
         desc, keep = model_desc(model)

@@ -24,6 +24,7 @@ typedef struct orc_decoder
 void orc_encoder_init(orc_encoder* e, size_t max_bytes);
 int orc_encoder_put(orc_encoder* e, uint16_t probability_zero, int bit);
 int orc_encoder_finish(orc_encoder* e);
+size_t orc_encoder_bit_position(const orc_encoder* e);
 int orc_decoder_init(orc_decoder* d, const uint8_t* bytes, size_t length);
 int orc_decoder_get(orc_decoder* d, uint16_t probability_zero, int* bit);
 int orc_encode_categorical(orc_encoder* e, const float* p, size_t n, size_t symbol);

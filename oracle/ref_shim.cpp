@@ -463,6 +463,47 @@ int ref_pack_normal(const orc_model_desc* desc, const orc_header* header,
         });
 }
 
+// The reference's pack_normal with an EntropyObserver that records, per symbol
+// in the order the observer sees them, before_symbol's position and
+// after_symbol's bit count (src/format/entropy.cpp:86-100).
+int ref_pack_normal_observed(const orc_model_desc* desc, const orc_header* header,
+                             const std::uint16_t* tokens, std::size_t count, std::uint8_t* out,
+                             std::size_t capacity, std::size_t* written, std::uint32_t* bits,
+                             std::uint64_t* positions)
+{
+    return guarded(
+        [&]
+        {
+            RefBackend backend(*desc);
+            TransformerPredictor predictor(backend);
+            std::size_t before = 0, after = 0;
+            EntropyObserver observer{
+                [&](const EntropyPosition& p)
+                {
+                    detail::require(before == after && before < count, "observer order");
+                    std::uint64_t* r = positions + 6 * before;
+                    r[0] = p.frame;
+                    r[1] = p.group;
+                    r[2] = p.codebook;
+                    r[3] = p.lane;
+                    r[4] = p.step;
+                    r[5] = p.token_offset;
+                    ++before;
+                },
+                [&](const EntropyPosition& p, std::size_t n)
+                {
+                    detail::require(after + 1 == before && positions[6 * after + 5] == p.token_offset,
+                                    "observer order");
+                    bits[after++] = static_cast<std::uint32_t>(n);
+                }};
+            const auto bytes =
+                pack_normal(header_of(*header), std::span(tokens, count), predictor, Limits{}, observer);
+            detail::require(bytes.size() <= capacity && after == count, "capacity");
+            std::memcpy(out, bytes.data(), bytes.size());
+            *written = bytes.size();
+        });
+}
+
 int ref_unpack_normal(const orc_model_desc* desc, const std::uint8_t* bytes, std::size_t length,
                       std::uint16_t* tokens, std::size_t capacity, std::size_t* count)
 {

@@ -136,6 +136,13 @@ int orc_backend_codebook_step(orc_model* model, size_t lane, size_t book, const 
  * concurrently, like the reference's executor. */
 int orc_pack_normal(orc_model* model, const orc_header* header, const uint16_t* tokens,
                     size_t count, unsigned threads, uint8_t** out, size_t* length);
+/* pack_normal with an EntropyObserver recording, per symbol in stream order,
+ * after_symbol's bit count (bits[count], src/format/entropy.cpp:86-100) and the
+ * position {frame, group, codebook, lane, step, token_offset} (positions[6*count]);
+ * either may be NULL. */
+int orc_pack_normal_observed(orc_model* model, const orc_header* header, const uint16_t* tokens,
+                             size_t count, unsigned threads, uint8_t** out, size_t* length,
+                             uint32_t* bits, uint64_t* positions);
 int orc_unpack_normal(orc_model* model, const uint8_t* bytes, size_t length, unsigned threads,
                       uint16_t** tokens, size_t* count);
 /* Teacher-forced distributions in token order: out[token_offset][alphabet] BF16. */

@@ -4,6 +4,8 @@ plus a message (no exception crosses the ABI)."""
 import ctypes
 import pathlib
 import re
+import shutil
+import subprocess
 
 import numpy as np
 import pytest
@@ -67,3 +69,23 @@ def test_synthetic_model_layout():
     assert model.embeddings.shape == (12, 1024, 1024)
     # Block scales are BF16-representable, as the packed format stores them.
     assert not (scales.view(np.uint32) & 0xFFFF).any()
+
+
+REFERENCE_TREE = pathlib.Path("/root/reference")
+
+
+@pytest.mark.parametrize("compiler", [["g++", "-std=c++2b"], ["/opt/rocm/llvm/bin/clang++", "-std=c++23"]],
+                         ids=["g++", "clang++"])
+def test_reference_side_adapter_compiles(compiler):
+    """tsac-metal_amd/integration/hip_transformer.cpp (HipTransformer, the
+    MetalTransformer drop-in) type-checks against the reference's own headers
+    and include/tsac_hip.h, so a change to either side that breaks it fails here."""
+    if not (REFERENCE_TREE / "src" / "format" / "entropy.hpp").exists():
+        pytest.skip("reference tree not present")
+    if shutil.which(compiler[0]) is None:
+        pytest.skip(f"{compiler[0]} not installed")
+    source = ROOT / "tsac-metal_amd" / "integration" / "hip_transformer.cpp"
+    run = subprocess.run(compiler + ["-fsyntax-only", "-Wall", "-Wextra", "-Werror", f"-I{ROOT / 'include'}",
+                                     f"-I{REFERENCE_TREE / 'src'}", f"-I{REFERENCE_TREE / 'include'}", str(source)],
+                         capture_output=True, text=True)
+    assert run.returncode == 0, run.stderr

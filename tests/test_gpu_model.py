@@ -2,6 +2,9 @@
 (GEMM/prefill shapes) and the decode-side pass (GEMV/step shapes) return the
 oracle's distributions bit for bit, encode writes the oracle's bytes, decode
 recovers the tokens."""
+import concurrent.futures
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -71,6 +74,60 @@ def test_stream_bytes_and_round_trip(native, oracle, small, frames, batch, group
 
     assert stream == oracle.model(model).pack_normal(header(frames, batch, groups, 12), tokens, threads=4)
     assert np.array_equal(session.decode(stream), tokens)
+
+
+def _recorder():
+    before, after = [], []
+
+    def on_before(p):
+        before.append((p.frame, p.group, p.codebook, p.lane, p.step, p.token_offset))
+
+    def on_after(p, bits):
+        after.append((p.frame, p.group, p.codebook, p.lane, p.step, p.token_offset, bits))
+
+    return before, after, on_before, on_after
+
+
+@pytest.mark.parametrize("frames,batch,groups", [(35, 3, 2), (17, 8, 1)])
+def test_observer_sees_the_oracle_positions_and_bits(native, oracle, small, frames, batch, groups):
+    """EntropyObserver across the C ABI: encode reports every symbol in stream
+    order with the bits the range coder spent on it, as the oracle's
+    pack_normal (pinned to the reference's own) does; decode reports the same
+    positions with 0 bits."""
+    from oracle import header
+
+    model, hip_model = small
+    h = native.header(frames, batch, groups, 12)
+    tokens = random_tokens(frames, groups, 12, seed=frames + groups)
+    expected_stream, bits, positions = oracle.model(model).pack_normal_observed(header(frames, batch, groups, 12),
+                                                                                 tokens, threads=3)
+    with hip_model.session() as session:
+        before, after, on_before, on_after = _recorder()
+        stream = session.encode_observed(h, tokens, on_before, on_after)
+        assert stream == expected_stream
+        assert np.array_equal(np.array(before, np.uint64), positions)
+        assert np.array_equal(np.array(after, np.uint64)[:, :6], positions)
+        assert np.array_equal(np.array(after, np.uint64)[:, 6], bits)
+        before, after, on_before, on_after = _recorder()
+        assert np.array_equal(session.decode_observed(stream, on_before, on_after), tokens)
+        assert np.array_equal(np.array(before, np.uint64), positions)
+        assert np.array_equal(np.array(after, np.uint64)[:, :6], positions)
+        assert not np.array(after, np.uint64)[:, 6].any()
+
+
+def test_observer_can_stop_a_call_and_the_session_recovers(native, small):
+    _, hip_model = small
+    h = native.header(9, 3, 1, 12)
+    tokens = pattern_tokens(9 * 12)
+    with hip_model.session() as session:
+        seen = []
+        with pytest.raises(native.HipError, match="stopped by the observer"):
+            session.encode_observed(h, tokens, after=lambda p, bits: seen.append(bits) or len(seen) == 5)
+        assert len(seen) == 5
+        stream = session.encode(h, tokens)
+        with pytest.raises(native.HipError, match="stopped by the observer"):
+            session.decode_observed(stream, before=lambda p: p.step == 2)
+        assert np.array_equal(session.decode_observed(stream), tokens)
 
 
 def test_rollover_replay(native, oracle):
@@ -183,3 +240,57 @@ def test_encode_validates_inputs(native, small):
         session.encode(native.header(1, 1, 1, 1), np.array([1024], np.uint16))
     with pytest.raises(native.HipError, match="codebook"):
         session.encode(native.header(1, 1, 1, 13), np.zeros(13, np.uint16))
+
+
+@pytest.mark.parametrize("geometry", ["small", "reference"])
+def test_concurrent_sessions_on_two_threads(native, small, reference_model, geometry):
+    """Two sessions of one model driven from two host threads at once give the
+    streams and tokens one session gives alone (tests/audio_analyzer.cpp:109-186);
+    the reference geometry runs the persistent frame-step launch in both."""
+    model, hip_model = small if geometry == "small" else reference_model
+    frames = 40 if geometry == "small" else 24
+    h = native.header(frames, 3, 1, 12)
+    tokens = [random_tokens(frames, 1, 12, seed=40 + i) for i in range(2)]
+    with hip_model.session() as alone:
+        expected = [alone.encode(h, t) for t in tokens]
+
+    def work(i):
+        with hip_model.session() as session:
+            out = []
+            for _ in range(3):
+                stream = session.encode(h, tokens[i])
+                out.append((stream, session.decode(stream)))
+            return out
+
+    with concurrent.futures.ThreadPoolExecutor(2) as pool:
+        results = list(pool.map(work, range(2)))
+    for i, runs in enumerate(results):
+        for stream, decoded in runs:
+            assert stream == expected[i]
+            assert np.array_equal(decoded, tokens[i])
+
+
+def test_nonfinite_activation_is_an_error_and_the_session_recovers(native, reference_model):
+    """A feedback embedding row of +inf (BF16 0x7f80) reaches the activations
+    only when its symbol is coded: every pass that meets it fails with the
+    nonfinite-activation error (tests/metal_range.cpp:21-61), in the frame-step
+    launch too, and the same session then codes a stream that avoids it."""
+    model, clean = reference_model
+    poisoned = dataclasses.replace(model, embeddings=model.embeddings.copy())
+    poisoned.embeddings[0, 1023, :] = 0x7F80
+    frames, batch = 6, 3
+    h = native.header(frames, batch, 1, 12)
+    bad = random_tokens(frames, 1, 12, seed=12) % 1023
+    bad[2 * 12 + 0] = 1023  # frame 2 (lane 1, step 0), book 0
+    good = random_tokens(frames, 1, 12, seed=13) % 1023
+    with clean.session() as session:
+        bad_stream = session.encode(h, bad)
+        good_stream = session.encode(h, good)
+    with native.HipModel(poisoned) as hip_poisoned, hip_poisoned.session() as session:
+        for call in (lambda: session.encode(h, bad), lambda: session.decode(bad_stream),
+                     lambda: session.distributions(h, bad, native.PASS_ENCODE),
+                     lambda: session.distributions(h, bad, native.PASS_DECODE)):
+            with pytest.raises(native.HipError, match="not finite"):
+                call()
+        assert session.encode(h, good) == good_stream
+        assert np.array_equal(session.decode(good_stream), good)

@@ -326,6 +326,26 @@ def test_pack_normal_matches_reference(oracle, reference, small_model, frames, b
     assert np.array_equal(om.unpack_normal(stream, threads=2), tokens)
 
 
+@pytest.mark.parametrize("frames,batch,groups,books", [(17, 3, 1, 12), (35, 3, 2, 12), (3, 8, 2, 12)])
+def test_observer_bits_and_order_match_reference(oracle, reference, small_model, frames, batch, groups, books):
+    """What an EntropyObserver sees during pack_normal: the position of every
+    symbol in the order the reference's own pack_normal visits them and the bits
+    after_symbol reports (RangeEncoder::bit_position deltas, src/format/entropy.cpp:86-100)."""
+    from oracle import header
+
+    h = header(frames, batch, groups, books)
+    tokens = pattern_tokens(frames * groups * books)
+    stream, bits, positions = oracle.model(small_model).pack_normal_observed(h, tokens, threads=2)
+    ref_stream, ref_bits, ref_positions = reference.pack_normal_observed(small_model, h, tokens)
+    assert stream == ref_stream
+    assert np.array_equal(positions, ref_positions)
+    assert np.array_equal(bits, ref_bits)
+    # Every token appears once; the bits add up to the payload's arithmetic length.
+    assert sorted(positions[:, 5].tolist()) == list(range(tokens.size))
+    payload_bits = (len(stream) - 18) * 8
+    assert payload_bits - 32 <= int(bits.sum()) <= payload_bits
+
+
 def test_rollover_replay_matches_reference(oracle, reference):
     """1026 frames in one lane crosses the 1024-position context: the last 256
     frames are replayed with replay rounding (src/common/transformer.cpp:187-203)."""

@@ -109,6 +109,35 @@ struct AsyncScratch
     }
 };
 
+tsac_hip_position position_of(const Position& p)
+{
+    return {p.frame, p.group, p.book, p.lane, p.step, p.offset};
+}
+
+// The C callbacks as the session's observer; a nonzero return becomes an
+// exception that ends the call.
+SymbolObserver observer_of(const tsac_hip_observer* o)
+{
+    SymbolObserver r;
+    if (o && o->before_symbol)
+    {
+        r.before = [o](const Position& p)
+        {
+            const tsac_hip_position c = position_of(p);
+            require(o->before_symbol(o->context, &c) == 0, "stopped by the observer (before_symbol)");
+        };
+    }
+    if (o && o->after_symbol)
+    {
+        r.after = [o](const Position& p, std::size_t bits)
+        {
+            const tsac_hip_position c = position_of(p);
+            require(o->after_symbol(o->context, &c, bits) == 0, "stopped by the observer (after_symbol)");
+        };
+    }
+    return r;
+}
+
 LinearPath path_of(int path)
 {
     require(path >= 0 && path <= 2, "invalid linear path");
@@ -187,11 +216,19 @@ int tsac_hip_session_clear(tsac_hip_session* session)
 int tsac_hip_encode(tsac_hip_session* session, const tsac_hip_header* header,
                     const uint16_t* tokens, size_t count, uint8_t** stream, size_t* length)
 {
+    return tsac_hip_encode_observed(session, header, tokens, count, nullptr, stream, length);
+}
+
+int tsac_hip_encode_observed(tsac_hip_session* session, const tsac_hip_header* header,
+                             const uint16_t* tokens, size_t count, const tsac_hip_observer* observer,
+                             uint8_t** stream, size_t* length)
+{
     return guarded(
         [&]
         {
             require(session && stream && length && (tokens || !count), "missing argument");
-            const auto bytes = session->session->encode(header_of(header), tokens, count);
+            const SymbolObserver o = observer_of(observer);
+            const auto bytes = session->session->encode(header_of(header), tokens, count, observer ? &o : nullptr);
             *stream = copy_out(bytes);
             *length = bytes.size();
         });
@@ -200,11 +237,18 @@ int tsac_hip_encode(tsac_hip_session* session, const tsac_hip_header* header,
 int tsac_hip_decode(tsac_hip_session* session, const uint8_t* stream, size_t length,
                     uint16_t** tokens, size_t* count)
 {
+    return tsac_hip_decode_observed(session, stream, length, nullptr, tokens, count);
+}
+
+int tsac_hip_decode_observed(tsac_hip_session* session, const uint8_t* stream, size_t length,
+                             const tsac_hip_observer* observer, uint16_t** tokens, size_t* count)
+{
     return guarded(
         [&]
         {
             require(session && stream && tokens && count, "missing argument");
-            const auto t = session->session->decode(stream, length);
+            const SymbolObserver o = observer_of(observer);
+            const auto t = session->session->decode(stream, length, observer ? &o : nullptr);
             *tokens = copy_out(t);
             *count = t.size();
         });

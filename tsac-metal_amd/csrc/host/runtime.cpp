@@ -354,20 +354,20 @@ void Session::validate(const Header& h, const uint16_t* tokens, std::size_t coun
     const Geometry& g = model_->geometry();
     const Limits& limits = model_->limits();
     validate_header(h, limits);
-    require(h.method == 1, "Transformer predictor requires normal framing");
-    require(h.frames <= 0xffffffffu, "normal frame count exceeds uint32");
-    require(count == h.symbols(), "normal token count does not match header");
+    require(h.method == 1, "the probability model codes normal (method 1) streams only");
+    require(h.frames <= 0xffffffffu, "normal stream frame count does not fit 32 bits");
+    require(count == h.symbols(), "token count differs from frames x groups x codebooks of the header");
     require(h.model_channels == g.channels && h.codebooks <= g.books,
-            "Transformer stream/model mismatch");
+            "header channels or codebooks do not match the model");
     if (tokens)
     {
         for (std::size_t i = 0; i < count; ++i)
         {
-            require(tokens[i] < 1024, "index outside 10-bit alphabet");
+            require(tokens[i] < 1024, "token above 1023: outside the 1024-symbol alphabet");
         }
     }
     const std::size_t independent = checked_mul(std::min<std::size_t>(h.batch, h.frames), h.groups);
-    require(independent <= limits.tensor_elements, "Transformer lane count exceeds limit");
+    require(independent <= limits.tensor_elements, "independent lane count is above Limits::tensor_elements");
     const std::size_t base = h.frames / h.batch, extra = h.frames % h.batch;
     const std::size_t contexts = checked_mul(
         h.groups, checked_add(checked_mul(h.batch - extra, std::min<std::size_t>(base, g.context)),
@@ -377,7 +377,7 @@ void Session::validate(const Header& h, const uint16_t* tokens, std::size_t coun
     const std::size_t codebook_bytes = checked_mul(
         checked_mul(independent, h.codebooks), std::size_t(g.codebook_layers) * g.width * 2 * sizeof(uint16_t));
     require(checked_add(temporal_bytes, codebook_bytes) <= limits.cache_bytes,
-            "Transformer caches exceed byte limit; reduce the encoding batch size or channel count");
+            "key/value caches would exceed Limits::cache_bytes: lower the entropy batch or the channel count");
 }
 
 // One transformer stack over rows with causal prefill attention
@@ -611,69 +611,66 @@ void Session::batched(const Header& h, const uint16_t* tokens, uint16_t* distrib
     }
 }
 
-std::vector<uint8_t> Session::encode(Header h, const uint16_t* tokens, std::size_t count)
+std::vector<uint8_t> Session::encode(Header h, const uint16_t* tokens, std::size_t count,
+                                     const SymbolObserver* observer)
 {
     check_hip(hipSetDevice(model_->device()), "hipSetDevice");
     const double t0 = now();
     h.method = 1;
     validate(h, tokens, count);
-    require(model_->limits().file_bytes >= 19, "normal framing exceeds file limit");
+    require(model_->limits().file_bytes >= 19, "the stream limit is below the 19-byte FBAZ framing");
     const uint32_t crc = token_crc32(tokens, count);
     std::vector<uint16_t> splits(count * 16);
     reset_errors();
     batched(h, tokens, nullptr, splits.data());
     check_errors();
     const double t1 = now();
+    // Host range coding in stream order (src/format/entropy.cpp:57-100): the ten
+    // Q15 splits along each symbol's bisection path, computed on the GPU.
     RangeEncoder encoder(model_->limits().file_bytes - 18);
-    const Lanes lanes(h);
-    for (std::size_t step = 0; step < lanes.steps(); ++step)
+    const bool before = observer && observer->before, after = observer && observer->after;
+    for_each_position(h, [&](const Position& p)
     {
-        for (std::size_t book = 0; book < h.codebooks; ++book)
+        if (before)
         {
-            for (std::size_t lane = 0; lane < lanes.count; ++lane)
+            observer->before(p);
+        }
+        const std::size_t start = after ? encoder.bit_position() : 0;
+        const uint16_t symbol = tokens[p.offset];
+        const uint16_t* s = splits.data() + p.offset * 16;
+        std::size_t base = 0, n = 1024;
+        for (int level = 0; n > 1; ++level)
+        {
+            const std::size_t half = n / 2;
+            const bool one = symbol >= base + half;
+            encoder.put(s[level], one);
+            if (one)
             {
-                if (step >= lanes.length(lane))
-                {
-                    continue;
-                }
-                const std::size_t frame = lanes.start(lane) + step;
-                for (std::size_t group = 0; group < h.groups; ++group)
-                {
-                    const std::size_t offset = (frame * h.groups + group) * h.codebooks + book;
-                    const uint16_t symbol = tokens[offset];
-                    const uint16_t* s = splits.data() + offset * 16;
-                    std::size_t base = 0, n = 1024;
-                    for (int level = 0; n > 1; ++level)
-                    {
-                        const std::size_t half = n / 2;
-                        const bool bit = symbol >= base + half;
-                        encoder.put(s[level], bit);
-                        if (bit)
-                        {
-                            base += half;
-                            n -= half;
-                        }
-                        else
-                        {
-                            n = half;
-                        }
-                    }
-                }
+                base += half;
+                n -= half;
+            }
+            else
+            {
+                n = half;
             }
         }
-    }
+        if (after)
+        {
+            observer->after(p, encoder.bit_position() - start);
+        }
+    });
     const auto bytes = frame_normal(h, crc, encoder.finish());
     const double t2 = now();
     timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds()};
     return bytes;
 }
 
-std::vector<uint16_t> Session::decode(const uint8_t* stream, std::size_t length)
+std::vector<uint16_t> Session::decode(const uint8_t* stream, std::size_t length, const SymbolObserver* observer)
 {
     check_hip(hipSetDevice(model_->device()), "hipSetDevice");
     const double t0 = now();
     const Header h = parse_header(stream, length, model_->limits());
-    require(h.method == 1, "unpack_normal requires method 1");
+    require(h.method == 1, "the probability model decodes normal (method 1) streams only");
     validate(h, nullptr, h.symbols());
     std::vector<uint16_t> tokens(h.symbols());
     // The initial interval is validated on the host (src/format/range.cpp:122-129).
@@ -681,9 +678,28 @@ std::vector<uint16_t> Session::decode(const uint8_t* stream, std::size_t length)
     reset_errors();
     stepwise(h, nullptr, stream + h.payload_offset, h.payload_bytes, tokens.data(), nullptr);
     check_errors();
-    require(token_crc32(tokens.data(), tokens.size()) == h.token_crc, "invalid token CRC32");
     const double t1 = now();
-    timing_ = {t1 - t0, 0.0, t1 - t0, input_seconds()};
+    // Every symbol was decoded on the GPU; observers see them in stream order
+    // with 0 bits, as unpack_normal reports them (src/format/entropy.cpp:137-149),
+    // before the CRC check.
+    if (observer && (observer->before || observer->after))
+    {
+        for_each_position(h, [&](const Position& p)
+        {
+            if (observer->before)
+            {
+                observer->before(p);
+            }
+            if (observer->after)
+            {
+                observer->after(p, 0);
+            }
+        });
+    }
+    require(token_crc32(tokens.data(), tokens.size()) == h.token_crc,
+            "decoded tokens fail the stream's CRC-32 check");
+    const double t2 = now();
+    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds()};
     return tokens;
 }
 

@@ -182,8 +182,12 @@ public:
     Session& operator=(const Session&) = delete;
 
     void clear();
-    std::vector<uint8_t> encode(Header header, const uint16_t* tokens, std::size_t count);
-    std::vector<uint16_t> decode(const uint8_t* stream, std::size_t length);
+    // pack_normal / unpack_normal on the GPU; an observer, when given, sees every
+    // symbol in stream order once the GPU work is done (encode: with its bits).
+    std::vector<uint8_t> encode(Header header, const uint16_t* tokens, std::size_t count,
+                                const SymbolObserver* observer = nullptr);
+    std::vector<uint16_t> decode(const uint8_t* stream, std::size_t length,
+                                 const SymbolObserver* observer = nullptr);
     // Teacher-forced distributions [count][alphabet]; decode_pass selects the
     // stepwise (GEMV) driver instead of the batched (GEMM) one.
     void distributions(Header header, const uint16_t* tokens, std::size_t count, bool decode_pass,

@@ -31,7 +31,7 @@ EXPORTS = (
     "tsac_hip_linear_apply", "tsac_hip_linear_apply_quantized", "tsac_hip_bf8l",
     "tsac_hip_layer_norm", "tsac_hip_softmax", "tsac_hip_gelu", "tsac_hip_rotary", "tsac_hip_add",
     "tsac_hip_attention", "tsac_hip_attention_causal", "tsac_hip_bf8l_tiles", "tsac_hip_tile_rows",
-    "tsac_hip_probe_read", "tsac_hip_probe_mfma",
+    "tsac_hip_probe_read", "tsac_hip_probe_mfma", "tsac_hip_encode_observed", "tsac_hip_decode_observed",
 )
 
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_TILES = 0, 1, 2, 3
@@ -68,6 +68,18 @@ class Header(C.Structure):
                 ("codebooks", C.c_uint8), ("frames", C.c_uint64), ("batch", C.c_uint16)]
 
 
+class Position(C.Structure):
+    _fields_ = [(name, C.c_uint64) for name in ("frame", "group", "codebook", "lane", "step", "token_offset")]
+
+
+BEFORE_SYMBOL = C.CFUNCTYPE(C.c_int, vp, C.POINTER(Position))
+AFTER_SYMBOL = C.CFUNCTYPE(C.c_int, vp, C.POINTER(Position), C.c_uint64)
+
+
+class Observer(C.Structure):
+    _fields_ = [("context", vp), ("before_symbol", BEFORE_SYMBOL), ("after_symbol", AFTER_SYMBOL)]
+
+
 def header(frames, batch, groups, codebooks, model_channels=2, method=1) -> Header:
     return Header(method, groups, model_channels, codebooks, frames, batch)
 
@@ -92,6 +104,10 @@ def library() -> C.CDLL:
         lib.tsac_hip_encode.argtypes = [vp, C.POINTER(Header), u16p, sz, C.POINTER(u8p), C.POINTER(sz)]
         lib.tsac_hip_decode.argtypes = [vp, u8p, sz, C.POINTER(u16p), C.POINTER(sz)]
         lib.tsac_hip_free.argtypes = [vp]
+        lib.tsac_hip_encode_observed.argtypes = [vp, C.POINTER(Header), u16p, sz, C.POINTER(Observer),
+                                                 C.POINTER(u8p), C.POINTER(sz)]
+        lib.tsac_hip_decode_observed.argtypes = [vp, u8p, sz, C.POINTER(Observer), C.POINTER(u16p),
+                                                 C.POINTER(sz)]
         lib.tsac_hip_distributions.argtypes = [vp, C.POINTER(Header), u16p, sz, C.c_int, u16p]
         lib.tsac_hip_session_timing.argtypes = [vp, C.POINTER(C.c_double), sz]
         lib.tsac_hip_linear_create.argtypes = [C.POINTER(Linear), sz, sz, C.POINTER(vp)]
@@ -232,6 +248,37 @@ class HipSession:
                                         C.byref(n)))
         tokens = np.ctypeslib.as_array(out, shape=(n.value,)).copy() if n.value else np.zeros(0, np.uint16)
         library().tsac_hip_free(out)
+        return tokens
+
+    @staticmethod
+    def _observer(before, after):
+        """C observer over Python callables before(position) and
+        after(position, bits), each given a Position; a callable returning a
+        true value stops the call."""
+        b = BEFORE_SYMBOL(lambda _, p: int(bool(before(p.contents)))) if before else BEFORE_SYMBOL()
+        a = AFTER_SYMBOL(lambda _, p, bits: int(bool(after(p.contents, bits)))) if after else AFTER_SYMBOL()
+        return Observer(None, b, a), (b, a)
+
+    def encode_observed(self, h: Header, tokens, before=None, after=None) -> bytes:
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out, n = u8p(), sz()
+        observer, keep = self._observer(before, after)
+        check(library().tsac_hip_encode_observed(self.handle, C.byref(h), _ptr(t, C.c_uint16), t.size,
+                                                 C.byref(observer), C.byref(out), C.byref(n)))
+        data = C.string_at(out, n.value)
+        library().tsac_hip_free(out)
+        del keep
+        return data
+
+    def decode_observed(self, data: bytes, before=None, after=None) -> np.ndarray:
+        b = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+        out, n = u16p(), sz()
+        observer, keep = self._observer(before, after)
+        check(library().tsac_hip_decode_observed(self.handle, _ptr(b, C.c_uint8), len(data), C.byref(observer),
+                                                 C.byref(out), C.byref(n)))
+        tokens = np.ctypeslib.as_array(out, shape=(n.value,)).copy() if n.value else np.zeros(0, np.uint16)
+        library().tsac_hip_free(out)
+        del keep
         return tokens
 
     def distributions(self, h: Header, tokens, mode: int = PASS_ENCODE) -> np.ndarray:
