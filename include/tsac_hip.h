@@ -188,6 +188,17 @@ void tsac_hip_linear_destroy(tsac_hip_device_linear* linear);
 int tsac_hip_linear_apply(const tsac_hip_device_linear* linear, const uint16_t* x, size_t M,
                           uint16_t* y, int path, void* stream);
 
+/* tsac_hip_linear_apply without any device allocation, for callers that cannot
+ * allocate (tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The BF8L buffer is a fixed per-device array of
+ * 16 MiB (plus its scales), held until the process ends: M x K (M rounded up to
+ * a multiple of 128 on the GEMM path) must not exceed 16 MiB, larger calls fail
+ * with an error. Every call on a device shares that array, so calls that
+ * overlap on one device race. Synchronises `stream` to report a non-finite
+ * activation, as tsac_hip_linear_apply does. */
+int tsac_hip_linear_apply_static(const tsac_hip_device_linear* linear, const uint16_t* x, size_t M,
+                                 uint16_t* y, int path, void* stream);
+
 /* The same product on activations already in BF8L form (q [M][K] int8, scales
  * [M][K/256] fp32 widened from BF16), with an optional BF16 residual [M][N]
  * added after rounding (bf16(residual + y), src/scalar/probability.cpp:6-14);

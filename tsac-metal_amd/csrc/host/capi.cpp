@@ -348,6 +348,17 @@ int tsac_hip_linear_apply(const tsac_hip_device_linear* linear, const uint16_t* 
         });
 }
 
+int tsac_hip_linear_apply_static(const tsac_hip_device_linear* linear, const uint16_t* x, size_t M,
+                                 uint16_t* y, int path, void* stream)
+{
+    return guarded(
+        [&]
+        {
+            require(linear && (x || !M) && (y || !M), "missing argument");
+            linear_apply_static(linear->linear, x, M, y, path_of(path), as_stream(stream));
+        });
+}
+
 int tsac_hip_linear_apply_quantized(const tsac_hip_device_linear* linear, const int8_t* q,
                                     const float* scales, size_t M, uint16_t* y,
                                     const uint16_t* residual, int path, void* stream)

@@ -98,6 +98,14 @@ void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::si
             Layout layout = Layout::rows);
 std::size_t gemv_max_rows();
 
+// x [M][K] BF16 -> y [M][N] like quantize_rows + linear, with the BF8L buffer in
+// a fixed per-device array (static_linear.hip) instead of caller or allocator
+// memory; padded rows x K must not exceed static_linear_max_bytes(). Fails if
+// an activation is not finite. Calls that overlap on one device race.
+void linear_apply_static(const DeviceLinear& w, const uint16_t* x, std::size_t M, uint16_t* y, LinearPath path,
+                         hipStream_t stream);
+std::size_t static_linear_max_bytes();
+
 // ---- row-wise elementwise kernels --------------------------------------------
 void layer_norm_rows(const uint16_t* x, std::size_t rows, std::size_t width, const uint16_t* gain,
                      const uint16_t* bias, uint16_t* out, hipStream_t stream);

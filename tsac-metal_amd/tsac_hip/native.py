@@ -32,6 +32,7 @@ EXPORTS = (
     "tsac_hip_layer_norm", "tsac_hip_softmax", "tsac_hip_gelu", "tsac_hip_rotary", "tsac_hip_add",
     "tsac_hip_attention", "tsac_hip_attention_causal", "tsac_hip_bf8l_tiles", "tsac_hip_tile_rows",
     "tsac_hip_probe_read", "tsac_hip_probe_mfma", "tsac_hip_encode_observed", "tsac_hip_decode_observed",
+    "tsac_hip_linear_apply_static",
 )
 
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_TILES = 0, 1, 2, 3
@@ -113,6 +114,7 @@ def library() -> C.CDLL:
         lib.tsac_hip_linear_create.argtypes = [C.POINTER(Linear), sz, sz, C.POINTER(vp)]
         lib.tsac_hip_linear_destroy.argtypes = [vp]
         lib.tsac_hip_linear_apply.argtypes = [vp, vp, sz, vp, C.c_int, vp]
+        lib.tsac_hip_linear_apply_static.argtypes = [vp, vp, sz, vp, C.c_int, vp]
         lib.tsac_hip_linear_apply_quantized.argtypes = [vp, vp, vp, sz, vp, vp, C.c_int, vp]
         lib.tsac_hip_bf8l.argtypes = [vp, sz, sz, vp, vp, vp]
         lib.tsac_hip_bf8l_tiles.argtypes = [vp, sz, sz, vp, vp, vp]
@@ -329,6 +331,11 @@ class DeviceLinear:
         """x: int16/uint16 cuda tensor [M][K] of BF16 bits -> y [M][N]."""
         m = x.numel() // self.K
         check(library().tsac_hip_linear_apply(self.handle, _dp(x), m, _dp(y), path, _stream(stream)))
+
+    def apply_static(self, x, y, path=PATH_AUTO, stream=None):
+        """apply() with the BF8L buffer in the library's fixed device array (no allocation)."""
+        m = x.numel() // self.K
+        check(library().tsac_hip_linear_apply_static(self.handle, _dp(x), m, _dp(y), path, _stream(stream)))
 
     def apply_quantized(self, q, scales, m, y, residual=None, path=PATH_AUTO, stream=None):
         check(library().tsac_hip_linear_apply_quantized(
