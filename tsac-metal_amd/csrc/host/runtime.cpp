@@ -223,22 +223,11 @@ Model::Model(const Geometry& g, const LinearHost* projections, const uint16_t* c
     rotations_ = reinterpret_cast<const uint16_t*>(constants + rotations_offset);
     embeddings_ = reinterpret_cast<const uint16_t*>(constants + embeddings_offset);
 
-    // Device copies of the projection and norm tables for the frame kernel.
-    const std::size_t linear_bytes = align_up(count * sizeof(DeviceLinear), 256);
-    const std::size_t pointer_bytes = align_up(g.norms() * sizeof(const uint16_t*), 256);
-    tables_ = DeviceBuffer(linear_bytes + 2 * pointer_bytes);
-    auto* tables = tables_.as<uint8_t>();
-    check_hip(hipMemcpy(tables, projections_.data(), count * sizeof(DeviceLinear), hipMemcpyHostToDevice),
-              "upload projection table");
-    check_hip(hipMemcpy(tables + linear_bytes, gain_.data(), g.norms() * sizeof(const uint16_t*),
-                        hipMemcpyHostToDevice),
-              "upload norm table");
-    check_hip(hipMemcpy(tables + linear_bytes + pointer_bytes, bias_.data(), g.norms() * sizeof(const uint16_t*),
-                        hipMemcpyHostToDevice),
-              "upload norm table");
-    frame_.linears = reinterpret_cast<const DeviceLinear*>(tables);
-    frame_.gain = reinterpret_cast<const uint16_t* const*>(tables + linear_bytes);
-    frame_.bias = reinterpret_cast<const uint16_t* const*>(tables + linear_bytes + pointer_bytes);
+    // The frame kernel's job descriptors are built per pass from these host
+    // arrays of device pointers (frame_job_table).
+    frame_.linears = projections_.data();
+    frame_.gain = gain_.data();
+    frame_.bias = bias_.data();
     frame_.positions = positions_;
     frame_.rotations = rotations_;
     frame_.embeddings = embeddings_;

@@ -156,7 +156,7 @@ public:
     {
         return embeddings_;
     }
-    // Device-resident tables of the model for the frame kernel.
+    // The model's projections and norms for the frame kernel's job table.
     const FrameModel& frame_tables() const
     {
         return frame_;
@@ -166,7 +166,7 @@ private:
     Geometry g_;
     Limits limits_;
     int device_ = 0;
-    DeviceBuffer values_, constants_, tables_;
+    DeviceBuffer values_, constants_;
     FrameModel frame_;
     std::vector<DeviceLinear> projections_;
     std::vector<const uint16_t*> gain_, bias_;

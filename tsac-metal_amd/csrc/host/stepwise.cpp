@@ -360,6 +360,11 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
         frame.error = err;
         frame.words = exchange;
         frame.abort = err + 2;
+        const std::vector<uint8_t> table = frame_job_table(frame);
+        auto* jobs = arena_.get<uint8_t>("s.jobs", table.size());
+        check_hip(hipMemcpyAsync(jobs, table.data(), table.size(), hipMemcpyHostToDevice, stream_), "upload jobs");
+        check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+        frame.jobs = jobs;
     }
 
     Graph graph;

@@ -11,6 +11,7 @@
 #include "step_ops.hpp"
 
 #include <algorithm>
+#include <cstring>
 
 namespace tsac_hip
 {
@@ -50,6 +51,22 @@ __device__ __forceinline__ void publish(word* w, std::size_t index, uint32_t pay
 template <class T> __device__ __forceinline__ const __attribute__((address_space(1))) T* global(const T* p)
 {
     return (const __attribute__((address_space(1))) T*)(p);
+}
+
+// Job functions stay out of line (each is one body in the instruction cache)
+// and are never tail-called: LLVM then gives these internal, non-recursive
+// functions no callee-saved registers (the kernel saves what it keeps live),
+// instead of saving and restoring up to ~100 registers in private memory on
+// every job.
+#define JOB __attribute__((not_tail_called))
+
+// Job descriptors live in a device table written before the launch and never
+// during it (frame_job_table), read through the constant address space so
+// every field is a scalar load into scalar registers.
+template <class T> using constant_ptr = const __attribute__((address_space(4))) T*;
+template <class T> __device__ __forceinline__ constant_ptr<T> constant(const void* p)
+{
+    return (constant_ptr<T>)(p);
 }
 
 // Job arguments reach each job through memory, so the compiler cannot see that
@@ -712,45 +729,46 @@ __device__ __forceinline__ void book_head(const word* qkv, std::size_t book_word
 
 // One 64-row tile of a projection for M lanes (decode.hip fused_linear_kernel).
 template <int V, In I, Out O, int HW = 0>
-__device__ __noinline__ void project_tile(const Projection& job, int M, int tile, const Exchange& exchange, uint32_t* error,
-                                          uint8_t* lds, const BookAttention* book_job = nullptr)
+__device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int position, int M, int tile, Exchange exchange,
+                                          uint32_t* error, uint8_t* lds, constant_ptr<BookAttention> book_job = nullptr,
+                                          int book_lane = 0)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
     Projection p;
-    p.w.values = uniform(job.w.values);
-    p.w.scales = uniform(job.w.scales);
-    p.w.bias = uniform(job.w.bias);
-    p.w.K = uniform(job.w.K);
-    p.w.N = uniform(job.w.N);
-    p.x = uniform(job.x);
-    p.gain = uniform(job.gain);
-    p.beta = uniform(job.beta);
-    p.embeddings = uniform(job.embeddings);
-    p.alphabet = uniform(job.alphabet);
-    p.books = uniform(job.books);
-    p.book = uniform(job.book);
-    p.tokens = uniform(job.tokens);
-    p.token_stride = uniform(job.token_stride);
-    p.token_words = uniform(job.token_words);
-    p.prefix_in = uniform(job.prefix_in);
-    p.prefix_out = uniform(job.prefix_out);
-    p.residual = uniform(job.residual);
-    p.residual_row = uniform(job.residual_row);
-    p.y = uniform(job.y);
-    p.keys = uniform(job.keys);
-    p.values = uniform(job.values);
-    p.lane_stride = uniform(job.lane_stride);
-    p.position = uniform(job.position);
-    p.rotations = uniform(job.rotations);
-    p.width = uniform(job.width);
-    p.head_width = uniform(job.head_width);
+    p.w.values = uniform(job->w.values);
+    p.w.scales = uniform(job->w.scales);
+    p.w.bias = uniform(job->w.bias);
+    p.w.K = uniform(job->w.K);
+    p.w.N = uniform(job->w.N);
+    p.x = uniform(job->x);
+    p.gain = uniform(job->gain);
+    p.beta = uniform(job->beta);
+    p.embeddings = uniform(job->embeddings);
+    p.alphabet = uniform(job->alphabet);
+    p.books = uniform(job->books);
+    p.book = uniform(job->book);
+    p.tokens = uniform(job->tokens);
+    p.token_stride = uniform(job->token_stride);
+    p.token_words = uniform(job->token_words);
+    p.prefix_in = uniform(job->prefix_in);
+    p.prefix_out = uniform(job->prefix_out);
+    p.residual = uniform(job->residual);
+    p.residual_row = uniform(job->residual_row);
+    p.y = uniform(job->y);
+    p.keys = uniform(job->keys);
+    p.values = uniform(job->values);
+    p.lane_stride = uniform(job->lane_stride);
+    p.position = uniform(position);
+    p.rotations = uniform(job->rotations);
+    p.width = uniform(job->width);
+    p.head_width = uniform(job->head_width);
     BookAttention book;
     if constexpr (I == In::attention)
     {
         book.qkv = uniform(book_job->qkv);
         book.book_words = uniform(book_job->book_words);
         book.time = uniform(book_job->time);
-        book.lane = uniform(book_job->lane);
+        book.lane = uniform(book_lane);
         book.scale = uniform(book_job->scale);
     }
     M = uniform(M);
@@ -1081,20 +1099,20 @@ template <int HW> constexpr int attend_lds()
 // codebook row) and the query are staged in LDS first, so the block loops read
 // only the cache and LDS.
 template <int HW>
-__device__ __noinline__ void attend_item(const Attend& job, int item, const Exchange& exchange, uint8_t* lds)
+__device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys, int item, Exchange exchange, uint8_t* lds)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
     Attend a;
-    a.heads = uniform(job.heads);
-    a.width = uniform(job.width);
-    a.scale = uniform(job.scale);
-    a.time = uniform(job.time);
-    a.keys = uniform(job.keys);
-    a.values = uniform(job.values);
-    a.lane_stride = uniform(job.lane_stride);
-    a.qkv = uniform(job.qkv);
-    a.book_words = uniform(job.book_words);
-    a.out = uniform(job.out);
+    a.heads = uniform(job->heads);
+    a.width = uniform(job->width);
+    a.scale = uniform(job->scale);
+    a.time = uniform(keys);
+    a.keys = uniform(job->keys);
+    a.values = uniform(job->values);
+    a.lane_stride = uniform(job->lane_stride);
+    a.qkv = uniform(job->qkv);
+    a.book_words = uniform(job->book_words);
+    a.out = uniform(job->out);
     item = uniform(item);
     constexpr int per_lane = HW / 64; // value columns per lane (adjacent)
     constexpr int row_words = HW;     // staged row: HW/2 key words, then HW/2 value words
@@ -1491,8 +1509,8 @@ __device__ __noinline__ void attend_item(const Attend& job, int item, const Exch
 // Book 0's codebook input: bf16(LayerNorm(x) + positions[0]) for every lane,
 // one wave per lane (decode.hip layer_norm_add_kernel).
 template <int V>
-__device__ __noinline__ void condition_rows(const word* in, const uint16_t* gain, const uint16_t* bias,
-                                            const uint16_t* add_row, word* out, int M, const Exchange& exchange)
+__device__ __noinline__ JOB void condition_rows(const word* in, const uint16_t* gain, const uint16_t* bias,
+                                            const uint16_t* add_row, word* out, int M, Exchange exchange)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
     in = uniform(in);
@@ -1540,6 +1558,86 @@ struct Draw
     uint16_t* distributions = nullptr;
     const uint8_t* payload = nullptr;
     unsigned long long payload_bytes = 0;
+};
+
+// Inputs of book 0's conditioning rows (condition_rows).
+struct Condition
+{
+    const word* in = nullptr;
+    const uint16_t* gain = nullptr;
+    const uint16_t* bias = nullptr;
+    const uint16_t* positions = nullptr;
+    word* out = nullptr;
+};
+
+// Where each job's descriptor sits in the job table: projections (the temporal
+// embedding, 4 per temporal layer, then per book its prefix, 4 per codebook
+// layer and its head), attention jobs (temporal layers, then (book, layer)),
+// the fused codebook attention per (book, layer), one draw per book and the
+// conditioning rows; each part 256-byte aligned.
+struct JobTable
+{
+    int TL, CL, C;
+    __host__ __device__ JobTable(int temporal_layers, int codebook_layers, int books)
+        : TL(temporal_layers), CL(codebook_layers), C(books)
+    {
+    }
+    __host__ __device__ static constexpr std::size_t align(std::size_t n)
+    {
+        return (n + 255) / 256 * 256;
+    }
+    __host__ __device__ int embed() const
+    {
+        return 0;
+    }
+    __host__ __device__ int temporal(int layer, int op) const
+    {
+        return 1 + 4 * layer + op;
+    }
+    __host__ __device__ int prefix(int book) const
+    {
+        return 1 + 4 * TL + book * (4 * CL + 2);
+    }
+    __host__ __device__ int codebook(int book, int layer, int op) const
+    {
+        return prefix(book) + 1 + 4 * layer + op;
+    }
+    __host__ __device__ int head(int book) const
+    {
+        return prefix(book) + 4 * CL + 1;
+    }
+    __host__ __device__ int projections() const
+    {
+        return prefix(C);
+    }
+    __host__ __device__ int attend(bool temporal_layer, int book, int layer) const
+    {
+        return temporal_layer ? layer : TL + book * CL + layer;
+    }
+    __host__ __device__ std::size_t projection_offset(int index) const
+    {
+        return std::size_t(index) * sizeof(Projection);
+    }
+    __host__ __device__ std::size_t attend_offset(int index) const
+    {
+        return align(std::size_t(projections()) * sizeof(Projection)) + std::size_t(index) * sizeof(Attend);
+    }
+    __host__ __device__ std::size_t book_offset(int index) const
+    {
+        return attend_offset(TL + C * CL) + std::size_t(index) * sizeof(BookAttention);
+    }
+    __host__ __device__ std::size_t draw_offset(int book) const
+    {
+        return align(book_offset(C * CL)) + std::size_t(book) * sizeof(Draw);
+    }
+    __host__ __device__ std::size_t condition_offset() const
+    {
+        return align(draw_offset(C));
+    }
+    __host__ __device__ std::size_t bytes() const
+    {
+        return align(condition_offset() + sizeof(Condition));
+    }
 };
 
 // Lane 0's softmax (src/common/probability.cpp:96-122) and subtree masses
@@ -1682,24 +1780,24 @@ __device__ __forceinline__ bool first_lane_masses(const word* logits, uint16_t* 
 // (first_lane_masses), every later lane's by one wave; wave 0 decodes the
 // lanes' symbols in stream order with the decoder held in `state` (LDS)
 // (decode.hip sample_kernel), each once its lane's masses are released.
-__device__ __noinline__ void draw_tokens(const Draw& job, int M, DecoderState* state, const Exchange& exchange,
+__device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, int M, DecoderState* state, Exchange exchange,
                                          uint32_t* error, uint8_t* lds)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
     Draw a;
-    a.book = uniform(job.book);
-    a.books = uniform(job.books);
-    a.logits = uniform(job.logits);
-    a.token_words = uniform(job.token_words);
-    a.current = uniform(job.current);
-    a.tokens = uniform(job.tokens);
-    a.row_base = uniform(job.row_base);
-    a.step = uniform(job.step);
-    a.step_stride = uniform(job.step_stride);
-    a.known = uniform(job.known);
-    a.distributions = uniform(job.distributions);
-    a.payload = uniform(job.payload);
-    a.payload_bytes = uniform(std::size_t(job.payload_bytes));
+    a.book = uniform(job->book);
+    a.books = uniform(job->books);
+    a.logits = uniform(job->logits);
+    a.token_words = uniform(job->token_words);
+    a.current = uniform(job->current);
+    a.tokens = uniform(job->tokens);
+    a.row_base = uniform(job->row_base);
+    a.step = uniform(step);
+    a.step_stride = uniform(job->step_stride);
+    a.known = uniform(job->known);
+    a.distributions = uniform(job->distributions);
+    a.payload = uniform(job->payload);
+    a.payload_bytes = uniform(std::size_t(job->payload_bytes));
     M = uniform(M);
     error = uniform(error);
     float* nodes = reinterpret_cast<float*>(lds);                                         // [8][1024]
@@ -1920,8 +2018,6 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
     __shared__ DecoderState decoder;
     const Exchange x{a.epoch, a.abort};
     const Words L(a.width, a.ffn, a.latent, a.alphabet, a.books, a.temporal_layers, a.codebook_layers);
-    word* const words = reinterpret_cast<word*>(a.words);
-    const FrameModel& model = a.model;
     const int M = a.lanes, G = int(gridDim.x), me = int(blockIdx.x);
     const int TL = a.temporal_layers, CL = a.codebook_layers, C = a.books, width = a.width;
     const int sampler = 0;
@@ -1994,40 +2090,21 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
     // when it does not: building a job reads the model tables from memory, which
     // would put a round trip between every two jobs of the workgroup's own kind.
     const auto member = [&](int kind, int parity = 0) { return first_tile(kind, parity) < kind_tiles[kind]; };
-    const auto linear = [&](bool temporal, int layer, int op) -> const DeviceLinear&
-    { return model.linears[(temporal ? 0 : 4 * TL) + 4 * layer + op]; };
-    const auto norm = [&](bool temporal, int layer, bool mlp) { return (temporal ? 0 : 2 * TL + 1) + 2 * layer + (mlp ? 1 : 0); };
-    const int final_temporal = 2 * TL, final_codebook = 2 * TL + 1 + 2 * CL;
-    const DeviceLinear& temporal_projection = model.linears[4 * (TL + CL)];
-    const DeviceLinear& codebook_projection = model.linears[4 * (TL + CL) + 1];
-    const DeviceLinear& output_projection = model.linears[4 * (TL + CL) + 2];
+    const JobTable T(TL, CL, C);
+    const uint8_t* const jobs = static_cast<const uint8_t*>(a.jobs);
+    const auto projection = [&](int index) { return constant<Projection>(jobs + T.projection_offset(index)); };
+    const int width_tiles = width / tile_rows;
 
-    // One stack layer; `x_of`... words of the layer's input, qkv, attention,
-    // mid residual, hidden and output.
-    const auto run_layer = [&](bool temporal, int layer, int parity, std::size_t in, std::size_t qkv, std::size_t att,
-                               std::size_t mid, std::size_t hid, std::size_t output, const Attend& attention)
+    // One stack layer: its four projections (table entries q + 0..3) and its
+    // attention (table entry `att`, over `time` keys).
+    const auto run_layer = [&](bool temporal, int q, int att, int time, int parity)
     {
         if (member(Kind::qkv, parity))
         {
-            Projection p;
-            p.w = linear(temporal, layer, 0);
-            p.x = words + in;
-            p.gain = model.gain[norm(temporal, layer, false)];
-            p.beta = model.bias[norm(temporal, layer, false)];
-            p.y = words + qkv;
-            p.width = width;
-            p.head_width = a.head_width;
-            if (temporal)
+            const auto p = projection(q);
+            for (int t = first_tile(Kind::qkv, parity); t < 3 * width_tiles; t += step(Kind::qkv))
             {
-                p.keys = a.keys + std::size_t(layer) * a.extent * width;
-                p.values = a.values + std::size_t(layer) * a.extent * width;
-                p.lane_stride = a.lane_stride;
-                p.position = a.position;
-                p.rotations = model.rotations;
-            }
-            for (int t = first_tile(Kind::qkv, parity); t < int(p.w.N) / tile_rows; t += step(Kind::qkv))
-            {
-                project_tile<VW, In::words_norm, Out::qkv>(p, M, t, x, a.error, lds);
+                project_tile<VW, In::words_norm, Out::qkv>(p, a.position, M, t, x, a.error, lds);
             }
         }
         // Temporal attention is a job of its own; with the fused layout a
@@ -2036,65 +2113,48 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
         const bool fused = !temporal && layout.fused;
         if (!fused)
         {
+            const auto attention = constant<Attend>(jobs + T.attend_offset(att));
             for (int t = first_tile(Kind::attend); t < M * a.heads; t += group_size[Kind::attend])
             {
-                attend_item<HW>(attention, t, x, lds);
+                attend_item<HW>(attention, time, t, x, lds);
             }
         }
         if (member(Kind::out))
         {
-            Projection p;
-            p.w = linear(temporal, layer, 1);
-            p.x = words + att;
-            p.residual = words + in;
-            p.y = words + mid;
+            const auto p = projection(q + 1);
             if (!fused)
             {
-                for (int t = first_tile(Kind::out); t < int(p.w.N) / tile_rows; t += group_size[Kind::out])
+                for (int t = first_tile(Kind::out); t < width_tiles; t += group_size[Kind::out])
                 {
-                    project_tile<VW, In::words, Out::residual_words>(p, M, t, x, a.error, lds);
+                    project_tile<VW, In::words, Out::residual_words>(p, 0, M, t, x, a.error, lds);
                 }
             }
             else if constexpr (book_attention_fits<VW, HW>)
             {
                 // One lane per workgroup: each stages its lane's earlier books
                 // while it waits, and no lane waits for another's attention.
-                BookAttention book;
-                book.qkv = attention.qkv;
-                book.book_words = attention.book_words;
-                book.time = attention.time;
-                book.scale = attention.scale;
-                const int tiles = int(p.w.N) / tile_rows;
-                for (int t = first_tile(Kind::out); t < M * tiles; t += group_size[Kind::out])
+                const auto book = constant<BookAttention>(jobs + T.book_offset(att - TL));
+                for (int t = first_tile(Kind::out); t < M * width_tiles; t += group_size[Kind::out])
                 {
-                    book.lane = t / tiles;
-                    project_tile<VW, In::attention, Out::residual_words, HW>(p, M, t % tiles, x, a.error, lds, &book);
+                    project_tile<VW, In::attention, Out::residual_words, HW>(p, 0, M, t % width_tiles, x, a.error, lds,
+                                                                             book, t / width_tiles);
                 }
             }
         }
         if (member(Kind::up, parity))
         {
-            Projection p;
-            p.w = linear(temporal, layer, 2);
-            p.x = words + mid;
-            p.gain = model.gain[norm(temporal, layer, true)];
-            p.beta = model.bias[norm(temporal, layer, true)];
-            p.y = words + hid;
-            for (int t = first_tile(Kind::up, parity); t < int(p.w.N) / tile_rows; t += step(Kind::up))
+            const auto p = projection(q + 2);
+            for (int t = first_tile(Kind::up, parity); t < a.ffn / tile_rows; t += step(Kind::up))
             {
-                project_tile<VW, In::words_norm, Out::gelu>(p, M, t, x, a.error, lds);
+                project_tile<VW, In::words_norm, Out::gelu>(p, 0, M, t, x, a.error, lds);
             }
         }
         if (member(Kind::down, parity))
         {
-            Projection p;
-            p.w = linear(temporal, layer, 3);
-            p.x = words + hid;
-            p.residual = words + mid;
-            p.y = words + output;
-            for (int t = first_tile(Kind::down, parity); t < int(p.w.N) / tile_rows; t += step(Kind::down))
+            const auto p = projection(q + 3);
+            for (int t = first_tile(Kind::down, parity); t < width_tiles; t += step(Kind::down))
             {
-                project_tile<VF, In::words, Out::residual_words>(p, M, t, x, a.error, lds);
+                project_tile<VF, In::words, Out::residual_words>(p, 0, M, t, x, a.error, lds);
             }
         }
     };
@@ -2102,101 +2162,47 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
     // Temporal stack: feedback embeddings of the previous frame, then layers.
     if (member(Kind::embed))
     {
-        Projection p;
-        p.w = temporal_projection;
-        p.embeddings = model.embeddings;
-        p.alphabet = a.alphabet;
-        p.books = C;
-        p.tokens = a.current;
-        p.token_stride = C;
-        p.y = words + L.t_x(0);
-        for (int t = first_tile(Kind::embed); t < int(p.w.N) / tile_rows; t += group_size[Kind::embed])
+        const auto p = projection(T.embed());
+        for (int t = first_tile(Kind::embed); t < width_tiles; t += group_size[Kind::embed])
         {
-            project_tile<VL, In::embed_sum, Out::plain>(p, M, t, x, a.error, lds);
+            project_tile<VL, In::embed_sum, Out::plain>(p, 0, M, t, x, a.error, lds);
         }
     }
     for (int l = 0; l < TL; ++l)
     {
-        Attend at;
-        at.heads = a.heads;
-        at.width = width;
-        at.scale = a.scale;
-        at.time = a.position + 1;
-        at.keys = a.keys + std::size_t(l) * a.extent * width;
-        at.values = a.values + std::size_t(l) * a.extent * width;
-        at.lane_stride = a.lane_stride;
-        at.qkv = words + L.t_qkv(l);
-        at.out = words + L.t_att(l);
-        run_layer(true, l, l % 2, L.t_x(l), L.t_qkv(l), L.t_att(l), L.t_mid(l), L.t_hid(l), L.t_x(l + 1), at);
+        run_layer(true, T.temporal(l, 0), T.attend(true, 0, l), a.position + 1, l % 2);
     }
     // Book 0's input.
     if (first_tile(Kind::condition) == 0)
     {
-        condition_rows<VW>(words + L.t_x(TL), model.gain[final_temporal], model.bias[final_temporal], model.positions,
-                           words + L.c_x(0, 0), M, x);
+        const auto c = constant<Condition>(jobs + T.condition_offset());
+        condition_rows<VW>(c->in, c->gain, c->bias, c->positions, c->out, M, x);
     }
     for (int b = 0; b < C; ++b)
     {
         if (b > 0 && member(Kind::prefix))
         {
-            Projection p;
-            p.w = codebook_projection;
-            p.embeddings = model.embeddings;
-            p.alphabet = a.alphabet;
-            p.book = b - 1;
-            p.token_words = words + L.c_token(b - 1, CL);
-            p.prefix_in = b > 1 ? words + L.c_prefix(b - 1) : nullptr;
-            p.prefix_out = words + L.c_prefix(b);
-            p.residual_row = model.positions + std::size_t(b) * width;
-            p.y = words + L.c_x(b, 0);
-            for (int t = first_tile(Kind::prefix); t < int(p.w.N) / tile_rows; t += group_size[Kind::prefix])
+            const auto p = projection(T.prefix(b));
+            for (int t = first_tile(Kind::prefix); t < width_tiles; t += group_size[Kind::prefix])
             {
-                project_tile<VL, In::embed_accumulate, Out::residual_row>(p, M, t, x, a.error, lds);
+                project_tile<VL, In::embed_accumulate, Out::residual_row>(p, 0, M, t, x, a.error, lds);
             }
         }
         for (int l = 0; l < CL; ++l)
         {
-            Attend at;
-            at.heads = a.heads;
-            at.width = width;
-            at.scale = a.scale;
-            at.time = b + 1;
-            at.qkv = words + L.c_qkv(0, l);
-            at.book_words = L.book;
-            at.out = words + L.c_att(b, l);
-            run_layer(false, l, (TL + b * CL + l) % 2, L.c_x(b, l), L.c_qkv(b, l), L.c_att(b, l), L.c_mid(b, l),
-                      L.c_hid(b, l), L.c_x(b, l + 1), at);
+            run_layer(false, T.codebook(b, l, 0), T.attend(false, b, l), b + 1, (TL + b * CL + l) % 2);
         }
         if (member(Kind::head))
         {
-            Projection p;
-            p.w = output_projection;
-            p.x = words + L.c_x(b, CL);
-            p.gain = model.gain[final_codebook];
-            p.beta = model.bias[final_codebook];
-            p.y = words + L.c_logits(b, CL);
-            for (int t = first_tile(Kind::head); t < int(p.w.N) / tile_rows; t += group_size[Kind::head])
+            const auto p = projection(T.head(b));
+            for (int t = first_tile(Kind::head); t < a.alphabet / tile_rows; t += group_size[Kind::head])
             {
-                project_tile<VW, In::words_norm, Out::plain>(p, M, t, x, a.error, lds);
+                project_tile<VW, In::words_norm, Out::plain>(p, 0, M, t, x, a.error, lds);
             }
         }
         if (me == sampler)
         {
-            Draw d;
-            d.book = b;
-            d.books = C;
-            d.logits = words + L.c_logits(b, CL);
-            d.token_words = words + L.c_token(b, CL);
-            d.current = a.current;
-            d.tokens = a.tokens;
-            d.row_base = a.row_base;
-            d.step = a.step;
-            d.step_stride = a.step_stride;
-            d.known = a.known;
-            d.distributions = a.distributions;
-            d.payload = a.payload;
-            d.payload_bytes = a.payload_bytes;
-            draw_tokens(d, M, &decoder, x, a.error, lds);
+            draw_tokens(constant<Draw>(jobs + T.draw_offset(b)), a.step, M, &decoder, x, a.error, lds);
         }
     }
     if (me == sampler && a.known == nullptr)
@@ -2245,6 +2251,155 @@ template <int VW, int VF, int VL, int HW> void launch_frame(const FrameArgs& a, 
 }
 } // namespace
 
+std::vector<uint8_t> frame_job_table(const FrameArgs& a)
+{
+    const int TL = a.temporal_layers, CL = a.codebook_layers, C = a.books, width = a.width;
+    require(a.words && a.model.linears && a.model.gain && a.model.bias, "frame job table: arguments");
+    const Words L(a.width, a.ffn, a.latent, a.alphabet, C, TL, CL);
+    const JobTable T(TL, CL, C);
+    std::vector<uint8_t> table(T.bytes(), 0);
+    word* const words = reinterpret_cast<word*>(a.words);
+    const FrameModel& model = a.model;
+    const auto put = [&](std::size_t offset, const auto& value)
+    {
+        require(offset + sizeof value <= table.size(), "frame job table: layout");
+        std::memcpy(table.data() + offset, &value, sizeof value);
+    };
+    const auto linear = [&](bool temporal, int layer, int op) { return model.linears[(temporal ? 0 : 4 * TL) + 4 * layer + op]; };
+    const auto norm = [&](bool temporal, int layer, bool mlp) { return (temporal ? 0 : 2 * TL + 1) + 2 * layer + (mlp ? 1 : 0); };
+    // One stack layer (src/common/cpu_transformer.tpp:139-173): word ranges of
+    // its input, qkv, attention, mid residual, hidden and output.
+    const auto layer = [&](bool temporal, int l, int book, std::size_t in, std::size_t qkv, std::size_t att,
+                           std::size_t mid, std::size_t hid, std::size_t output)
+    {
+        const int q = temporal ? T.temporal(l, 0) : T.codebook(book, l, 0);
+        Projection p;
+        p.w = linear(temporal, l, 0);
+        p.x = words + in;
+        p.gain = model.gain[norm(temporal, l, false)];
+        p.beta = model.bias[norm(temporal, l, false)];
+        p.y = words + qkv;
+        p.width = width;
+        p.head_width = a.head_width;
+        if (temporal)
+        {
+            p.keys = a.keys + std::size_t(l) * a.extent * width;
+            p.values = a.values + std::size_t(l) * a.extent * width;
+            p.lane_stride = a.lane_stride;
+            p.rotations = model.rotations;
+        }
+        put(T.projection_offset(q), p);
+        Projection o;
+        o.w = linear(temporal, l, 1);
+        o.x = words + att;
+        o.residual = words + in;
+        o.y = words + mid;
+        put(T.projection_offset(q + 1), o);
+        Projection u;
+        u.w = linear(temporal, l, 2);
+        u.x = words + mid;
+        u.gain = model.gain[norm(temporal, l, true)];
+        u.beta = model.bias[norm(temporal, l, true)];
+        u.y = words + hid;
+        put(T.projection_offset(q + 2), u);
+        Projection d;
+        d.w = linear(temporal, l, 3);
+        d.x = words + hid;
+        d.residual = words + mid;
+        d.y = words + output;
+        put(T.projection_offset(q + 3), d);
+        Attend at;
+        at.heads = a.heads;
+        at.width = width;
+        at.scale = a.scale;
+        at.out = words + att;
+        if (temporal)
+        {
+            at.keys = a.keys + std::size_t(l) * a.extent * width;
+            at.values = a.values + std::size_t(l) * a.extent * width;
+            at.lane_stride = a.lane_stride;
+            at.qkv = words + qkv;
+        }
+        else
+        {
+            at.qkv = words + L.c_qkv(0, l);
+            at.book_words = L.book;
+            BookAttention fused;
+            fused.qkv = at.qkv;
+            fused.book_words = at.book_words;
+            fused.time = book + 1;
+            fused.scale = a.scale;
+            put(T.book_offset(book * CL + l), fused);
+        }
+        put(T.attend_offset(T.attend(temporal, book, l)), at);
+    };
+
+    Projection embed;
+    embed.w = model.linears[4 * (TL + CL)];
+    embed.embeddings = model.embeddings;
+    embed.alphabet = a.alphabet;
+    embed.books = C;
+    embed.tokens = a.current;
+    embed.token_stride = C;
+    embed.y = words + L.t_x(0);
+    put(T.projection_offset(T.embed()), embed);
+    for (int l = 0; l < TL; ++l)
+    {
+        layer(true, l, 0, L.t_x(l), L.t_qkv(l), L.t_att(l), L.t_mid(l), L.t_hid(l), L.t_x(l + 1));
+    }
+    Condition condition;
+    condition.in = words + L.t_x(TL);
+    condition.gain = model.gain[2 * TL];
+    condition.bias = model.bias[2 * TL];
+    condition.positions = model.positions;
+    condition.out = words + L.c_x(0, 0);
+    put(T.condition_offset(), condition);
+    for (int b = 0; b < C; ++b)
+    {
+        if (b > 0)
+        {
+            Projection prefix;
+            prefix.w = model.linears[4 * (TL + CL) + 1];
+            prefix.embeddings = model.embeddings;
+            prefix.alphabet = a.alphabet;
+            prefix.book = b - 1;
+            prefix.token_words = words + L.c_token(b - 1, CL);
+            prefix.prefix_in = b > 1 ? words + L.c_prefix(b - 1) : nullptr;
+            prefix.prefix_out = words + L.c_prefix(b);
+            prefix.residual_row = model.positions + std::size_t(b) * width;
+            prefix.y = words + L.c_x(b, 0);
+            put(T.projection_offset(T.prefix(b)), prefix);
+        }
+        for (int l = 0; l < CL; ++l)
+        {
+            layer(false, l, b, L.c_x(b, l), L.c_qkv(b, l), L.c_att(b, l), L.c_mid(b, l), L.c_hid(b, l),
+                  L.c_x(b, l + 1));
+        }
+        Projection head;
+        head.w = model.linears[4 * (TL + CL) + 2];
+        head.x = words + L.c_x(b, CL);
+        head.gain = model.gain[2 * TL + 1 + 2 * CL];
+        head.beta = model.bias[2 * TL + 1 + 2 * CL];
+        head.y = words + L.c_logits(b, CL);
+        put(T.projection_offset(T.head(b)), head);
+        Draw d;
+        d.book = b;
+        d.books = C;
+        d.logits = words + L.c_logits(b, CL);
+        d.token_words = words + L.c_token(b, CL);
+        d.current = a.current;
+        d.tokens = a.tokens;
+        d.row_base = a.row_base;
+        d.step_stride = a.step_stride;
+        d.known = a.known;
+        d.distributions = a.distributions;
+        d.payload = a.payload;
+        d.payload_bytes = a.payload_bytes;
+        put(T.draw_offset(b), d);
+    }
+    return table;
+}
+
 bool frame_supported(int width, int heads, int head_width, int ffn, int latent, int alphabet, int lanes)
 {
     const bool reference = width == 512 && head_width == 128 && ffn == 2048 && latent == 1024;
@@ -2266,7 +2421,7 @@ void frame_step(const FrameArgs& a, hipStream_t stream)
     require(a.position >= 0 && a.position < a.extent && a.extent <= max_blocks * 64, "frame step: position");
     require(a.books >= 1 && a.books <= max_books && a.temporal_layers >= 1 && a.codebook_layers >= 1,
             "frame step: layers");
-    require(a.words && a.abort && a.error && a.current && a.tokens && a.row_base && a.epoch != 0,
+    require(a.words && a.abort && a.error && a.current && a.tokens && a.row_base && a.jobs && a.epoch != 0,
             "frame step: arguments");
     require(a.known || (a.state && a.payload), "frame step: needs known tokens or a decoder");
     if (a.width == 512)

@@ -26,9 +26,11 @@
 
 #include "decode.hpp"
 
+#include <vector>
+
 namespace tsac_hip
 {
-// Device-resident model tables for the frame kernel.
+// The model as frame_job_table reads it: host arrays of device pointers.
 struct FrameModel
 {
     const DeviceLinear* linears = nullptr; // reference projection order
@@ -67,6 +69,7 @@ struct FrameArgs
     unsigned long long* words = nullptr; // frame_exchange_words() words, zero before the first step
     uint32_t epoch = 0;                  // nonzero, different for every launch over the same words
     unsigned* abort = nullptr;           // zero before the first step; nonzero after a stalled wait
+    const void* jobs = nullptr;          // device copy of frame_job_table(*this), unchanged during a launch
 };
 
 // Geometries the frame kernel is instantiated for, at 1..8 lanes.
@@ -74,5 +77,10 @@ bool frame_supported(int width, int heads, int head_width, int ffn, int latent, 
 // Exchange words one step needs.
 std::size_t frame_exchange_words(int width, int ffn, int latent, int alphabet, int books, int temporal_layers,
                                  int codebook_layers);
+// Every job's descriptor (weights, norms, exchange-word ranges, caches) for the
+// launches of one pass, built on the host from the pointers in `args` (all but
+// position, step, lanes and epoch, which the launches pass themselves); the
+// launches read it from device memory through FrameArgs::jobs.
+std::vector<uint8_t> frame_job_table(const FrameArgs& args);
 void frame_step(const FrameArgs& args, hipStream_t stream);
 } // namespace tsac_hip
