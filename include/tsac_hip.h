@@ -159,8 +159,11 @@ int tsac_hip_distributions(tsac_hip_session* session, const tsac_hip_header* hea
 /* Wall-clock split of the session's last encode/decode/distributions call
  * (seconds): [0] GPU model work, [1] host range coding, [2] total, [3] the
  * host-to-device copy of the call's input (tokens, or the stream's payload),
- * included in [0] and [2]. No counterpart in the reference; for callers that
- * report throughput with inputs already in device memory. */
+ * included in [0] and [2]; for decode-side passes [4] the GPU time of the
+ * frame-step loop, between two HIP events on the session's stream, and [5] the
+ * number of frame steps in it (both 0 otherwise). No counterpart in the
+ * reference; for callers that report throughput with inputs already in device
+ * memory. */
 int tsac_hip_session_timing(const tsac_hip_session* session, double* seconds, size_t count);
 
 /* ---- operators on device memory (hipStream_t passed as void*) -------------- */

@@ -272,6 +272,8 @@ Session::Session(std::shared_ptr<const Model> model) : model_(std::move(model))
     check_hip(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
     check_hip(hipEventCreate(&upload_start_), "hipEventCreate");
     check_hip(hipEventCreate(&upload_stop_), "hipEventCreate");
+    check_hip(hipEventCreate(&steps_start_), "hipEventCreate");
+    check_hip(hipEventCreate(&steps_stop_), "hipEventCreate");
     errors_ = DeviceBuffer(256);
     pinned_errors_.reserve(256);
 }
@@ -287,10 +289,26 @@ Session::~Session()
     {
         (void)hipEventDestroy(upload_start_);
     }
-    if (upload_stop_)
+    for (hipEvent_t e : {upload_stop_, steps_start_, steps_stop_})
     {
-        (void)hipEventDestroy(upload_stop_);
+        if (e)
+        {
+            (void)hipEventDestroy(e);
+        }
     }
+}
+
+double Session::steps_seconds()
+{
+    if (!stepped_)
+    {
+        return 0.0;
+    }
+    stepped_ = false;
+    float ms = 0.0f;
+    check_hip(hipEventSynchronize(steps_stop_), "hipEventSynchronize");
+    check_hip(hipEventElapsedTime(&ms, steps_start_, steps_stop_), "hipEventElapsedTime");
+    return ms / 1000.0;
 }
 
 void Session::upload_input(void* device, const void* host, std::size_t bytes)
@@ -650,7 +668,7 @@ std::vector<uint8_t> Session::encode(Header h, const uint16_t* tokens, std::size
     });
     const auto bytes = frame_normal(h, crc, encoder.finish());
     const double t2 = now();
-    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds()};
+    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), 0.0, 0.0};
     return bytes;
 }
 
@@ -688,7 +706,8 @@ std::vector<uint16_t> Session::decode(const uint8_t* stream, std::size_t length,
     require(token_crc32(tokens.data(), tokens.size()) == h.token_crc,
             "decoded tokens fail the stream's CRC-32 check");
     const double t2 = now();
-    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds()};
+    const double steps = double(Lanes(h).steps());
+    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), steps_seconds(), steps};
     return tokens;
 }
 
@@ -710,6 +729,7 @@ void Session::distributions(Header h, const uint16_t* tokens, std::size_t count,
     }
     check_errors();
     const double t1 = now();
-    timing_ = {t1 - t0, 0.0, t1 - t0, input_seconds()};
+    const double steps = decode_pass ? double(Lanes(h).steps()) : 0.0;
+    timing_ = {t1 - t0, 0.0, t1 - t0, input_seconds(), decode_pass ? steps_seconds() : 0.0, steps};
 }
 } // namespace tsac_hip

@@ -192,10 +192,12 @@ public:
     // stepwise (GEMV) driver instead of the batched (GEMM) one.
     void distributions(Header header, const uint16_t* tokens, std::size_t count, bool decode_pass,
                        uint16_t* out);
-    // Seconds of the last call: GPU model work, host range coding, total, and
-    // the host-to-device copy of the call's input (tokens or payload), which
-    // the first and third include.
-    std::array<double, 4> timing() const
+    // Seconds of the last call: GPU model work, host range coding, total, the
+    // host-to-device copy of the call's input (tokens or payload), which the
+    // first and third include, then (decode-side passes) the GPU time of the
+    // frame-step loop between two events on the session stream and the number
+    // of frame steps in it.
+    std::array<double, 6> timing() const
     {
         return timing_;
     }
@@ -208,6 +210,8 @@ private:
     // (after the stream has drained) is that copy's duration.
     void upload_input(void* device, const void* host, std::size_t bytes);
     double input_seconds();
+    // GPU seconds between the events around the last stepwise loop.
+    double steps_seconds();
     void validate(const Header& h, const uint16_t* tokens, std::size_t count) const;
     // Batched known-token pass. Writes either the BF16 distributions of every
     // token (distributions != null) or its ten Q15 splits (splits != null).
@@ -233,8 +237,10 @@ private:
     Arena arena_;
     DeviceBuffer errors_;
     PinnedBuffer pinned_errors_, staging_, staging_nodes_, staging_tokens_;
-    std::array<double, 4> timing_{};
+    std::array<double, 6> timing_{};
     hipEvent_t upload_start_ = nullptr, upload_stop_ = nullptr;
+    hipEvent_t steps_start_ = nullptr, steps_stop_ = nullptr;
+    bool stepped_ = false;
     bool uploaded_ = false;
 };
 } // namespace tsac_hip

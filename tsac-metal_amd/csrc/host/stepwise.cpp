@@ -369,6 +369,7 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
 
     Graph graph;
     std::size_t context_used = 0;
+    check_hip(hipEventRecord(steps_start_, stream_), "hipEventRecord");
     for (std::size_t step = 0; step < lanes.steps(); ++step)
     {
         const std::size_t active = step < lanes.base ? independent : lanes.extra * G;
@@ -436,6 +437,8 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
             ++context_used;
         }
     }
+    check_hip(hipEventRecord(steps_stop_, stream_), "hipEventRecord");
+    stepped_ = true;
     if (tokens_out)
     {
         check_hip(hipMemcpyAsync(tokens_out, tokens, symbols * 2, hipMemcpyDeviceToHost, stream_),

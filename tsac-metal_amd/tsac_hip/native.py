@@ -291,9 +291,10 @@ class HipSession:
         return out
 
     def timing(self):
-        t = (C.c_double * 4)()
-        check(library().tsac_hip_session_timing(self.handle, t, 4))
-        return {"model": t[0], "range_coding": t[1], "total": t[2], "input_upload": t[3]}
+        t = (C.c_double * 6)()
+        check(library().tsac_hip_session_timing(self.handle, t, 6))
+        return {"model": t[0], "range_coding": t[1], "total": t[2], "input_upload": t[3], "steps_gpu": t[4],
+                "steps": int(t[5])}
 
 
 # ---------------------------------------------------------------- operators on torch tensors
