@@ -174,6 +174,83 @@ class _Kernels:
         return self._f("token_crc32")(ptr(t, C.c_uint16), t.size)
 
 
+class OrcConv(C.Structure):
+    _fields_ = [(n, sz) for n in ("input", "output", "kernel", "stride", "padding", "dilation")] + \
+        [("transposed", C.c_int)]
+
+
+class OrcDac(C.Structure):
+    _fields_ = [("synthesis", C.c_int), ("channels", C.c_uint), ("weights", f32p * 30), ("bias", f32p * 30),
+                ("alpha", f32p * 29)]
+
+
+class OrcRvq(C.Structure):
+    _fields_ = [("books", C.c_uint)] + [(n, f32p * 12) for n in (
+        "codebook", "search", "input_weights", "input_bias", "output_weights", "output_bias")]
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+class _DspKernels:
+    """DAC/RVQ primitives shared by the oracle (orc_) and the compiled reference (ref_)."""
+
+    def _declare_dsp(self):
+        f = self._f
+        f("conv1d").argtypes = [C.POINTER(OrcConv), f32p, f32p, f32p, sz, sz, f32p] + \
+            ([C.c_uint] if self.prefix == "orc_" else [])
+        f("snake").argtypes = [f32p, sz, sz, f32p, f32p]
+        f("fold_dac_weight_norm").argtypes = [f32p, f32p, sz, sz, f32p]
+        f("normalize_search").argtypes = [f32p, f32p]
+        f("normalize_search").restype = None
+        f("nearest_rvq").argtypes = [f32p, f32p]
+        f("nearest_rvq").restype = C.c_uint16
+        f("project_codebook").argtypes = [C.c_uint16, f32p, f32p, f32p, f32p]
+        f("project_codebook").restype = None
+
+    def conv1d(self, config: OrcConv, w, bias, x, frames, groups=1, threads=4):
+        x, w, bias = _f32(x), _f32(w), _f32(bias)
+        if config.transposed:
+            span = (config.kernel - 1) * config.dilation + 1
+            out_frames = (frames - 1) * config.stride + span - 2 * config.padding
+        else:
+            out_frames = (frames + 2 * config.padding - ((config.kernel - 1) * config.dilation + 1)) // config.stride + 1
+        y = np.zeros(out_frames * groups * config.output, np.float32)
+        args = [C.byref(config), ptr(w, C.c_float), ptr(bias, C.c_float), ptr(x, C.c_float), frames, groups,
+                ptr(y, C.c_float)] + ([threads] if self.prefix == "orc_" else [])
+        self._check(self._f("conv1d")(*args))
+        return y
+
+    def snake(self, x, channels, alpha):
+        x, alpha = _f32(x), _f32(alpha)
+        out = np.zeros_like(x)
+        self._check(self._f("snake")(ptr(x, C.c_float), x.size, channels, ptr(alpha, C.c_float), ptr(out, C.c_float)))
+        return out
+
+    def fold_dac_weight_norm(self, v, g, fan_in):
+        v, g = _f32(v), _f32(g)
+        out = np.zeros(v.size, np.float32)
+        self._check(self._f("fold_dac_weight_norm")(ptr(v, C.c_float), ptr(g, C.c_float), fan_in, g.size,
+                                                    ptr(out, C.c_float)))
+        return out
+
+    def normalize_search(self, x):
+        x = _f32(x)
+        out = np.zeros(8, np.float32)
+        self._f("normalize_search")(ptr(x, C.c_float), ptr(out, C.c_float))
+        return out
+
+    def nearest_rvq(self, x, vectors):
+        return int(self._f("nearest_rvq")(ptr(_f32(x), C.c_float), ptr(_f32(vectors), C.c_float)))
+
+    def project_codebook(self, index, codebook, weights, bias):
+        out = np.zeros(1024, np.float32)
+        self._f("project_codebook")(index, ptr(_f32(codebook), C.c_float), ptr(_f32(weights), C.c_float),
+                                    ptr(_f32(bias), C.c_float), ptr(out, C.c_float))
+        return out
+
+
 def model_desc(model):
     """Builds a ModelDesc over the numpy arrays of a tsac_hip.synthetic.Model.
     The returned tuple keeps every array alive while the descriptor is used."""
@@ -199,10 +276,22 @@ def header(frames, batch, groups, codebooks, model_channels=2, method=1) -> Head
     return Header(method, groups, model_channels, codebooks, frames, batch)
 
 
-class Oracle(_Kernels):
+class Oracle(_Kernels, _DspKernels):
     def __init__(self):
         lib = _load(ORACLE_PATH)
         super().__init__(lib, "orc_")
+        self._declare_dsp()
+        lib.orc_dac_sine_squared.argtypes = [C.c_float]
+        lib.orc_dac_sine_squared.restype = C.c_float
+        lib.orc_expand_bf8.argtypes = [i8p, u16p, sz, sz, sz, f32p]
+        lib.orc_dac_conv_config.argtypes = [C.c_int, C.c_uint, C.c_uint, C.POINTER(OrcConv)]
+        lib.orc_dac_apply.argtypes = [C.POINTER(OrcDac), f32p, sz, f32p, C.POINTER(sz), C.c_uint]
+        lib.orc_rvq_encode.argtypes = [C.POINTER(OrcRvq), f32p, sz, u16p]
+        lib.orc_rvq_decode.argtypes = [C.POINTER(OrcRvq), u16p, sz, f32p]
+        lib.orc_analyze_audio.argtypes = [C.POINTER(OrcDac), C.POINTER(OrcRvq), f32p, sz, sz, sz, C.c_uint, u16p]
+        lib.orc_synthesize_audio.argtypes = [C.POINTER(OrcDac), C.POINTER(OrcRvq), u16p, sz, sz, sz, C.c_uint, f32p]
+        lib.orc_pcm16.argtypes = [C.c_float]
+        lib.orc_pcm16.restype = C.c_int16
         lib.orc_attention.argtypes = [u16p, u16p, u16p, sz, sz, sz, C.c_float, C.c_int, u16p]
         lib.orc_gelu_batch.argtypes = [u16p, sz, u16p]
         lib.orc_range_roundtrip_encode.argtypes = [f32p, u16p, sz, sz, u8p, sz, C.POINTER(sz)]
@@ -271,6 +360,36 @@ class Oracle(_Kernels):
 
     def model(self, model) -> "OracleModel":
         return OracleModel(self, model)
+
+    def dac_sine_squared(self, phase: float) -> float:
+        return self.lib.orc_dac_sine_squared(phase)
+
+    def dac_conv_config(self, synthesis: bool, channels: int, index: int) -> OrcConv:
+        c = OrcConv()
+        self._check(self.lib.orc_dac_conv_config(int(synthesis), channels, index, C.byref(c)))
+        return c
+
+    def expand_bf8(self, values, scales, dims):
+        rows, cols, outer = dims
+        values = np.ascontiguousarray(values, np.int8)
+        scales = np.ascontiguousarray(scales, np.uint16)
+        out = np.zeros(rows * cols * outer, np.float32)
+        self._check(self.lib.orc_expand_bf8(ptr(values, C.c_int8), ptr(scales, C.c_uint16), rows, cols, outer,
+                                            ptr(out, C.c_float)))
+        return out
+
+    def prepare_convolution(self, conv):
+        """Convolution::from_weights preparation (src/common/dsp.tpp:117-155):
+        expand the source encoding, then fold the DAC weight norm per stored column."""
+        rows, cols, outer = conv.dims
+        values = self.expand_bf8(conv.values, conv.scales, conv.dims) if conv.bf8 else _f32(conv.values)
+        return self.fold_dac_weight_norm(values, conv.gain, rows * cols)
+
+    def dac_model(self, model, books=None) -> "OracleDacModel":
+        return OracleDacModel(self, model, books)
+
+    def pcm16(self, x: float) -> int:
+        return int(self.lib.orc_pcm16(x))
 
 
 class OracleModel:
@@ -350,12 +469,13 @@ class OracleModel:
         return out
 
 
-class Reference(_Kernels):
+class Reference(_Kernels, _DspKernels):
     """The reference's own scalar sources (compiled here from the reference tree)."""
 
     def __init__(self):
         lib = _load(REF_PATH)
         super().__init__(lib, "ref_")
+        self._declare_dsp()
         lib.ref_gelu_table.argtypes = [u16p, sz]
         lib.ref_attention.argtypes = [u16p, u16p, u16p, sz, sz, sz, C.c_float, C.c_int, u16p]
         lib.ref_range_encode.argtypes = [f32p, u16p, sz, sz, u8p, sz, C.POINTER(sz)]
@@ -436,3 +556,98 @@ class Reference(_Kernels):
 
 def host_threads() -> int:
     return len(os.sched_getaffinity(0))
+
+
+# ---------------------------------------------------------------- DAC and RVQ models
+
+
+class OracleDacModel:
+    """A tsac_hip.synthetic.DacModel prepared the way the reference's runtime
+    prepares it (BF8 expansion and DAC weight-norm folding, RVQ search vectors
+    and folded projections), bound to the oracle's DAC graphs and quantizer."""
+
+    def __init__(self, oracle: "Oracle", model, books=None):
+        self.oracle, self.lib, self.model = oracle, oracle.lib, model
+        self.books = books or len(model.codebook)
+        self._keep = []
+        self.graphs = {}
+        for synthesis in (False, True):
+            convs = model.synthesis if synthesis else model.analysis
+            alphas = model.synthesis_alpha if synthesis else model.analysis_alpha
+            desc = OrcDac()
+            desc.synthesis = int(synthesis)
+            desc.channels = model.channels
+            prepared = []
+            for i, conv in enumerate(convs):
+                w = oracle.prepare_convolution(conv)
+                b = _f32(conv.bias)
+                prepared.append(w)
+                self._keep += [w, b]
+                desc.weights[i] = ptr(w, C.c_float)
+                desc.bias[i] = ptr(b, C.c_float)
+            for i, a in enumerate(alphas):
+                a = _f32(a)
+                self._keep.append(a)
+                desc.alpha[i] = ptr(a, C.c_float)
+            self.graphs[synthesis] = (desc, prepared)
+        q = OrcRvq()
+        q.books = self.books
+        self.rvq_tensors = []
+        for book in range(self.books):
+            codebook = _f32(model.codebook[book])
+            search = np.stack([oracle.normalize_search(row) for row in codebook])
+            input_weights = oracle.fold_dac_weight_norm(model.in_v[book], model.in_g[book], 1024)
+            output_weights = oracle.fold_dac_weight_norm(model.out_v[book], model.out_g[book], 8)
+            tensors = (codebook, _f32(search), input_weights, _f32(model.in_bias[book]), output_weights,
+                       _f32(model.out_bias[book]))
+            self.rvq_tensors.append(tensors)
+            self._keep += list(tensors)
+            for name, t in zip(("codebook", "search", "input_weights", "input_bias", "output_weights",
+                                "output_bias"), tensors):
+                getattr(q, name)[book] = ptr(t, C.c_float)
+        self.rvq = q
+
+    def apply(self, synthesis: bool, x, frames, threads=8):
+        """One DAC graph on one group: analysis PCM [frames][channels] -> latent
+        [frames/512][1024]; synthesis latent [frames][1024] -> [frames*512][channels]."""
+        desc = self.graphs[synthesis][0]
+        x = _f32(x)
+        out_frames = frames * 512 if synthesis else frames // 512
+        out = np.zeros(out_frames * (self.model.channels if synthesis else 1024), np.float32)
+        produced = sz()
+        self.oracle._check(self.lib.orc_dac_apply(C.byref(desc), ptr(x, C.c_float), frames, ptr(out, C.c_float),
+                                                  C.byref(produced), threads))
+        assert produced.value == out_frames
+        return out
+
+    def rvq_encode(self, latent, frames):
+        latent = _f32(latent)
+        tokens = np.zeros(frames * self.books, np.uint16)
+        self.oracle._check(self.lib.orc_rvq_encode(C.byref(self.rvq), ptr(latent, C.c_float), frames,
+                                                   ptr(tokens, C.c_uint16)))
+        return tokens
+
+    def rvq_decode(self, tokens, frames):
+        tokens = np.ascontiguousarray(tokens, np.uint16)
+        latent = np.zeros(frames * 1024, np.float32)
+        self.oracle._check(self.lib.orc_rvq_decode(C.byref(self.rvq), ptr(tokens, C.c_uint16), frames,
+                                                   ptr(latent, C.c_float)))
+        return latent
+
+    def analyze_audio(self, pcm, frames, groups=1, chunk=400, threads=8):
+        """Padded PCM [groups][frames*512][channels] -> tokens [frame][group][book]."""
+        pcm = _f32(pcm)
+        tokens = np.zeros(frames * groups * self.books, np.uint16)
+        self.oracle._check(self.lib.orc_analyze_audio(C.byref(self.graphs[False][0]), C.byref(self.rvq),
+                                                      ptr(pcm, C.c_float), frames, groups, chunk, threads,
+                                                      ptr(tokens, C.c_uint16)))
+        return tokens
+
+    def synthesize_audio(self, tokens, frames, groups=1, chunk=400, threads=8):
+        """Tokens -> float PCM [frames*512][groups*channels]."""
+        tokens = np.ascontiguousarray(tokens, np.uint16)
+        pcm = np.zeros(frames * 512 * groups * self.model.channels, np.float32)
+        self.oracle._check(self.lib.orc_synthesize_audio(C.byref(self.graphs[True][0]), C.byref(self.rvq),
+                                                         ptr(tokens, C.c_uint16), frames, groups, chunk, threads,
+                                                         ptr(pcm, C.c_float)))
+        return pcm

@@ -17,6 +17,9 @@
 #include "format/entropy.hpp"
 #include "format/range.hpp"
 #include "scalar/kernels.hpp"
+#include "scalar/dsp.hpp"
+#include "weights/normalization.hpp"
+#include "weights/preparation.hpp"
 
 #include "tsac_oracle.h"
 
@@ -25,6 +28,12 @@
 #include <string>
 
 using namespace tsac;
+
+namespace tsac
+{
+// Defined in src/common/rvq.cpp, declared there only by src/common/rvq.tpp.
+std::uint16_t nearest_rvq_index(std::span<const float, 8> input, std::span<const float> vectors);
+} // namespace tsac
 
 namespace
 {
@@ -542,5 +551,61 @@ int ref_distributions(const orc_model_desc* desc, const orc_header* header,
                                         predictor.commit(p, tokens[p.token_offset]);
                                     });
         });
+}
+
+// ---- DAC and RVQ primitives (src/scalar/dsp.cpp, src/weights/*.cpp, src/common/rvq.cpp)
+
+int ref_conv1d(const orc_conv* c, const float* w, const float* bias, const float* x, std::size_t frames,
+               std::size_t groups, float* y)
+{
+    return guarded(
+        [&]
+        {
+            const Conv1dConfig config{c->in, c->out, c->kernel, c->stride, c->padding, c->dilation,
+                                      c->transposed ? ConvolutionKind::transposed : ConvolutionKind::ordinary};
+            const std::size_t count = c->in * c->kernel * c->out;
+            const scalar::Conv1d conv(config, std::span(w, count), std::span(bias, c->out));
+            const auto out = conv.apply(std::span(x, frames * groups * c->in), SignalShape{c->in, frames, groups});
+            std::memcpy(y, out.values.data(), out.values.size() * sizeof(float));
+        });
+}
+
+int ref_snake(const float* x, std::size_t count, std::size_t channels, const float* alpha, float* out)
+{
+    return guarded(
+        [&]
+        {
+            Signal result;
+            scalar::snake_dac_into(std::span(x, count), SignalShape{channels, count / channels, 1},
+                                   std::span(alpha, channels), result);
+            std::memcpy(out, result.values.data(), count * sizeof(float));
+        });
+}
+
+int ref_fold_dac_weight_norm(const float* v, const float* g, std::size_t fan_in, std::size_t columns, float* out)
+{
+    return guarded(
+        [&]
+        {
+            const auto w = fold_dac_weight_norm(std::span(v, fan_in * columns), std::span(g, columns), fan_in);
+            std::memcpy(out, w.data(), w.size() * sizeof(float));
+        });
+}
+
+void ref_normalize_search(const float* input, float* output)
+{
+    weights::normalize_search(std::span<const float, 8>(input, 8), std::span<float, 8>(output, 8));
+}
+
+std::uint16_t ref_nearest_rvq(const float* input, const float* vectors)
+{
+    return nearest_rvq_index(std::span<const float, 8>(input, 8), std::span(vectors, 8192));
+}
+
+void ref_project_codebook(std::uint16_t index, const float* codebook, const float* weights, const float* bias,
+                          float* out)
+{
+    weights::project_codebook(index, std::span(codebook, 8192), std::span(weights, 8192), std::span(bias, 1024),
+                              std::span(out, 1024), true);
 }
 }

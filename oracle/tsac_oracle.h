@@ -153,6 +153,59 @@ int orc_distributions_prefix(orc_model* model, const orc_header* header, const u
                              size_t count, unsigned threads, size_t max_symbols, uint16_t* out);
 void orc_free(void* pointer);
 
+/* ---- DAC analysis/synthesis and RVQ (oracle/dac.c) --------------------------- */
+typedef struct orc_conv
+{
+    size_t in, out, kernel, stride, padding, dilation;
+    int transposed;
+} orc_conv;
+
+/* A DAC graph: 30 convolutions (prepared fp32 weights in the stored layout,
+ * fp32 bias) and 29 Snake alphas, indexed as src/models/contract.cpp numbers them. */
+typedef struct orc_dac
+{
+    int synthesis;
+    unsigned channels;
+    const float* weights[30];
+    const float* bias[30];
+    const float* alpha[29];
+} orc_dac;
+
+/* Prepared RVQ tensors per book: codebook [1024][8], normalised search vectors
+ * [1024][8], input projection [8][1024] (output-major, ordinary conv layout) +
+ * bias [8], output projection [1024][8] + bias [1024]. */
+typedef struct orc_rvq
+{
+    unsigned books;
+    const float* codebook[12];
+    const float* search[12];
+    const float* input_weights[12];
+    const float* input_bias[12];
+    const float* output_weights[12];
+    const float* output_bias[12];
+} orc_rvq;
+
+float orc_dac_sine_squared(float phase);
+int orc_snake(const float* x, size_t count, size_t channels, const float* alpha, float* out);
+int orc_fold_dac_weight_norm(const float* v, const float* g, size_t fan_in, size_t columns, float* out);
+int orc_expand_bf8(const int8_t* data, const uint16_t* scales, size_t rows, size_t cols, size_t outer, float* out);
+size_t orc_conv_output_frames(const orc_conv* c, size_t frames);
+int orc_conv1d(const orc_conv* c, const float* w, const float* bias, const float* x, size_t frames, size_t groups,
+               float* y, unsigned threads);
+int orc_dac_conv_config(int synthesis, unsigned channels, unsigned index, orc_conv* c);
+size_t orc_dac_activation_width(int synthesis, unsigned index);
+int orc_dac_apply(const orc_dac* m, const float* in, size_t frames, float* out, size_t* out_frames, unsigned threads);
+void orc_normalize_search(const float* input, float* output);
+uint16_t orc_nearest_rvq(const float* input, const float* vectors);
+void orc_project_codebook(uint16_t index, const float* codebook, const float* weights, const float* bias, float* out);
+int orc_rvq_encode(const orc_rvq* q, const float* latent, size_t frames, uint16_t* tokens);
+int orc_rvq_decode(const orc_rvq* q, const uint16_t* tokens, size_t frames, float* latent);
+int orc_analyze_audio(const orc_dac* analysis, const orc_rvq* q, const float* pcm, size_t frames, size_t groups,
+                      size_t chunk, unsigned threads, uint16_t* tokens);
+int orc_synthesize_audio(const orc_dac* synthesis, const orc_rvq* q, const uint16_t* tokens, size_t frames,
+                         size_t groups, size_t chunk, unsigned threads, float* pcm);
+int16_t orc_pcm16(float x);
+
 #ifdef __cplusplus
 }
 #endif

@@ -154,3 +154,154 @@ def pattern_tokens(count: int) -> np.ndarray:
     """The reference tests' token pattern (i*73+19) % 1024 (tests/metal_optimized.cpp:270-273)."""
     i = np.arange(count, dtype=np.int64)
     return ((i * 73 + 19) % 1024).astype(np.uint16)
+
+
+# ---------------------------------------------------------------- DAC and RVQ
+
+#: Strides of the four DAC stages (src/common/analysis.tpp, synthesis.tpp).
+ANALYSIS_STRIDES = (2, 4, 8, 8)
+SYNTHESIS_STRIDES = (8, 8, 4, 2)
+
+
+def dac_shape(synthesis: bool, channels: int, index: int) -> tuple[int, int, int]:
+    """Stored axes (axis 0 fastest) of DAC convolution `index`
+    (src/models/contract.cpp:55-84): ordinary [input, kernel, output],
+    transposed [output, kernel, input]."""
+    if index == 0:
+        return (1024, 7, 1536) if synthesis else (channels, 7, 64)
+    if index == 29:
+        return (96, 7, channels) if synthesis else (1024, 3, 1024)
+    stage, within = divmod(index - 1, 7)
+    width = (1536 >> stage) if synthesis else (64 << stage)
+    stride = (SYNTHESIS_STRIDES if synthesis else ANALYSIS_STRIDES)[stage]
+    if synthesis and within == 0:
+        return (width // 2, 2 * stride, width)
+    if not synthesis and within == 6:
+        return (width, 2 * stride, width * 2)
+    residual = within - 1 if synthesis else within
+    w = width // 2 if synthesis else width
+    return (w, 7 if residual % 2 == 0 else 1, w)
+
+
+def dac_bf8(synthesis: bool, index: int) -> bool:
+    """Whether the source stores convolution `index` as BF8 (int8 plus one
+    BF16 scale per 32 rows) rather than float32 (src/models/contract.cpp:86-92)."""
+    return not ((not synthesis and index == 0) or (synthesis and index >= 22))
+
+
+def dac_activation_width(synthesis: bool, index: int) -> int:
+    """Channels of Snake activation `index` (src/models/contract.cpp:109-116)."""
+    if index == 28:
+        return 96 if synthesis else 1024
+    return ((1536 >> (index // 7)) // (1 if index % 7 == 0 else 2)) if synthesis else (64 << (index // 7))
+
+
+@dataclasses.dataclass
+class DacConvolution:
+    """One convolution as the DAC source stores it (src/models/types.hpp:33-37):
+    `values` float32 [elements] or int8 [elements] with BF16 `scales`
+    [outer][rows/32][align8(cols)] (src/weights/preparation.cpp:31-56), the
+    weight-norm gain per stored column (last axis) and the bias per output channel."""
+    dims: tuple
+    values: np.ndarray
+    scales: np.ndarray | None
+    gain: np.ndarray
+    bias: np.ndarray
+    transposed: bool
+
+    @property
+    def bf8(self) -> bool:
+        return self.scales is not None
+
+
+@dataclasses.dataclass
+class DacModel:
+    """DAC analysis and synthesis (30 convolutions and 29 Snake alphas each) and
+    the quantizer's source tensors per codebook: codebook [1024][8], in_proj
+    v [8][1024] (column per output) / g [8] / bias [8], out_proj v [1024][8] /
+    g [1024] / bias [1024]."""
+    channels: int
+    analysis: list
+    analysis_alpha: list
+    synthesis: list
+    synthesis_alpha: list
+    codebook: list
+    in_v: list
+    in_g: list
+    in_bias: list
+    out_v: list
+    out_g: list
+    out_bias: list
+
+
+def _random_convolution(rng, synthesis, channels, index):
+    dims = dac_shape(synthesis, channels, index)
+    rows, cols, outer = dims
+    count = rows * cols * outer
+    transposed = synthesis and 1 <= index <= 28 and (index - 1) % 7 == 0
+    out_channels = rows if transposed else outer
+    if dac_bf8(synthesis, index):
+        values = rng.integers(-127, 128, size=count, dtype=np.int8)
+        padded = (cols + 7) // 8 * 8
+        scales = bf16_bits(rng.uniform(0.002, 0.02, size=(outer, rows // 32, padded)).astype(np.float32))
+    else:
+        values = rng.standard_normal(count).astype(np.float32)
+        scales = None
+    gain = rng.uniform(0.6, 1.2, size=outer).astype(np.float32)
+    bias = (0.02 * rng.standard_normal(out_channels)).astype(np.float32)
+    return DacConvolution(dims, values, scales, gain, bias, transposed)
+
+
+def random_dac(channels: int = 2, books: int = 12, seed: int = 1) -> DacModel:
+    """Seeded random-init DAC and quantizer in the source layouts. Weight norm
+    rescales every column to RMS 1/sqrt(fan_in) times its gain, so signals keep
+    a moderate scale through both graphs."""
+    rng = np.random.default_rng(seed)
+    graphs = {}
+    for synthesis in (False, True):
+        convs = [_random_convolution(rng, synthesis, channels, i) for i in range(30)]
+        alphas = [rng.uniform(0.5, 2.0, size=dac_activation_width(synthesis, i)).astype(np.float32)
+                  for i in range(29)]
+        graphs[synthesis] = (convs, alphas)
+    codebook, in_v, in_g, in_bias, out_v, out_g, out_bias = ([] for _ in range(7))
+    for _ in range(books):
+        codebook.append(rng.standard_normal((1024, 8)).astype(np.float32))
+        in_v.append(rng.standard_normal((8, 1024)).astype(np.float32))
+        in_g.append(rng.uniform(0.5, 1.5, size=8).astype(np.float32))
+        in_bias.append((0.05 * rng.standard_normal(8)).astype(np.float32))
+        out_v.append(rng.standard_normal((1024, 8)).astype(np.float32))
+        out_g.append(rng.uniform(0.05, 0.15, size=1024).astype(np.float32))
+        out_bias.append((0.01 * rng.standard_normal(1024)).astype(np.float32))
+    return DacModel(channels, graphs[False][0], graphs[False][1], graphs[True][0], graphs[True][1],
+                    codebook, in_v, in_g, in_bias, out_v, out_g, out_bias)
+
+
+def synthetic_audio(seconds: float, channels: int = 2, seed: int = 0, rate: int = 44100) -> np.ndarray:
+    """PCM16 test signal, interleaved [frames][channels]: three seeded sines per
+    channel (80-4000 Hz, random phases, -12 dBFS each) plus independent pink
+    noise at -12 dBFS (Voss-McCartney, 16 rows), scaled to int16."""
+    rng = np.random.default_rng(seed)
+    frames = int(round(seconds * rate))
+    t = np.arange(frames) / rate
+    amplitude = 10 ** (-12 / 20)
+    out = np.zeros((frames, channels), np.float64)
+    for c in range(channels):
+        for _ in range(3):
+            f = rng.uniform(80, 4000)
+            out[:, c] += amplitude * np.sin(2 * np.pi * f * t + rng.uniform(0, 2 * np.pi))
+        rows = 16
+        noise = np.zeros(frames)
+        values = rng.uniform(-1, 1, rows)
+        total = values.sum()
+        updates = rng.uniform(-1, 1, (frames, rows))
+        index = np.arange(1, frames + 1)
+        trailing = np.minimum(np.log2(index & -index).astype(np.int64), rows - 1)
+        for i in range(frames):
+            r = trailing[i]
+            total += updates[i, r] - values[r]
+            values[r] = updates[i, r]
+            noise[i] = total
+        noise /= np.max(np.abs(noise)) + 1e-12
+        out[:, c] += amplitude * noise
+    out /= max(1.0, np.max(np.abs(out)) / 0.99)
+    return np.clip(np.round(out * 32767), -32768, 32767).astype(np.int16)
