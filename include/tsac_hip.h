@@ -166,6 +166,111 @@ int tsac_hip_distributions(tsac_hip_session* session, const tsac_hip_header* hea
  * memory. */
 int tsac_hip_session_timing(const tsac_hip_session* session, double* seconds, size_t count);
 
+/* ---- the DAC codec around the model (AudioAnalyzer, include/tsac/audio_analyzer.hpp) ---- */
+
+/* ConvolutionWeights (src/models/types.hpp:33-37) as the DAC source stores a
+ * convolution: dims are the stored axes, axis 0 fastest (ordinary [in, kernel,
+ * out], transposed [out, kernel, in]); either float32 `values`, or int8
+ * `quantized` with BF16 `scales` [dims[2]][dims[0]/32][align8(dims[1])]
+ * (src/weights/preparation.cpp:31-56); the weight-norm gain per stored column
+ * [dims[2]]; the bias per output channel. */
+typedef struct tsac_hip_dac_convolution
+{
+    uint32_t dims[3];
+    const float* values;
+    const int8_t* quantized;
+    const uint16_t* scales;
+    const float* gain;
+    const float* bias;
+} tsac_hip_dac_convolution;
+
+/* One quantizer codebook as the packed RVQ roles hold it
+ * (src/weights/pack_main.cpp:244-300): codebook [1024][8], normalised search
+ * vectors [1024][8], folded input projection [8][1024] + bias [8], folded
+ * output projection [1024][8] + bias [1024]. */
+typedef struct tsac_hip_rvq_book
+{
+    const float* codebook;
+    const float* search;
+    const float* input_weights;
+    const float* input_bias;
+    const float* output_weights;
+    const float* output_bias;
+} tsac_hip_rvq_book;
+
+/* DacAnalysisModel, DacSynthesisModel (convolutions and Snake alphas numbered
+ * as src/models/contract.cpp numbers them) and RvqEncoderModel/RvqDecoderModel. */
+typedef struct tsac_hip_dac_desc
+{
+    uint32_t channels, books;
+    tsac_hip_dac_convolution analysis[30];
+    const float* analysis_alpha[29];
+    tsac_hip_dac_convolution synthesis[30];
+    const float* synthesis_alpha[29];
+    tsac_hip_rvq_book rvq[12];
+} tsac_hip_dac_desc;
+
+typedef struct tsac_hip_dac tsac_hip_dac;
+
+/* DacAnalysis / DacSynthesis / RvqEncoder / RvqDecoder ::from_model
+ * (src/common/{analysis,synthesis}.tpp, src/common/rvq.{cpp,tpp}): prepares every
+ * convolution (BF8 expansion, DAC weight-norm folding,
+ * src/common/dsp.tpp:117-155) and uploads it to the current device. The
+ * description's memory may be released after return. */
+int tsac_hip_dac_create(const tsac_hip_dac_desc* desc, const tsac_hip_limits* limits, tsac_hip_dac** dac);
+void tsac_hip_dac_destroy(tsac_hip_dac* dac);
+
+/* The packer's quantizer preparation for one codebook (src/weights/pack_main.cpp:244-300):
+ * search [1024][8] = normalize_search of each codebook row; input_weights
+ * [8][1024] and output_weights [1024][8] = DAC weight-norm folds of the source
+ * in_proj (v [8][1024], g [8]) and out_proj (v [1024][8], g [1024]). */
+int tsac_hip_prepare_rvq(const float* codebook, const float* in_v, const float* in_g, const float* out_v,
+                         const float* out_g, float* search, float* input_weights, float* output_weights);
+
+/* analyze_audio (src/common/audio_pipeline.hpp:37-58) on the GPU: padded PCM,
+ * interleaved float [frames*512][groups*dac channels], through DAC analysis and
+ * the quantizer in chunks of 400 latent frames with 8/9 context frames, to
+ * tokens [frame][group][codebook] (frames*groups*codebooks). */
+int tsac_hip_dac_analyze(tsac_hip_session* session, const tsac_hip_dac* dac, const float* pcm, size_t frames,
+                         size_t groups, uint32_t codebooks, uint16_t* tokens);
+/* synthesize_audio (src/common/audio_pipeline.hpp:60-79): tokens through the
+ * quantizer's decoder and DAC synthesis in chunks with 11 context frames, to
+ * float PCM [frames*512][groups*channels] (no rounding, as the reference). */
+int tsac_hip_dac_synthesize(tsac_hip_session* session, const tsac_hip_dac* dac, const uint16_t* tokens,
+                            size_t frames, size_t groups, uint32_t codebooks, float* pcm);
+
+/* DacAnalysis::apply / DacSynthesis::apply (src/common/analysis.hpp:31-33,
+ * src/common/synthesis.hpp:36-38) on one window without chunking, in the
+ * reference's Signal layout (channels fastest): synthesis == 0 takes PCM
+ * [frames][channels] (frames a multiple of 512) to latent [frames/512][1024];
+ * synthesis == 1 takes latent [frames][1024] to [frames*512][channels]. */
+int tsac_hip_dac_apply(tsac_hip_session* session, const tsac_hip_dac* dac, int synthesis, const float* input,
+                       size_t frames, float* output);
+
+/* EncodeOptions (include/tsac/audio_analyzer.hpp:16-22): method 0 fast,
+ * 1 normal; codebooks 0 = the model's maximum; entropy_batch 0 = automatic. */
+typedef struct tsac_hip_encode_options
+{
+    uint8_t method;
+    uint8_t codebooks;
+    uint8_t separate_channels;
+    uint16_t entropy_batch;
+} tsac_hip_encode_options;
+
+/* AudioAnalyzer::encode (include/tsac/audio_analyzer.hpp:33-34, as
+ * ScalarAnalyzer::encode composes it, src/scalar/audio_analyzer.cpp:14-38):
+ * interleaved float PCM [frames][channels] -> an FBAZ stream (library-allocated,
+ * release with tsac_hip_free); normal framing runs the session's model with
+ * `observer` (may be NULL). */
+int tsac_hip_audio_encode(tsac_hip_session* session, const tsac_hip_dac* dac, const float* samples, size_t frames,
+                          uint32_t channels, const tsac_hip_encode_options* options,
+                          const tsac_hip_observer* observer, uint8_t** stream, size_t* length);
+/* AudioAnalyzer::decode (:35-36, src/scalar/audio_analyzer.cpp:40-63): an
+ * FBAZ stream -> interleaved float PCM [frames][channels], padded to whole
+ * 512-sample frames (library-allocated, release with tsac_hip_free). */
+int tsac_hip_audio_decode(tsac_hip_session* session, const tsac_hip_dac* dac, const uint8_t* stream, size_t length,
+                          const tsac_hip_observer* observer, float** samples, size_t* frames, uint32_t* channels);
+
 /* ---- operators on device memory (hipStream_t passed as void*) -------------- */
 
 typedef struct tsac_hip_device_linear tsac_hip_device_linear;

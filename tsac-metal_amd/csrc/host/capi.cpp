@@ -1,6 +1,7 @@
 // C ABI of the probability model (include/tsac_hip.h). Exceptions stop here and
 // become a nonzero status plus a thread-local message.
 #include "../../../include/tsac_hip.h"
+#include "audio.hpp"
 #include "runtime.hpp"
 
 #include <cstdlib>
@@ -17,6 +18,11 @@ struct tsac_hip_model
 struct tsac_hip_session
 {
     std::unique_ptr<Session> session;
+};
+
+struct tsac_hip_dac
+{
+    std::unique_ptr<DacModel> dac;
 };
 
 struct tsac_hip_device_linear
@@ -257,6 +263,115 @@ int tsac_hip_decode_observed(tsac_hip_session* session, const uint8_t* stream, s
 void tsac_hip_free(void* pointer)
 {
     std::free(pointer);
+}
+
+int tsac_hip_dac_create(const tsac_hip_dac_desc* desc, const tsac_hip_limits* limits, tsac_hip_dac** dac)
+{
+    return guarded(
+        [&]
+        {
+            require(desc && dac, "missing argument");
+            static_assert(sizeof(DacConvolutionSource) == sizeof(tsac_hip_dac_convolution));
+            static_assert(sizeof(RvqSource) == sizeof(tsac_hip_rvq_book));
+            require(desc->books >= 1 && desc->books <= 12, "DAC model codebooks out of range");
+            *dac = new tsac_hip_dac{std::make_unique<DacModel>(
+                desc->channels, desc->books, reinterpret_cast<const DacConvolutionSource*>(desc->analysis),
+                desc->analysis_alpha, reinterpret_cast<const DacConvolutionSource*>(desc->synthesis),
+                desc->synthesis_alpha, reinterpret_cast<const RvqSource*>(desc->rvq), limits_of(limits))};
+        });
+}
+
+void tsac_hip_dac_destroy(tsac_hip_dac* dac)
+{
+    delete dac;
+}
+
+int tsac_hip_prepare_rvq(const float* codebook, const float* in_v, const float* in_g, const float* out_v,
+                         const float* out_g, float* search, float* input_weights, float* output_weights)
+{
+    return guarded(
+        [&]
+        {
+            require(codebook && in_v && in_g && out_v && out_g && search && input_weights && output_weights,
+                    "missing argument");
+            prepare_rvq(codebook, in_v, in_g, out_v, out_g, search, input_weights, output_weights);
+        });
+}
+
+int tsac_hip_dac_analyze(tsac_hip_session* session, const tsac_hip_dac* dac, const float* pcm, size_t frames,
+                         size_t groups, uint32_t codebooks, uint16_t* tokens)
+{
+    return guarded(
+        [&]
+        {
+            require(session && dac && (pcm || !frames) && (tokens || !frames), "missing argument");
+            session->session->analyze(*dac->dac, pcm, frames, groups, codebooks, tokens);
+        });
+}
+
+int tsac_hip_dac_synthesize(tsac_hip_session* session, const tsac_hip_dac* dac, const uint16_t* tokens,
+                            size_t frames, size_t groups, uint32_t codebooks, float* pcm)
+{
+    return guarded(
+        [&]
+        {
+            require(session && dac && (pcm || !frames) && (tokens || !frames), "missing argument");
+            session->session->synthesize(*dac->dac, tokens, frames, groups, codebooks, pcm);
+        });
+}
+
+int tsac_hip_dac_apply(tsac_hip_session* session, const tsac_hip_dac* dac, int synthesis, const float* input,
+                       size_t frames, float* output)
+{
+    return guarded(
+        [&]
+        {
+            require(session && dac && input && output, "missing argument");
+            session->session->dac_apply(*dac->dac, synthesis != 0, input, frames, output);
+        });
+}
+
+int tsac_hip_audio_encode(tsac_hip_session* session, const tsac_hip_dac* dac, const float* samples, size_t frames,
+                          uint32_t channels, const tsac_hip_encode_options* options,
+                          const tsac_hip_observer* observer, uint8_t** stream, size_t* length)
+{
+    return guarded(
+        [&]
+        {
+            require(session && dac && (samples || !frames) && stream && length, "missing argument");
+            EncodeOptions o;
+            if (options)
+            {
+                o.method = options->method;
+                o.codebooks = options->codebooks;
+                o.separate_channels = options->separate_channels != 0;
+                if (options->entropy_batch)
+                {
+                    o.entropy_batch = options->entropy_batch;
+                }
+            }
+            const SymbolObserver obs = observer_of(observer);
+            const auto bytes =
+                session->session->encode_audio(*dac->dac, samples, frames, channels, o, observer ? &obs : nullptr);
+            *stream = copy_out(bytes);
+            *length = bytes.size();
+        });
+}
+
+int tsac_hip_audio_decode(tsac_hip_session* session, const tsac_hip_dac* dac, const uint8_t* stream, size_t length,
+                          const tsac_hip_observer* observer, float** samples, size_t* frames, uint32_t* channels)
+{
+    return guarded(
+        [&]
+        {
+            require(session && dac && stream && samples && frames && channels, "missing argument");
+            const SymbolObserver obs = observer_of(observer);
+            std::size_t c = 0;
+            const auto pcm = session->session->decode_audio(*dac->dac, stream, length, observer ? &obs : nullptr, &c);
+            *samples = copy_out(pcm);
+            *channels = uint32_t(c);
+            *frames = c ? pcm.size() / c : 0;
+        });
 }
 
 int tsac_hip_distributions(tsac_hip_session* session, const tsac_hip_header* header,

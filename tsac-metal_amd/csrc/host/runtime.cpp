@@ -13,11 +13,6 @@ constexpr std::size_t replay_frames = 256;
 // rows * (3*width + ffn) * 2 bytes.
 constexpr std::size_t batch_rows = 65536;
 
-double now()
-{
-    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
-}
-
 std::size_t align_up(std::size_t n, std::size_t a)
 {
     return (n + a - 1) / a * a;

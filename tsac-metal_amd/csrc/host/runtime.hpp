@@ -3,11 +3,13 @@
 
 #include "../kernels/attention.hpp"
 #include "../kernels/codec.hpp"
+#include "../kernels/dac.hpp"
 #include "../kernels/frame.hpp"
 #include "../kernels/kernels.hpp"
 #include "format.hpp"
 
 #include <array>
+#include <chrono>
 #include <map>
 #include <memory>
 #include <string>
@@ -15,6 +17,15 @@
 
 namespace tsac_hip
 {
+class DacModel;
+struct EncodeOptions;
+
+// Monotonic wall clock, seconds.
+inline double now()
+{
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
 struct Geometry
 {
     uint32_t width = 512, heads = 4, head_width = 128, ffn = 2048;
@@ -188,6 +199,27 @@ public:
                                 const SymbolObserver* observer = nullptr);
     std::vector<uint16_t> decode(const uint8_t* stream, std::size_t length,
                                  const SymbolObserver* observer = nullptr);
+    // The DAC side (audio.cpp). analyze: padded PCM interleaved
+    // [frames*512][groups*channels] -> tokens [frame][group][book]
+    // (analyze_audio, src/common/audio_pipeline.hpp:37-58); synthesize: the
+    // inverse (synthesize_audio, :60-79), float PCM without rounding.
+    void analyze(const DacModel& dac, const float* pcm, std::size_t frames, std::size_t groups, unsigned books,
+                 uint16_t* tokens);
+    void synthesize(const DacModel& dac, const uint16_t* tokens, std::size_t frames, std::size_t groups,
+                    unsigned books, float* pcm);
+    // DacAnalysis::apply / DacSynthesis::apply on one window, reference Signal
+    // layout [frame][channel]: analysis PCM of `frames` samples (a multiple of
+    // 512) -> latent [frames/512][1024]; synthesis latent [frames][1024] ->
+    // [frames*512][channels].
+    void dac_apply(const DacModel& dac, bool synthesis, const float* input, std::size_t frames, float* output);
+    // AudioAnalyzer::encode / decode (include/tsac/audio_analyzer.hpp:31-36):
+    // interleaved float PCM of `count` frames <-> an FBAZ stream, fast or normal
+    // framing; decoded PCM keeps the padding to whole frames.
+    std::vector<uint8_t> encode_audio(const DacModel& dac, const float* samples, std::size_t count,
+                                      std::size_t channels, const EncodeOptions& options,
+                                      const SymbolObserver* observer = nullptr);
+    std::vector<float> decode_audio(const DacModel& dac, const uint8_t* stream, std::size_t length,
+                                    const SymbolObserver* observer, std::size_t* channels);
     // Teacher-forced distributions [count][alphabet]; decode_pass selects the
     // stepwise (GEMV) driver instead of the batched (GEMM) one.
     void distributions(Header header, const uint16_t* tokens, std::size_t count, bool decode_pass,
@@ -205,6 +237,10 @@ public:
 private:
     struct Stepwise;
     void check_errors();
+    void check_dsp_errors();
+    void analysis_graph(const DacModel& dac, Strided input, int samples, Strided output, float* const* slots);
+    void synthesis_graph(const DacModel& dac, Strided input, int frames, Strided output, int first, int last,
+                         float* const* slots);
     void reset_errors();
     // Copies the call's input to the device between two events; input_seconds()
     // (after the stream has drained) is that copy's duration.

@@ -32,7 +32,9 @@ EXPORTS = (
     "tsac_hip_layer_norm", "tsac_hip_softmax", "tsac_hip_gelu", "tsac_hip_rotary", "tsac_hip_add",
     "tsac_hip_attention", "tsac_hip_attention_causal", "tsac_hip_bf8l_tiles", "tsac_hip_tile_rows",
     "tsac_hip_probe_read", "tsac_hip_probe_mfma", "tsac_hip_encode_observed", "tsac_hip_decode_observed",
-    "tsac_hip_linear_apply_static",
+    "tsac_hip_linear_apply_static", "tsac_hip_dac_create", "tsac_hip_dac_destroy", "tsac_hip_prepare_rvq",
+    "tsac_hip_dac_analyze", "tsac_hip_dac_synthesize", "tsac_hip_audio_encode", "tsac_hip_audio_decode",
+    "tsac_hip_dac_apply",
 )
 
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_TILES = 0, 1, 2, 3
@@ -81,6 +83,27 @@ class Observer(C.Structure):
     _fields_ = [("context", vp), ("before_symbol", BEFORE_SYMBOL), ("after_symbol", AFTER_SYMBOL)]
 
 
+class DacConvolution(C.Structure):
+    _fields_ = [("dims", C.c_uint32 * 3), ("values", f32p), ("quantized", i8p), ("scales", u16p), ("gain", f32p),
+                ("bias", f32p)]
+
+
+class RvqBook(C.Structure):
+    _fields_ = [(n, f32p) for n in ("codebook", "search", "input_weights", "input_bias", "output_weights",
+                                    "output_bias")]
+
+
+class DacDesc(C.Structure):
+    _fields_ = [("channels", C.c_uint32), ("books", C.c_uint32), ("analysis", DacConvolution * 30),
+                ("analysis_alpha", f32p * 29), ("synthesis", DacConvolution * 30), ("synthesis_alpha", f32p * 29),
+                ("rvq", RvqBook * 12)]
+
+
+class EncodeOptions(C.Structure):
+    _fields_ = [("method", C.c_uint8), ("codebooks", C.c_uint8), ("separate_channels", C.c_uint8),
+                ("entropy_batch", C.c_uint16)]
+
+
 def header(frames, batch, groups, codebooks, model_channels=2, method=1) -> Header:
     return Header(method, groups, model_channels, codebooks, frames, batch)
 
@@ -105,6 +128,16 @@ def library() -> C.CDLL:
         lib.tsac_hip_encode.argtypes = [vp, C.POINTER(Header), u16p, sz, C.POINTER(u8p), C.POINTER(sz)]
         lib.tsac_hip_decode.argtypes = [vp, u8p, sz, C.POINTER(u16p), C.POINTER(sz)]
         lib.tsac_hip_free.argtypes = [vp]
+        lib.tsac_hip_dac_create.argtypes = [C.POINTER(DacDesc), C.POINTER(Limits), C.POINTER(vp)]
+        lib.tsac_hip_dac_destroy.argtypes = [vp]
+        lib.tsac_hip_prepare_rvq.argtypes = [f32p] * 8
+        lib.tsac_hip_dac_analyze.argtypes = [vp, vp, f32p, sz, sz, C.c_uint32, u16p]
+        lib.tsac_hip_dac_synthesize.argtypes = [vp, vp, u16p, sz, sz, C.c_uint32, f32p]
+        lib.tsac_hip_dac_apply.argtypes = [vp, vp, C.c_int, f32p, sz, f32p]
+        lib.tsac_hip_audio_encode.argtypes = [vp, vp, f32p, sz, C.c_uint32, C.POINTER(EncodeOptions),
+                                              C.POINTER(Observer), C.POINTER(u8p), C.POINTER(sz)]
+        lib.tsac_hip_audio_decode.argtypes = [vp, vp, u8p, sz, C.POINTER(Observer), C.POINTER(f32p), C.POINTER(sz),
+                                              C.POINTER(C.c_uint32)]
         lib.tsac_hip_encode_observed.argtypes = [vp, C.POINTER(Header), u16p, sz, C.POINTER(Observer),
                                                  C.POINTER(u8p), C.POINTER(sz)]
         lib.tsac_hip_decode_observed.argtypes = [vp, u8p, sz, C.POINTER(Observer), C.POINTER(u16p),
@@ -295,6 +328,125 @@ class HipSession:
         check(library().tsac_hip_session_timing(self.handle, t, 6))
         return {"model": t[0], "range_coding": t[1], "total": t[2], "input_upload": t[3], "steps_gpu": t[4],
                 "steps": int(t[5])}
+
+
+def prepare_rvq(codebook, in_v, in_g, out_v, out_g):
+    """The packer's quantizer preparation (tsac_hip_prepare_rvq): (search,
+    input_weights, output_weights) for one codebook."""
+    a = [np.ascontiguousarray(x, np.float32) for x in (codebook, in_v, in_g, out_v, out_g)]
+    out = [np.zeros(8192, np.float32) for _ in range(3)]
+    check(library().tsac_hip_prepare_rvq(*[_ptr(x, C.c_float) for x in a + out]))
+    return out
+
+
+class HipDac:
+    """The DAC codec's device model (tsac_hip_dac_create) from a
+    tsac_hip.synthetic.DacModel: convolutions in their source encoding, Snake
+    alphas, and the quantizer prepared as the packer prepares it."""
+
+    def __init__(self, model, limits: Limits | None = None):
+        self.channels, self.books = model.channels, len(model.codebook)
+        desc = DacDesc()
+        desc.channels, desc.books = model.channels, self.books
+        keep = []
+        for name, convs, alphas in (("analysis", model.analysis, model.analysis_alpha),
+                                    ("synthesis", model.synthesis, model.synthesis_alpha)):
+            for i, conv in enumerate(convs):
+                d = getattr(desc, name)[i]
+                d.dims = (C.c_uint32 * 3)(*conv.dims)
+                gain, bias = np.ascontiguousarray(conv.gain, np.float32), np.ascontiguousarray(conv.bias, np.float32)
+                keep += [gain, bias]
+                d.gain, d.bias = _ptr(gain, C.c_float), _ptr(bias, C.c_float)
+                if conv.bf8:
+                    q, sc = np.ascontiguousarray(conv.values, np.int8), np.ascontiguousarray(conv.scales, np.uint16)
+                    keep += [q, sc]
+                    d.quantized, d.scales = _ptr(q, C.c_int8), _ptr(sc, C.c_uint16)
+                else:
+                    v = np.ascontiguousarray(conv.values, np.float32)
+                    keep.append(v)
+                    d.values = _ptr(v, C.c_float)
+            for i, a in enumerate(alphas):
+                a = np.ascontiguousarray(a, np.float32)
+                keep.append(a)
+                getattr(desc, name + "_alpha")[i] = _ptr(a, C.c_float)
+        for b in range(self.books):
+            search, input_weights, output_weights = prepare_rvq(model.codebook[b], model.in_v[b], model.in_g[b],
+                                                                model.out_v[b], model.out_g[b])
+            parts = [np.ascontiguousarray(model.codebook[b], np.float32), search, input_weights,
+                     np.ascontiguousarray(model.in_bias[b], np.float32), output_weights,
+                     np.ascontiguousarray(model.out_bias[b], np.float32)]
+            keep += parts
+            desc.rvq[b] = RvqBook(*[_ptr(x, C.c_float) for x in parts])
+        handle = vp()
+        check(library().tsac_hip_dac_create(C.byref(desc), C.byref(limits) if limits else None, C.byref(handle)))
+        self.handle, self._library = handle, library()
+        del keep
+
+    def __del__(self):
+        _release(self, "tsac_hip_dac_destroy")
+
+    def close(self):
+        _release(self, "tsac_hip_dac_destroy")
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def analyze(self, session: "HipSession", pcm, frames, groups=1, codebooks=None) -> np.ndarray:
+        """Padded interleaved PCM [frames*512][groups*channels] -> tokens [frame][group][book]."""
+        books = codebooks or self.books
+        pcm = np.ascontiguousarray(pcm, np.float32)
+        tokens = np.zeros(frames * groups * books, np.uint16)
+        check(library().tsac_hip_dac_analyze(session.handle, self.handle, _ptr(pcm, C.c_float), frames, groups, books,
+                                             _ptr(tokens, C.c_uint16)))
+        return tokens
+
+    def apply(self, session: "HipSession", synthesis: bool, x, frames) -> np.ndarray:
+        """DacAnalysis/DacSynthesis::apply on one window (reference Signal layout)."""
+        x = np.ascontiguousarray(x, np.float32)
+        count = frames * 512 * self.channels if synthesis else frames // 512 * 1024
+        out = np.zeros(count, np.float32)
+        check(library().tsac_hip_dac_apply(session.handle, self.handle, int(synthesis), _ptr(x, C.c_float), frames,
+                                           _ptr(out, C.c_float)))
+        return out
+
+    def synthesize(self, session: "HipSession", tokens, frames, groups=1, codebooks=None) -> np.ndarray:
+        books = codebooks or self.books
+        tokens = np.ascontiguousarray(tokens, np.uint16)
+        pcm = np.zeros(frames * 512 * groups * self.channels, np.float32)
+        check(library().tsac_hip_dac_synthesize(session.handle, self.handle, _ptr(tokens, C.c_uint16), frames,
+                                                groups, books, _ptr(pcm, C.c_float)))
+        return pcm
+
+    def encode(self, session: "HipSession", samples, channels, method=1, codebooks=0, separate_channels=False,
+               entropy_batch=0, before=None, after=None) -> bytes:
+        """AudioAnalyzer::encode of interleaved float PCM [frames][channels]."""
+        samples = np.ascontiguousarray(samples, np.float32)
+        options = EncodeOptions(method, codebooks, int(separate_channels), entropy_batch)
+        observer, keep = HipSession._observer(before, after)
+        out, n = u8p(), sz()
+        check(library().tsac_hip_audio_encode(session.handle, self.handle, _ptr(samples, C.c_float),
+                                              samples.size // channels, channels, C.byref(options), C.byref(observer),
+                                              C.byref(out), C.byref(n)))
+        data = C.string_at(out, n.value)
+        library().tsac_hip_free(out)
+        del keep
+        return data
+
+    def decode(self, session: "HipSession", data: bytes, before=None, after=None):
+        """AudioAnalyzer::decode: (interleaved float PCM [frames][channels], channels)."""
+        b = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+        observer, keep = HipSession._observer(before, after)
+        out, frames, channels = f32p(), sz(), C.c_uint32()
+        check(library().tsac_hip_audio_decode(session.handle, self.handle, _ptr(b, C.c_uint8), len(data),
+                                              C.byref(observer), C.byref(out), C.byref(frames), C.byref(channels)))
+        count = frames.value * channels.value
+        pcm = np.ctypeslib.as_array(out, shape=(count,)).copy() if count else np.zeros(0, np.float32)
+        library().tsac_hip_free(out)
+        del keep
+        return pcm.reshape(frames.value, channels.value), channels.value
 
 
 # ---------------------------------------------------------------- operators on torch tensors

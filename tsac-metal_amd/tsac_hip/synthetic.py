@@ -260,6 +260,10 @@ def random_dac(channels: int = 2, books: int = 12, seed: int = 1) -> DacModel:
     graphs = {}
     for synthesis in (False, True):
         convs = [_random_convolution(rng, synthesis, channels, i) for i in range(30)]
+        if synthesis:
+            # Random residual stacks grow the signal about a hundredfold; a small
+            # exit gain brings the PCM back to roughly full scale.
+            convs[29].gain *= np.float32(0.005)
         alphas = [rng.uniform(0.5, 2.0, size=dac_activation_width(synthesis, i)).astype(np.float32)
                   for i in range(29)]
         graphs[synthesis] = (convs, alphas)
