@@ -69,7 +69,8 @@ def parse():
     p.add_argument("--frames", type=int, default=2580)
     p.add_argument("--batch", type=int, default=3)
     p.add_argument("--geometry", choices=["reference", "wide"], default="reference")
-    p.add_argument("--only", choices=["all", "model", "gemv", "gemm", "attention", "qlinear", "wide"], default="all")
+    p.add_argument("--only", choices=["all", "model", "gemv", "gemm", "attention", "qlinear", "wide", "audio"],
+                   default="all")
     p.add_argument("--gemv-launches", type=int, default=64)
     p.add_argument("--cpu-frames", type=int, default=1290, help="CPU baseline sample (frames)")
     p.add_argument("--no-cpu", action="store_true")
@@ -418,6 +419,84 @@ def wide_geometry(native, frames=2580, batch=3, steps=2):
                          "ffn": WIDE.ffn, "layers": [WIDE.temporal_layers, WIDE.codebook_layers]}}
 
 
+def end_to_end(native, seconds, codebooks, batch, seed, steps=2):
+    """AudioAnalyzer encode + decode of synthetic joint-stereo PCM on the GPU
+    (DAC analysis, RVQ, probability model + range coding; then the model with
+    the GPU range decoder, RVQ decoding, DAC synthesis), random-init DAC and
+    reference-geometry transformer weights. Host wall clock around each call
+    (PCM in and out of host memory included); the DAC-only passes are also timed
+    alone to split the cost."""
+    from tsac_hip.synthetic import REFERENCE, random_dac, random_model, synthetic_audio
+
+    audio = synthetic_audio(seconds, 2, seed).astype(np.float32) / np.float32(32768)
+    frames = -(-len(audio) // 512)
+    padded = np.zeros((frames * 512, 2), np.float32)
+    padded[:len(audio)] = audio
+    with native.HipModel(random_model(REFERENCE, seed=1)) as hip_model, hip_model.session() as session, \
+            native.HipDac(random_dac(2, 12, seed=1)) as dac:
+        stream = dac.encode(session, audio, 2, codebooks=codebooks, entropy_batch=batch)
+        pcm, _ = dac.decode(session, stream)
+        encode_s = decode_s = 0.0
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            stream = dac.encode(session, audio, 2, codebooks=codebooks, entropy_batch=batch)
+            t1 = time.perf_counter()
+            pcm, channels = dac.decode(session, stream)
+            t2 = time.perf_counter()
+            encode_s += t1 - t0
+            decode_s += t2 - t1
+        assert channels == 2 and pcm.shape == (frames * 512, 2) and np.all(np.isfinite(pcm))
+        t0 = time.perf_counter()
+        tokens = dac.analyze(session, padded, frames, 1, codebooks)
+        t1 = time.perf_counter()
+        dac.synthesize(session, tokens, frames, 1, codebooks)
+        t2 = time.perf_counter()
+    encode_s /= steps
+    decode_s /= steps
+    return {"seconds_of_audio": seconds, "frames": frames, "codebooks": codebooks, "batch": batch,
+            "encode_s": round(encode_s, 4), "decode_s": round(decode_s, 4),
+            "round_trip_s": round(encode_s + decode_s, 4),
+            "realtime_factor": round(seconds / (encode_s + decode_s), 1),
+            "dac_analysis_rvq_s": round(t1 - t0, 4), "rvq_dac_synthesis_s": round(t2 - t1, 4),
+            "stream_bytes": len(stream),
+            "timing": "host wall clock around tsac_hip_audio_encode / tsac_hip_audio_decode, PCM in host memory"}
+
+
+def cpu_end_to_end(seconds, codebooks, batch, seed):
+    """The oracle's whole CPU chain (DAC analysis, RVQ, pack_normal; then
+    unpack_normal, RVQ decoding, DAC synthesis) on `seconds` of the same
+    synthetic audio, convolutions split over the host's cores, the model's
+    lanes over at most `batch` threads."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    from oracle import Oracle, header
+    from tsac_hip.synthetic import REFERENCE, random_dac, random_model, synthetic_audio
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    audio = synthetic_audio(seconds, 2, seed).astype(np.float32) / np.float32(32768)
+    frames = -(-len(audio) // 512)
+    padded = np.zeros((frames * 512, 2), np.float32)
+    padded[:len(audio)] = audio
+    o = Oracle()
+    dm = o.dac_model(random_dac(2, 12, seed=1))
+    om = o.model(random_model(REFERENCE, seed=1))
+    threads = min(cores, batch)
+    t0 = time.perf_counter()
+    tokens = dm.analyze_audio(padded, frames, 1, threads=cores)
+    t1 = time.perf_counter()
+    h = header(frames, batch, 1, codebooks)
+    selected = tokens.reshape(frames, 12)[:, :codebooks].copy()
+    stream = om.pack_normal(h, selected, threads=threads)
+    t2 = time.perf_counter()
+    decoded = om.unpack_normal(stream, threads=threads)
+    t3 = time.perf_counter()
+    dm.synthesize_audio(tokens, frames, 1, threads=cores)
+    t4 = time.perf_counter()
+    assert np.array_equal(decoded, selected.ravel())
+    return {"seconds": round(t4 - t0, 3), "analysis_s": round(t1 - t0, 3), "pack_normal_s": round(t2 - t1, 3),
+            "unpack_normal_s": round(t3 - t2, 3), "synthesis_s": round(t4 - t3, 3), "cores": cores,
+            "sample": f"{seconds} s of joint stereo ({frames} frames), {codebooks} codebooks, batch {batch}"}
+
+
 def cpu_baseline(model, frames, batch):
     """The C oracle on a bounded sample of the same workload: a pack_normal +
     unpack_normal round trip of `frames` frames (same geometry, batch, books),
@@ -535,6 +614,18 @@ def main():
         result["wide_geometry"] = wide_geometry(native)
     if args.only in ("all", "qlinear"):
         result["qlinear"] = qlinear_table(torch, native)
+    if args.only in ("all", "audio"):
+        # BASELINE configs 4 (30 s joint stereo, 12 codebooks, batch 3) and 0
+        # (10 s, 3 codebooks, automatic batch) end to end; the CPU chain on a
+        # bounded sample, scaled to the same audio length.
+        audio = {"config4": end_to_end(native, 30.0, 12, 3, seed=4), "config0": end_to_end(native, 10.0, 3, 0, seed=3)}
+        if not args.no_cpu:
+            cpu = cpu_end_to_end(1.0, 12, 3, seed=4)
+            cpu["scaled_to_30s_s"] = round(cpu["seconds"] * 30.0, 1)
+            cpu["kind"] = "port"
+            audio["cpu_baseline"] = cpu
+            audio["config4_speedup_vs_cpu"] = round(cpu["scaled_to_30s_s"] / audio["config4"]["round_trip_s"], 1)
+        result["end_to_end"] = audio
     if args.only == "all":
         if not args.no_cpu:
             result["cpu_baseline"] = cpu_baseline(random_model(geometry, seed=1), args.cpu_frames,

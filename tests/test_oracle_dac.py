@@ -132,3 +132,23 @@ def test_dac_graphs_run_end_to_end(oracle):
     assert np.all(np.isfinite(decoded))
     audio = dm.apply(True, decoded[:1024], 1)
     assert audio.shape == (512 * 2,) and np.all(np.isfinite(audio))
+
+
+def test_library_prepare_rvq_matches_oracle_and_reference(oracle, reference):
+    """tsac_hip_prepare_rvq (host code of the library, no device needed) gives the
+    oracle's and the compiled reference's search vectors and folded projections."""
+    from tsac_hip import native
+
+    rng = np.random.default_rng(21)
+    codebook = rng.standard_normal((1024, 8)).astype(np.float32)
+    in_v = rng.standard_normal(8 * 1024).astype(np.float32)
+    in_g = rng.uniform(0.1, 2.0, 8).astype(np.float32)
+    out_v = rng.standard_normal(1024 * 8).astype(np.float32)
+    out_g = rng.uniform(0.1, 2.0, 1024).astype(np.float32)
+    search, input_weights, output_weights = native.prepare_rvq(codebook, in_v, in_g, out_v, out_g)
+    expected_search = np.stack([reference.normalize_search(row) for row in codebook]).ravel()
+    assert np.array_equal(search.view(np.uint32), expected_search.view(np.uint32))
+    assert np.array_equal(search, np.stack([oracle.normalize_search(row) for row in codebook]).ravel())
+    for got, v, g, fan_in in ((input_weights, in_v, in_g, 1024), (output_weights, out_v, out_g, 8)):
+        assert np.array_equal(got.view(np.uint32), reference.fold_dac_weight_norm(v, g, fan_in).view(np.uint32))
+        assert np.array_equal(got.view(np.uint32), oracle.fold_dac_weight_norm(v, g, fan_in).view(np.uint32))
