@@ -41,16 +41,60 @@ struct Exchange
     unsigned* abort;
 };
 
-__device__ __forceinline__ void publish(word* w, std::size_t index, uint32_t payload, uint32_t epoch)
-{
-    __hip_atomic_store(w + index, (word(epoch) << 32) | payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Global-address views: job arguments reach the jobs through memory, so their
-// pointers are generic; these keep the loads global (not flat).
+// pointers are generic; these keep the accesses global, not flat. A flat access
+// counts against both the vector-memory and the LDS counters, so every later
+// wait for the wave's LDS accesses would also wait for it (for a store, until
+// memory acknowledges it).
 template <class T> __device__ __forceinline__ const __attribute__((address_space(1))) T* global(const T* p)
 {
     return (const __attribute__((address_space(1))) T*)(p);
+}
+template <class T> __device__ __forceinline__ __attribute__((address_space(1))) T* global_out(T* p)
+{
+    return (__attribute__((address_space(1))) T*)(p);
+}
+
+__device__ __forceinline__ void publish(word* w, std::size_t index, uint32_t payload, uint32_t epoch)
+{
+    __hip_atomic_store(global_out(w + index), (word(epoch) << 32) | payload, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// V consecutive BF16 values of a row in global memory (p aligned to V values).
+template <int V> __device__ __forceinline__ void load_global_row(const uint16_t* p, uint16_t (&v)[V])
+{
+    if constexpr (V == 1)
+    {
+        v[0] = *global(p);
+    }
+    else if constexpr (V == 2)
+    {
+        const uint32_t u = *global(reinterpret_cast<const uint32_t*>(p));
+        v[0] = uint16_t(u & 0xffff), v[1] = uint16_t(u >> 16);
+    }
+    else
+    {
+        static_assert(V % 4 == 0, "1, 2 or a multiple of 4 values");
+#pragma unroll
+        for (int c = 0; c < V / 4; ++c)
+        {
+            const unsigned long long u = *global(reinterpret_cast<const unsigned long long*>(p) + c);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                v[4 * c + i] = uint16_t(u >> (16 * i));
+            }
+        }
+    }
+}
+
+// The workgroup's LDS block as a pointer the compiler knows to be in LDS (job
+// functions receive it as a generic pointer), so that the accesses through it
+// are LDS instructions rather than flat ones.
+__device__ __forceinline__ uint8_t* in_lds(uint8_t* p)
+{
+    return (uint8_t*)((__attribute__((address_space(3))) uint8_t*)(p));
 }
 
 // Job functions stay out of line (each is one body in the instruction cache)
@@ -174,13 +218,13 @@ __device__ __forceinline__ bool keep_polling(unsigned& spins, const Exchange& x)
 {
     if (++spins % 64 == 0)
     {
-        if (__hip_atomic_load(x.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+        if (__hip_atomic_load(global_out(x.abort), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
         {
             return false;
         }
         if (spins > spin_limit)
         {
-            __hip_atomic_store(x.abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(global_out(x.abort), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return false;
         }
     }
@@ -734,6 +778,7 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
                                           int book_lane = 0)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
+    lds = in_lds(lds);
     Projection p;
     p.w.values = uniform(job->w.values);
     p.w.scales = uniform(job->w.scales);
@@ -812,6 +857,12 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
     const int n0 = tile * tile_rows + 2 * pair;
     const float2 bias = load_float2(p.w.bias + n0);
     const float bias0 = bias.x, bias1 = bias.y;
+    // A fixed residual row (the codebook position row) is known before any wait.
+    uint32_t fixed_residual = 0;
+    if constexpr (O == Out::residual_row)
+    {
+        fixed_residual = *global(reinterpret_cast<const uint32_t*>(p.residual_row + n0));
+    }
     float ws0[blocks], ws1[blocks];
 #pragma unroll
     for (int b = 0; b < blocks; ++b)
@@ -835,8 +886,8 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
     uint16_t norm_gain[V], norm_bias[V], spread_gain[Vw > 0 ? Vw : 1], spread_bias[Vw > 0 ? Vw : 1];
     if constexpr (I == In::words_norm && spread)
     {
-        load_row<Vw>(p.gain + (warp * wave + lane) * Vw, spread_gain);
-        load_row<Vw>(p.beta + (warp * wave + lane) * Vw, spread_bias);
+        load_global_row<Vw>(p.gain + (warp * wave + lane) * Vw, spread_gain);
+        load_global_row<Vw>(p.beta + (warp * wave + lane) * Vw, spread_bias);
     }
     else if constexpr (I == In::words_norm)
     {
@@ -906,13 +957,13 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
             {
                 // src/common/cpu_transformer.tpp:205-224: copy book 0, add later books in order.
                 const uint16_t* t = p.tokens + std::size_t(warp) * p.token_stride;
-                const int t0 = min(int(t[0]), p.alphabet - 1);
-                load_row<V>(p.embeddings + std::size_t(t0) * K + lane * V, v);
+                const int t0 = min(int(*global(t)), p.alphabet - 1);
+                load_global_row<V>(p.embeddings + std::size_t(t0) * K + lane * V, v);
                 for (int b = 1; b < p.books; ++b)
                 {
-                    const int tb = min(int(t[b]), p.alphabet - 1);
+                    const int tb = min(int(*global(t + b)), p.alphabet - 1);
                     uint16_t e[V];
-                    load_row<V>(p.embeddings + (std::size_t(b) * p.alphabet + tb) * K + lane * V, e);
+                    load_global_row<V>(p.embeddings + (std::size_t(b) * p.alphabet + tb) * K + lane * V, e);
 #pragma unroll
                     for (int i = 0; i < V; ++i)
                     {
@@ -923,7 +974,7 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
             else
             {
                 const int token = min(int(take(p.token_words, warp, x) & 0xffffu), p.alphabet - 1);
-                load_row<V>(p.embeddings + (std::size_t(p.book) * p.alphabet + token) * K + lane * V, v);
+                load_global_row<V>(p.embeddings + (std::size_t(p.book) * p.alphabet + token) * K + lane * V, v);
                 if (p.prefix_in)
                 {
                     uint16_t prev[V];
@@ -969,18 +1020,26 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
             const int slot = b * waves_per_block + (rounds > 1 ? 0 : warp % waves_per_block);
             for (int m = m0; m < m1; ++m)
             {
+                // Four independent accumulators: the block dot is an exact
+                // integer (|dot| < 2^24), so their order does not matter,
+                // and the chain is a quarter as long.
                 const uint4* xq = reinterpret_cast<const uint4*>(q + m * K + b * 256 + first_segment * 16);
-                int dot = 0;
+                uint4 u[wave_segments];
 #pragma unroll
                 for (int s = 0; s < wave_segments; ++s)
                 {
-                    const uint4 u = xq[s];
-                    dot = __builtin_amdgcn_sdot4(int(w[s].x), int(u.x), dot, false);
-                    dot = __builtin_amdgcn_sdot4(int(w[s].y), int(u.y), dot, false);
-                    dot = __builtin_amdgcn_sdot4(int(w[s].z), int(u.z), dot, false);
-                    dot = __builtin_amdgcn_sdot4(int(w[s].w), int(u.w), dot, false);
+                    u[s] = xq[s];
                 }
-                dots[(slot * max_lanes + m) * tile_rows + lane] = dot;
+                int part[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int s = 0; s < wave_segments; ++s)
+                {
+                    part[0] = __builtin_amdgcn_sdot4(int(w[s].x), int(u[s].x), part[0], false);
+                    part[1] = __builtin_amdgcn_sdot4(int(w[s].y), int(u[s].y), part[1], false);
+                    part[2] = __builtin_amdgcn_sdot4(int(w[s].z), int(u[s].z), part[2], false);
+                    part[3] = __builtin_amdgcn_sdot4(int(w[s].w), int(u[s].w), part[3], false);
+                }
+                dots[(slot * max_lanes + m) * tile_rows + lane] = (part[0] + part[1]) + (part[2] + part[3]);
             }
         }
         lds_barrier();
@@ -1019,8 +1078,8 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
         }
         else if constexpr (O == Out::residual_row)
         {
-            y0 = float_to_bf16(bf16_to_float(p.residual_row[n0]) + bf16_to_float(y0));
-            y1 = float_to_bf16(bf16_to_float(p.residual_row[n0 + 1]) + bf16_to_float(y1));
+            y0 = float_to_bf16(bf16_to_float(uint16_t(fixed_residual & 0xffff)) + bf16_to_float(y0));
+            y1 = float_to_bf16(bf16_to_float(uint16_t(fixed_residual >> 16)) + bf16_to_float(y1));
         }
         else if constexpr (O == Out::gelu)
         {
@@ -1043,8 +1102,8 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
             if (p.keys && n0 >= width)
             {
                 uint16_t* cache = n0 < 2 * width ? p.keys + (n0 - width) : p.values + (n0 - 2 * width);
-                *reinterpret_cast<uint32_t*>(cache + std::size_t(m) * p.lane_stride + std::size_t(p.position) * width) =
-                    y0 | (uint32_t(y1) << 16);
+                *global_out(reinterpret_cast<uint32_t*>(cache + std::size_t(m) * p.lane_stride +
+                                                        std::size_t(p.position) * width)) = y0 | (uint32_t(y1) << 16);
             }
         }
         publish(p.y, out_word, y0 | (uint32_t(y1) << 16), x.epoch);
@@ -1102,6 +1161,7 @@ template <int HW>
 __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys, int item, Exchange exchange, uint8_t* lds)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
+    lds = in_lds(lds);
     Attend a;
     a.heads = uniform(job->heads);
     a.width = uniform(job->width);
@@ -1526,11 +1586,14 @@ __device__ __noinline__ JOB void condition_rows(const word* in, const uint16_t* 
     {
         return;
     }
+    // Constants first: the input is the last thing to arrive.
+    uint16_t g[V], b[V], p[V];
+    load_global_row<V>(gain + lane * V, g);
+    load_global_row<V>(bias + lane * V, b);
+    load_global_row<V>(add_row + lane * V, p);
     uint16_t v[V];
     take_row<V>(in, std::size_t(row) * width + lane * V, x, v);
-    layer_norm_lane<V>(v, gain, bias, lane);
-    uint16_t p[V];
-    load_row<V>(add_row + lane * V, p);
+    layer_norm_values<V>(v, g, b);
 #pragma unroll
     for (int i = 0; i < V; ++i)
     {
@@ -1712,7 +1775,7 @@ __device__ __forceinline__ bool first_lane_masses(const word* logits, uint16_t* 
     const uint32_t pair = v[0] | (uint32_t(v[1]) << 16);
     if (distributions)
     {
-        *reinterpret_cast<uint32_t*>(distributions + 2 * position) = pair;
+        *global_out(reinterpret_cast<uint32_t*>(distributions + 2 * position)) = pair;
     }
     if (!decoding)
     {
@@ -1776,6 +1839,46 @@ __device__ __forceinline__ bool first_lane_masses(const word* logits, uint16_t* 
     return valid;
 }
 
+// A flag in LDS that hands data in LDS from one wave of the workgroup to
+// another. LDS performs one wave's accesses in order, so the writer's data is
+// in once its own LDS accesses are done (lgkmcnt(0)), and the reader's later
+// LDS reads follow its read of the flag. A release or acquire at workgroup
+// scope would also wait for the wave's global stores (such as the tokens just
+// published), which this hand-off does not need.
+__device__ __forceinline__ void raise_lds_flag(int* flag)
+{
+    asm volatile("" ::: "memory");
+    wait_shared_memory();
+    __hip_atomic_store((__attribute__((address_space(3))) int*)(flag), 1, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ bool lds_flag_raised(int* flag)
+{
+    const int v = __hip_atomic_load((__attribute__((address_space(3))) int*)(flag), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");
+    return v != 0;
+}
+
+// Stores the compiler does not track, for a wave that never reads back what
+// it stored: for a tracked store the compiler waits for the acknowledgement
+// (s_waitcnt vmcnt(0)) before it reuses the store's data registers, while the
+// decoding wave's next symbol needs nothing from memory. The vector-memory
+// counter retires in issue order, so stores left out of the compiler's count
+// only ever make its own waits longer, never shorter. sc1 is the cache policy
+// of an agent-scope atomic store (the exchange words are polled with
+// agent-scope loads).
+__device__ __forceinline__ void untracked_store_u16(uint16_t* p, uint32_t value)
+{
+    asm volatile("global_store_short %0, %1, off" ::"v"(p), "v"(value) : "memory");
+}
+__device__ __forceinline__ void untracked_publish(word* w, std::size_t index, uint32_t payload, uint32_t epoch)
+{
+    const word value = (word(epoch) << 32) | payload;
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(w + index), "v"(value) : "memory");
+}
+
 // Softmax, masses and top decisions per lane: lane 0's by all waves
 // (first_lane_masses), every later lane's by one wave; wave 0 decodes the
 // lanes' symbols in stream order with the decoder held in `state` (LDS)
@@ -1784,6 +1887,8 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
                                          uint32_t* error, uint8_t* lds)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
+    lds = in_lds(lds);
+    state = reinterpret_cast<DecoderState*>(in_lds(reinterpret_cast<uint8_t*>(state)));
     Draw a;
     a.book = uniform(job->book);
     a.books = uniform(job->books);
@@ -1814,7 +1919,7 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
     int row = 0;
     if (active)
     {
-        row = a.row_base[warp] + a.step * a.step_stride + a.book;
+        row = *global(a.row_base + warp) + a.step * a.step_stride + a.book;
     }
     lds_barrier(); // the previous job's readers of LDS are done; `state` is current
     if (threadIdx.x < max_lanes)
@@ -1833,13 +1938,13 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
             const unsigned long long at = base_offset + uint32_t(lane * 4 + i);
             if (decoding && at < a.payload_bytes)
             {
-                four |= uint32_t(a.payload[at]) << (8 * i);
+                four |= uint32_t(*global(a.payload + at)) << (8 * i);
             }
         }
         reinterpret_cast<uint32_t*>(bytes)[lane] = four;
     }
     {
-        const int first_row = a.row_base[0] + a.step * a.step_stride + a.book;
+        const int first_row = *global(a.row_base) + a.step * a.step_stride + a.book;
         const bool ok = first_lane_masses(a.logits, a.distributions ? a.distributions + std::size_t(first_row) * 1024
                                                                     : nullptr,
                                           decoding, x, error, nodes, leaves, partials);
@@ -1855,7 +1960,7 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
             {
                 valid[0] = ok;
                 rows[0] = first_row;
-                __hip_atomic_store(ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                raise_lds_flag(ready);
             }
         }
     }
@@ -1915,7 +2020,7 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
         // Lane `warp`'s row, masses and decisions are in LDS: release them to wave 0.
         if (lane == 0)
         {
-            __hip_atomic_store(ready + warp, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            raise_lds_flag(ready + warp);
         }
     }
     if (warp != 0)
@@ -1925,36 +2030,48 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
     // Wave 0 decodes the lanes' symbols in stream order (decode.hip sample_kernel),
     // each as soon as its lane's masses are in, and publishes each token at once,
     // so the next book of lane w can start while the later lanes are decoded.
-    DecoderState s = decoding ? *state : DecoderState{};
-    const ByteWindow staged{bytes, window, base_offset, a.payload, a.payload_bytes};
-    for (int w = 0; w < M; ++w)
+    const auto output = [&](int w, int r, int token)
     {
-        while (__hip_atomic_load(ready + w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+        if (lane == 0)
+        {
+            untracked_publish(a.token_words, w, uint32_t(token), x.epoch);
+            untracked_store_u16(a.current + std::size_t(w) * a.books + a.book, uint32_t(token));
+            untracked_store_u16(a.tokens + r, uint32_t(token));
+        }
+    };
+    const auto wait_for_lane = [&](int w)
+    {
+        while (!lds_flag_raised(ready + w))
         {
             __builtin_amdgcn_s_sleep(1);
         }
-        const int r = __builtin_amdgcn_readfirstlane(rows[w]);
-        int token;
-        if (!decoding)
+        return __builtin_amdgcn_readfirstlane(rows[w]);
+    };
+    // Two loops, so that the decoding one makes no global load whose
+    // destination register a later lane's code reuses: the compiler would
+    // then wait for all of the wave's memory accesses, the stores just made
+    // included, at the start of every lane.
+    if (!decoding)
+    {
+        for (int w = 0; w < M; ++w)
         {
-            token = a.known[r];
+            const int r = wait_for_lane(w);
+            output(w, r, *global(a.known + r));
         }
-        else
-        {
-            if (!__builtin_amdgcn_readfirstlane(valid[w]))
-            {
-                s.failed = 1;
-            }
-            token = decode_symbol(top + w * 64, Masses{nodes + w * 1024, leaves + w * 1024}, s, staged);
-        }
-        if (lane == 0)
-        {
-            a.current[std::size_t(w) * a.books + a.book] = uint16_t(token);
-            a.tokens[r] = uint16_t(token);
-            publish(a.token_words, w, uint32_t(token), x.epoch);
-        }
+        return;
     }
-    if (decoding && lane == 0)
+    DecoderState s = *state;
+    const ByteWindow staged{bytes, window, base_offset, a.payload, a.payload_bytes};
+    for (int w = 0; w < M; ++w)
+    {
+        const int r = wait_for_lane(w);
+        if (!__builtin_amdgcn_readfirstlane(valid[w]))
+        {
+            s.failed = 1;
+        }
+        output(w, r, decode_symbol(top + w * 64, Masses{nodes + w * 1024, leaves + w * 1024}, s, staged));
+    }
+    if (lane == 0)
     {
         *state = s;
     }

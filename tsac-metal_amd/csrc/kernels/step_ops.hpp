@@ -232,7 +232,8 @@ __device__ __forceinline__ Bytes16 next_bytes(const ByteWindow& window, unsigned
         uint32_t v = 0;
         if (i < b.available)
         {
-            v = at + i < size ? uint32_t(staged[at + i]) : uint32_t(window.payload[from + i]);
+            v = at + i < size ? uint32_t(staged[at + i])
+                              : uint32_t(*(const __attribute__((address_space(1))) uint8_t*)(window.payload + from + i));
         }
         b.word[i / 4] |= __builtin_amdgcn_readfirstlane(v) << (8 * (i % 4));
     }
