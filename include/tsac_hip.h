@@ -271,6 +271,68 @@ int tsac_hip_audio_encode(tsac_hip_session* session, const tsac_hip_dac* dac, co
 int tsac_hip_audio_decode(tsac_hip_session* session, const tsac_hip_dac* dac, const uint8_t* stream, size_t length,
                           const tsac_hip_observer* observer, float** samples, size_t* frames, uint32_t* channels);
 
+/* ---- the original model files (tsac_*_q8.bin, dac_*_q8.bin) ---------------- */
+
+typedef struct tsac_hip_source tsac_hip_source;
+
+/* The file-format part of Limits (include/tsac/types.hpp:21-31); a zero field
+ * takes the reference default. */
+typedef struct tsac_hip_source_limits
+{
+    uint64_t file_bytes, tensor_elements, tensors, metadata_bytes, name_bytes;
+} tsac_hip_source_limits;
+
+/* Tensor (src/weights/source_model.hpp:19-29): storage 0 float32, 1 BF16,
+ * 0x8000b BF8, 0x8000e BF8L; dims axis 0 fastest. `name` lives as long as the
+ * source. */
+typedef struct tsac_hip_source_tensor
+{
+    const char* name;
+    uint32_t storage, rank;
+    uint64_t dims[8];
+    uint64_t elements;
+} tsac_hip_source_tensor;
+
+/* SourceModel::load and ::parse (src/weights/source_model.hpp:33-34,
+ * src/weights/source_model.cpp:63-166): the record format with every check of
+ * the reference's parser; the bytes are copied. */
+int tsac_hip_source_load(const char* path, const tsac_hip_source_limits* limits, tsac_hip_source** source);
+int tsac_hip_source_parse(const uint8_t* bytes, size_t length, const tsac_hip_source_limits* limits,
+                          tsac_hip_source** source);
+void tsac_hip_source_destroy(tsac_hip_source* source);
+/* SourceModel::tensors and ::metadata_json (src/weights/source_model.hpp:36-44). */
+int tsac_hip_source_tensor_count(const tsac_hip_source* source, size_t* count);
+int tsac_hip_source_tensor_info(const tsac_hip_source* source, size_t index, tsac_hip_source_tensor* info);
+int tsac_hip_source_metadata(const tsac_hip_source* source, const char** json, size_t* length);
+/* SourceModel::dequantize (src/weights/source_model.cpp:284-329) into `out`
+ * (capacity in floats, at least the tensor's element count). */
+int tsac_hip_source_dequantize(const tsac_hip_source* source, const char* name, float* out, size_t capacity);
+/* SourceModel::dac_config and ::transformer_config
+ * (src/weights/source_model.cpp:168-266): the shape and inventory checks. */
+int tsac_hip_source_dac_config(const tsac_hip_source* source, uint32_t* channels, uint32_t* books);
+int tsac_hip_source_transformer_config(const tsac_hip_source* source, uint32_t* books);
+
+/* The packer's preparation of a probability model (src/weights/pack_main.cpp:305-391)
+ * from its file and the codec file of the same variant, whose codebook
+ * projections are the feedback embeddings: fills `desc` for
+ * tsac_hip_model_create with pointers into `prepared` (valid until it is
+ * destroyed). */
+typedef struct tsac_hip_prepared_transformer tsac_hip_prepared_transformer;
+int tsac_hip_prepare_transformer(const tsac_hip_source* transformer, const tsac_hip_source* dac,
+                                 tsac_hip_prepared_transformer** prepared, tsac_hip_model_desc* desc);
+void tsac_hip_prepared_transformer_destroy(tsac_hip_prepared_transformer* prepared);
+/* The packer's preparation of a codec (src/weights/pack_main.cpp:172-300):
+ * fills `desc` for tsac_hip_dac_create with pointers into `prepared`. */
+typedef struct tsac_hip_prepared_dac tsac_hip_prepared_dac;
+int tsac_hip_prepare_dac(const tsac_hip_source* dac, tsac_hip_prepared_dac** prepared, tsac_hip_dac_desc* desc);
+void tsac_hip_prepared_dac_destroy(tsac_hip_prepared_dac* prepared);
+/* Preparation and creation in one call (ModelDirectory + MetalTransformer::from_model,
+ * src/weights/model_directory.hpp, src/metal/transformer.hpp:16; the DAC
+ * models' from_model): the prepared host arrays are released on return. */
+int tsac_hip_model_create_from_source(const tsac_hip_source* transformer, const tsac_hip_source* dac,
+                                      const tsac_hip_limits* limits, tsac_hip_model** model);
+int tsac_hip_dac_create_from_source(const tsac_hip_source* dac, const tsac_hip_limits* limits, tsac_hip_dac** model);
+
 /* ---- operators on device memory (hipStream_t passed as void*) -------------- */
 
 typedef struct tsac_hip_device_linear tsac_hip_device_linear;

@@ -485,10 +485,36 @@ class Reference(_Kernels, _DspKernels):
         lib.ref_pack_normal_observed.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u8p, sz,
                                                  C.POINTER(sz), C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]
         lib.ref_distributions.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u16p]
+        lib.ref_source_parse.argtypes = [u8p, sz, C.c_uint64, C.c_uint64, C.POINTER(sz)]
+        lib.ref_source_dequantize.argtypes = [u8p, sz, C.c_char_p, f32p, sz]
+        lib.ref_source_configs.argtypes = [u8p, sz] + [C.POINTER(C.c_uint)] * 3
 
     @staticmethod
     def available() -> bool:
         return REF_PATH.exists()
+
+    # SourceModel (src/weights/source_model.cpp) on an original-format file.
+    def source_parse(self, data: bytes, file_bytes: int = 0, metadata_bytes: int = 0):
+        """The tensor count, or None when the reference's parser rejects the file."""
+        b = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+        n = sz()
+        status = self.lib.ref_source_parse(ptr(b, C.c_uint8), len(data), file_bytes, metadata_bytes, C.byref(n))
+        return None if status else n.value
+
+    def source_dequantize(self, data: bytes, name: str, count: int) -> np.ndarray:
+        b = np.frombuffer(data, np.uint8).copy()
+        out = np.zeros(max(count, 1), np.float32)
+        self._check(self.lib.ref_source_dequantize(ptr(b, C.c_uint8), len(data), name.encode(), ptr(out, C.c_float),
+                                                   out.size))
+        return out[:count]
+
+    def source_configs(self, data: bytes) -> tuple:
+        """(channels, codebooks) of dac_config and codebooks of transformer_config,
+        each 0 where the reference rejects the file for that role."""
+        b = np.frombuffer(data, np.uint8).copy()
+        c, d, t = C.c_uint(), C.c_uint(), C.c_uint()
+        self._check(self.lib.ref_source_configs(ptr(b, C.c_uint8), len(data), C.byref(c), C.byref(d), C.byref(t)))
+        return c.value, d.value, t.value
 
     def gelu_table(self, values):
         v = np.ascontiguousarray(values, np.uint16).copy()

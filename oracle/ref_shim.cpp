@@ -20,6 +20,7 @@
 #include "scalar/dsp.hpp"
 #include "weights/normalization.hpp"
 #include "weights/preparation.hpp"
+#include "weights/source_model.hpp"
 
 #include "tsac_oracle.h"
 
@@ -607,5 +608,67 @@ void ref_project_codebook(std::uint16_t index, const float* codebook, const floa
 {
     weights::project_codebook(index, std::span(codebook, 8192), std::span(weights, 8192), std::span(bias, 1024),
                               std::span(out, 1024), true);
+}
+
+// SourceModel (src/weights/source_model.cpp) on an in-memory file: 0 when it
+// parses (tensor count to *tensors), nonzero when the reference rejects it.
+int ref_source_parse(const std::uint8_t* bytes, std::size_t length, std::uint64_t file_bytes,
+                     std::uint64_t metadata_bytes, std::size_t* tensors)
+{
+    return guarded(
+        [&]
+        {
+            Limits limits;
+            if (file_bytes)
+            {
+                limits.file_bytes = file_bytes;
+            }
+            if (metadata_bytes)
+            {
+                limits.metadata_bytes = metadata_bytes;
+            }
+            const auto model = packing::SourceModel::parse(Bytes(bytes, bytes + length), limits);
+            *tensors = model.tensors().size();
+        });
+}
+
+int ref_source_dequantize(const std::uint8_t* bytes, std::size_t length, const char* name, float* out,
+                          std::size_t capacity)
+{
+    return guarded(
+        [&]
+        {
+            const auto model = packing::SourceModel::parse(Bytes(bytes, bytes + length));
+            const auto values = model.dequantize(name);
+            detail::require(values.size() <= capacity, "capacity");
+            std::memcpy(out, values.data(), values.size() * sizeof(float));
+        });
+}
+
+int ref_source_configs(const std::uint8_t* bytes, std::size_t length, unsigned* channels, unsigned* dac_books,
+                       unsigned* transformer_books)
+{
+    return guarded(
+        [&]
+        {
+            const auto model = packing::SourceModel::parse(Bytes(bytes, bytes + length));
+            *channels = *dac_books = *transformer_books = 0;
+            try
+            {
+                const auto c = model.dac_config();
+                *channels = c.channels;
+                *dac_books = c.codebooks;
+            }
+            catch (const std::exception&)
+            {
+            }
+            try
+            {
+                *transformer_books = model.transformer_config().codebooks;
+            }
+            catch (const std::exception&)
+            {
+            }
+        });
 }
 }

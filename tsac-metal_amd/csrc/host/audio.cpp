@@ -20,9 +20,8 @@ float bf16_float(uint16_t bits)
     return std::bit_cast<float>(uint32_t(bits) << 16);
 }
 
-// fold_dac_weight_norm_into (src/weights/normalization.cpp:47-95): each stored
-// column's squares reduced by a balanced adjacent-pair tree (an odd tail carried
-// up), RMS-normalised, times 1/sqrt(fan_in), times the column's gain.
+} // namespace
+
 void fold_dac_weight_norm(std::vector<float>& w, const float* gain, std::size_t fan_in, std::size_t columns)
 {
     require(fan_in > 0 && w.size() == fan_in * columns, "weight normalization shape mismatch");
@@ -61,7 +60,6 @@ void fold_dac_weight_norm(std::vector<float>& w, const float* gain, std::size_t 
         }
     }
 }
-} // namespace
 
 ConvShape dac_conv_shape(bool synthesis, unsigned channels, unsigned index)
 {

@@ -48,6 +48,12 @@ std::size_t dac_activation_width(bool synthesis, unsigned index);
 // (src/weights/normalization.cpp:47-95), into the stored layout.
 std::vector<float> prepare_dac_convolution(const DacConvolutionSource& source, const ConvShape& shape);
 
+// fold_dac_weight_norm_into (src/weights/normalization.cpp:47-95), in place on
+// `columns` stored columns of `fan_in` values: each column's squares reduced by
+// a balanced adjacent-pair tree (an odd tail carried up), RMS-normalised, times
+// 1/sqrt(fan_in), times the column's gain.
+void fold_dac_weight_norm(std::vector<float>& w, const float* gain, std::size_t fan_in, std::size_t columns);
+
 // The packer's quantizer preparation for one codebook (src/weights/pack_main.cpp:244-300):
 // normalize_search of each codebook row (src/weights/preparation.cpp:62-84) and the
 // DAC weight-norm folds of in_proj (fan-in 1024) and out_proj (fan-in 8).

@@ -3,6 +3,7 @@
 #include "../../../include/tsac_hip.h"
 #include "audio.hpp"
 #include "runtime.hpp"
+#include "source.hpp"
 
 #include <cstdlib>
 #include <cstring>
@@ -23,6 +24,21 @@ struct tsac_hip_session
 struct tsac_hip_dac
 {
     std::unique_ptr<DacModel> dac;
+};
+
+struct tsac_hip_source
+{
+    SourceModel model;
+};
+
+struct tsac_hip_prepared_transformer
+{
+    PreparedTransformer prepared;
+};
+
+struct tsac_hip_prepared_dac
+{
+    PreparedDac prepared;
 };
 
 struct tsac_hip_device_linear
@@ -142,6 +158,49 @@ SymbolObserver observer_of(const tsac_hip_observer* o)
         };
     }
     return r;
+}
+
+SourceLimits source_limits_of(const tsac_hip_source_limits* l)
+{
+    SourceLimits r;
+    if (l)
+    {
+        r.file_bytes = l->file_bytes ? l->file_bytes : r.file_bytes;
+        r.tensor_elements = l->tensor_elements ? l->tensor_elements : r.tensor_elements;
+        r.tensors = l->tensors ? l->tensors : r.tensors;
+        r.metadata_bytes = l->metadata_bytes ? l->metadata_bytes : r.metadata_bytes;
+        r.name_bytes = l->name_bytes ? l->name_bytes : r.name_bytes;
+    }
+    return r;
+}
+
+void fill_model_desc(const ModelDesc& m, tsac_hip_model_desc* desc)
+{
+    const Geometry& g = m.geometry;
+    desc->geometry = tsac_hip_geometry{g.width,  g.heads,    g.head_width, g.ffn,   g.temporal_layers,
+                                       g.codebook_layers, g.latent, g.alphabet, g.books, g.channels,
+                                       g.context, g.attention_scale};
+    static_assert(sizeof(LinearHost) == sizeof(tsac_hip_linear));
+    desc->projections = reinterpret_cast<const tsac_hip_linear*>(m.projections);
+    desc->norm_gain = m.gain;
+    desc->norm_bias = m.bias;
+    desc->positions = m.positions;
+    desc->rotations = m.rotations;
+    desc->embeddings = m.embeddings;
+}
+
+void fill_dac_desc(const PreparedDac& d, tsac_hip_dac_desc* desc)
+{
+    static_assert(sizeof(DacConvolutionSource) == sizeof(tsac_hip_dac_convolution));
+    static_assert(sizeof(RvqSource) == sizeof(tsac_hip_rvq_book));
+    *desc = tsac_hip_dac_desc{};
+    desc->channels = d.channels();
+    desc->books = d.books();
+    std::memcpy(desc->analysis, d.analysis(), sizeof desc->analysis);
+    std::memcpy(desc->synthesis, d.synthesis(), sizeof desc->synthesis);
+    std::memcpy(desc->analysis_alpha, d.analysis_alpha(), sizeof desc->analysis_alpha);
+    std::memcpy(desc->synthesis_alpha, d.synthesis_alpha(), sizeof desc->synthesis_alpha);
+    std::memcpy(desc->rvq, d.rvq(), d.books() * sizeof(tsac_hip_rvq_book));
 }
 
 LinearPath path_of(int path)
@@ -284,6 +343,180 @@ int tsac_hip_dac_create(const tsac_hip_dac_desc* desc, const tsac_hip_limits* li
 void tsac_hip_dac_destroy(tsac_hip_dac* dac)
 {
     delete dac;
+}
+
+
+int tsac_hip_source_load(const char* path, const tsac_hip_source_limits* limits, tsac_hip_source** source)
+{
+    return guarded(
+        [&]
+        {
+            require(path && source, "missing argument");
+            *source = new tsac_hip_source{SourceModel::load(path, source_limits_of(limits))};
+        });
+}
+
+int tsac_hip_source_parse(const uint8_t* bytes, size_t length, const tsac_hip_source_limits* limits,
+                          tsac_hip_source** source)
+{
+    return guarded(
+        [&]
+        {
+            require((bytes || !length) && source, "missing argument");
+            *source = new tsac_hip_source{
+                SourceModel::parse(std::vector<uint8_t>(bytes, bytes + length), source_limits_of(limits))};
+        });
+}
+
+void tsac_hip_source_destroy(tsac_hip_source* source)
+{
+    delete source;
+}
+
+int tsac_hip_source_tensor_count(const tsac_hip_source* source, size_t* count)
+{
+    return guarded(
+        [&]
+        {
+            require(source && count, "missing argument");
+            *count = source->model.tensors().size();
+        });
+}
+
+int tsac_hip_source_tensor_info(const tsac_hip_source* source, size_t index, tsac_hip_source_tensor* info)
+{
+    return guarded(
+        [&]
+        {
+            require(source && info, "missing argument");
+            require(index < source->model.tensors().size(), "tensor index out of range");
+            const SourceTensor& t = source->model.tensors()[index];
+            *info = tsac_hip_source_tensor{};
+            info->name = t.name.c_str();
+            info->storage = uint32_t(t.storage);
+            info->rank = uint32_t(t.dims.size());
+            for (std::size_t a = 0; a < t.dims.size(); ++a)
+            {
+                info->dims[a] = t.dims[a];
+            }
+            info->elements = t.elements;
+        });
+}
+
+int tsac_hip_source_metadata(const tsac_hip_source* source, const char** json, size_t* length)
+{
+    return guarded(
+        [&]
+        {
+            require(source && json && length, "missing argument");
+            *json = source->model.metadata().data();
+            *length = source->model.metadata().size();
+        });
+}
+
+int tsac_hip_source_dequantize(const tsac_hip_source* source, const char* name, float* out, size_t capacity)
+{
+    return guarded(
+        [&]
+        {
+            require(source && name && out, "missing argument");
+            const auto values = source->model.dequantize(name);
+            require(values.size() <= capacity, "output buffer too small for the tensor");
+            std::memcpy(out, values.data(), values.size() * sizeof(float));
+        });
+}
+
+int tsac_hip_source_dac_config(const tsac_hip_source* source, uint32_t* channels, uint32_t* books)
+{
+    return guarded(
+        [&]
+        {
+            require(source && channels && books, "missing argument");
+            const SourceDacConfig c = source_dac_config(source->model);
+            *channels = c.channels;
+            *books = c.books;
+        });
+}
+
+int tsac_hip_source_transformer_config(const tsac_hip_source* source, uint32_t* books)
+{
+    return guarded(
+        [&]
+        {
+            require(source && books, "missing argument");
+            *books = source_transformer_books(source->model);
+        });
+}
+
+int tsac_hip_prepare_transformer(const tsac_hip_source* transformer, const tsac_hip_source* dac,
+                                 tsac_hip_prepared_transformer** prepared, tsac_hip_model_desc* desc)
+{
+    return guarded(
+        [&]
+        {
+            require(transformer && dac && prepared && desc, "missing argument");
+            auto p = std::make_unique<tsac_hip_prepared_transformer>(
+                tsac_hip_prepared_transformer{PreparedTransformer(transformer->model, dac->model)});
+            fill_model_desc(p->prepared.desc(), desc);
+            *prepared = p.release();
+        });
+}
+
+void tsac_hip_prepared_transformer_destroy(tsac_hip_prepared_transformer* prepared)
+{
+    delete prepared;
+}
+
+int tsac_hip_prepare_dac(const tsac_hip_source* dac, tsac_hip_prepared_dac** prepared, tsac_hip_dac_desc* desc)
+{
+    return guarded(
+        [&]
+        {
+            require(dac && prepared && desc, "missing argument");
+            auto p = std::make_unique<tsac_hip_prepared_dac>(tsac_hip_prepared_dac{PreparedDac(dac->model)});
+            fill_dac_desc(p->prepared, desc);
+            *prepared = p.release();
+        });
+}
+
+void tsac_hip_prepared_dac_destroy(tsac_hip_prepared_dac* prepared)
+{
+    delete prepared;
+}
+
+int tsac_hip_model_create_from_source(const tsac_hip_source* transformer, const tsac_hip_source* dac,
+                                      const tsac_hip_limits* limits, tsac_hip_model** model)
+{
+    tsac_hip_prepared_transformer* prepared = nullptr;
+    tsac_hip_model_desc desc{};
+    if (const int status = tsac_hip_prepare_transformer(transformer, dac, &prepared, &desc); status != TSAC_HIP_OK)
+    {
+        return status;
+    }
+    const int status = model ? tsac_hip_model_create(&desc, limits, model) : TSAC_HIP_ERROR;
+    if (!model)
+    {
+        last_error = "missing argument";
+    }
+    tsac_hip_prepared_transformer_destroy(prepared);
+    return status;
+}
+
+int tsac_hip_dac_create_from_source(const tsac_hip_source* dac, const tsac_hip_limits* limits, tsac_hip_dac** model)
+{
+    tsac_hip_prepared_dac* prepared = nullptr;
+    tsac_hip_dac_desc desc{};
+    if (const int status = tsac_hip_prepare_dac(dac, &prepared, &desc); status != TSAC_HIP_OK)
+    {
+        return status;
+    }
+    const int status = model ? tsac_hip_dac_create(&desc, limits, model) : TSAC_HIP_ERROR;
+    if (!model)
+    {
+        last_error = "missing argument";
+    }
+    tsac_hip_prepared_dac_destroy(prepared);
+    return status;
 }
 
 int tsac_hip_prepare_rvq(const float* codebook, const float* in_v, const float* in_g, const float* out_v,

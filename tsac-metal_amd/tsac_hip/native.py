@@ -34,7 +34,11 @@ EXPORTS = (
     "tsac_hip_probe_read", "tsac_hip_probe_mfma", "tsac_hip_encode_observed", "tsac_hip_decode_observed",
     "tsac_hip_linear_apply_static", "tsac_hip_dac_create", "tsac_hip_dac_destroy", "tsac_hip_prepare_rvq",
     "tsac_hip_dac_analyze", "tsac_hip_dac_synthesize", "tsac_hip_audio_encode", "tsac_hip_audio_decode",
-    "tsac_hip_dac_apply",
+    "tsac_hip_dac_apply", "tsac_hip_source_load", "tsac_hip_source_parse", "tsac_hip_source_destroy",
+    "tsac_hip_source_tensor_count", "tsac_hip_source_tensor_info", "tsac_hip_source_metadata",
+    "tsac_hip_source_dequantize", "tsac_hip_source_dac_config", "tsac_hip_source_transformer_config",
+    "tsac_hip_prepare_transformer", "tsac_hip_prepared_transformer_destroy", "tsac_hip_prepare_dac",
+    "tsac_hip_prepared_dac_destroy", "tsac_hip_model_create_from_source", "tsac_hip_dac_create_from_source",
 )
 
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_TILES = 0, 1, 2, 3
@@ -97,6 +101,16 @@ class DacDesc(C.Structure):
     _fields_ = [("channels", C.c_uint32), ("books", C.c_uint32), ("analysis", DacConvolution * 30),
                 ("analysis_alpha", f32p * 29), ("synthesis", DacConvolution * 30), ("synthesis_alpha", f32p * 29),
                 ("rvq", RvqBook * 12)]
+
+
+class SourceLimits(C.Structure):
+    _fields_ = [(name, C.c_uint64) for name in (
+        "file_bytes", "tensor_elements", "tensors", "metadata_bytes", "name_bytes")]
+
+
+class SourceTensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("storage", C.c_uint32), ("rank", C.c_uint32), ("dims", C.c_uint64 * 8),
+                ("elements", C.c_uint64)]
 
 
 class EncodeOptions(C.Structure):
@@ -162,6 +176,21 @@ def library() -> C.CDLL:
         lib.tsac_hip_attention_causal.argtypes = [vp, sz, sz, vp, vp, vp, sz, sz, vp, C.c_float, vp, vp]
         lib.tsac_hip_probe_read.argtypes = [vp, sz, vp]
         lib.tsac_hip_probe_mfma.argtypes = [sz, C.c_int, C.POINTER(C.c_double), vp]
+        lib.tsac_hip_source_load.argtypes = [C.c_char_p, C.POINTER(SourceLimits), C.POINTER(vp)]
+        lib.tsac_hip_source_parse.argtypes = [u8p, sz, C.POINTER(SourceLimits), C.POINTER(vp)]
+        lib.tsac_hip_source_destroy.argtypes = [vp]
+        lib.tsac_hip_source_tensor_count.argtypes = [vp, C.POINTER(sz)]
+        lib.tsac_hip_source_tensor_info.argtypes = [vp, sz, C.POINTER(SourceTensorInfo)]
+        lib.tsac_hip_source_metadata.argtypes = [vp, C.POINTER(C.c_char_p), C.POINTER(sz)]
+        lib.tsac_hip_source_dequantize.argtypes = [vp, C.c_char_p, f32p, sz]
+        lib.tsac_hip_source_dac_config.argtypes = [vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]
+        lib.tsac_hip_source_transformer_config.argtypes = [vp, C.POINTER(C.c_uint32)]
+        lib.tsac_hip_prepare_transformer.argtypes = [vp, vp, C.POINTER(vp), C.POINTER(ModelDesc)]
+        lib.tsac_hip_prepared_transformer_destroy.argtypes = [vp]
+        lib.tsac_hip_prepare_dac.argtypes = [vp, C.POINTER(vp), C.POINTER(DacDesc)]
+        lib.tsac_hip_prepared_dac_destroy.argtypes = [vp]
+        lib.tsac_hip_model_create_from_source.argtypes = [vp, vp, C.POINTER(Limits), C.POINTER(vp)]
+        lib.tsac_hip_dac_create_from_source.argtypes = [vp, C.POINTER(Limits), C.POINTER(vp)]
         _lib = lib
     return _lib
 
@@ -210,6 +239,138 @@ def _release(owner, destroy: str):
     owner.handle = None
 
 
+class SourceFile:
+    """An original model file (tsac_*_q8.bin or dac_*_q8.bin) parsed by the
+    library (tsac_hip_source_parse/load: SourceModel, src/weights/source_model.hpp)."""
+
+    def __init__(self, data: bytes | None = None, path: str | None = None, limits: SourceLimits | None = None):
+        lib = library()
+        handle = vp()
+        if path is not None:
+            check(lib.tsac_hip_source_load(str(path).encode(), C.byref(limits) if limits else None,
+                                           C.byref(handle)))
+        else:
+            b = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+            check(lib.tsac_hip_source_parse(_ptr(b, C.c_uint8), len(data), C.byref(limits) if limits else None,
+                                            C.byref(handle)))
+        self.handle, self._library = handle, lib
+
+    def __del__(self):
+        _release(self, "tsac_hip_source_destroy")
+
+    def close(self):
+        _release(self, "tsac_hip_source_destroy")
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def tensors(self) -> list:
+        """[(name, storage, dims (axis 0 fastest), elements)] in file order."""
+        n = sz()
+        check(library().tsac_hip_source_tensor_count(self.handle, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            info = SourceTensorInfo()
+            check(library().tsac_hip_source_tensor_info(self.handle, i, C.byref(info)))
+            out.append((info.name.decode(), info.storage, tuple(info.dims[:info.rank]), info.elements))
+        return out
+
+    def metadata(self) -> bytes:
+        p, n = C.c_char_p(), sz()
+        check(library().tsac_hip_source_metadata(self.handle, C.byref(p), C.byref(n)))
+        return C.string_at(p, n.value)
+
+    def dequantize(self, name: str) -> np.ndarray:
+        elements = {t[0]: t[3] for t in self.tensors()}.get(name, 0)
+        out = np.zeros(max(elements, 1), np.float32)
+        check(library().tsac_hip_source_dequantize(self.handle, name.encode(), _ptr(out, C.c_float), out.size))
+        return out[:elements]
+
+    def dac_config(self) -> tuple:
+        channels, books = C.c_uint32(), C.c_uint32()
+        check(library().tsac_hip_source_dac_config(self.handle, C.byref(channels), C.byref(books)))
+        return channels.value, books.value
+
+    def transformer_books(self) -> int:
+        books = C.c_uint32()
+        check(library().tsac_hip_source_transformer_config(self.handle, C.byref(books)))
+        return books.value
+
+
+def prepare_transformer(transformer: SourceFile, dac: SourceFile):
+    """The packer's preparation of a probability model (tsac_hip_prepare_transformer),
+    copied out as a tsac_hip.synthetic.Model."""
+    from .synthetic import Geometry as GeometryShape, Model
+
+    prepared, desc = vp(), ModelDesc()
+    check(library().tsac_hip_prepare_transformer(transformer.handle, dac.handle, C.byref(prepared),
+                                                 C.byref(desc)))
+    try:
+        g = desc.geometry
+        geometry = GeometryShape(g.width, g.heads, g.head_width, g.ffn, g.temporal_layers, g.codebook_layers,
+                                 g.latent, g.alphabet, g.books, g.channels, g.context)
+        projections = []
+        for i in range(geometry.projection_count):
+            k, n = geometry.projection_shape(i)
+            linear = desc.projections[i]
+            projections.append((np.ctypeslib.as_array(linear.values, shape=(n, k)).copy(),
+                                np.ctypeslib.as_array(linear.scales, shape=(k // 256, n)).copy(),
+                                np.ctypeslib.as_array(linear.bias, shape=(n,)).copy()))
+        gains = [np.ctypeslib.as_array(desc.norm_gain[i], shape=(g.width,)).copy() for i in range(geometry.norm_count)]
+        biases = [np.ctypeslib.as_array(desc.norm_bias[i], shape=(g.width,)).copy() for i in range(geometry.norm_count)]
+        positions = np.ctypeslib.as_array(desc.positions, shape=(g.books, g.width)).copy()
+        rotations = np.ctypeslib.as_array(desc.rotations, shape=(g.context, g.head_width)).copy()
+        embeddings = np.ctypeslib.as_array(desc.embeddings, shape=(g.books, g.alphabet, g.latent)).copy()
+        return Model(geometry, projections, gains, biases, positions, rotations, embeddings)
+    finally:
+        library().tsac_hip_prepared_transformer_destroy(prepared)
+
+
+def prepare_dac(dac: SourceFile) -> dict:
+    """The packer's preparation of a codec (tsac_hip_prepare_dac), copied out:
+    {"channels", "books", "analysis"/"synthesis": [(dims, values or (int8, BF16 scales), gain, bias)],
+    "analysis_alpha"/"synthesis_alpha": [alpha], "rvq": [(codebook, search, input_weights,
+    input_bias, output_weights, output_bias)]}."""
+    prepared, desc = vp(), DacDesc()
+    check(library().tsac_hip_prepare_dac(dac.handle, C.byref(prepared), C.byref(desc)))
+    try:
+        out = {"channels": desc.channels, "books": desc.books}
+        for graph in ("analysis", "synthesis"):
+            convs = []
+            for c in getattr(desc, graph):
+                dims = tuple(c.dims)
+                count = dims[0] * dims[1] * dims[2]
+                outer = dims[2]
+                channels_out = dims[0] if (graph == "synthesis" and len(convs) in range(1, 29) and
+                                           (len(convs) - 1) % 7 == 0) else dims[2]
+                if c.quantized:
+                    padded = (dims[1] + 7) // 8 * 8
+                    values = (np.ctypeslib.as_array(c.quantized, shape=(count,)).copy(),
+                              np.ctypeslib.as_array(c.scales, shape=(outer, dims[0] // 32, padded)).copy())
+                else:
+                    values = np.ctypeslib.as_array(c.values, shape=(count,)).copy()
+                convs.append((dims, values, np.ctypeslib.as_array(c.gain, shape=(outer,)).copy(),
+                              np.ctypeslib.as_array(c.bias, shape=(channels_out,)).copy()))
+            out[graph] = convs
+        from .synthetic import dac_activation_width
+
+        for graph, synthesis in (("analysis", False), ("synthesis", True)):
+            out[graph + "_alpha"] = [np.ctypeslib.as_array(getattr(desc, graph + "_alpha")[i],
+                                                           shape=(dac_activation_width(synthesis, i),)).copy()
+                                     for i in range(29)]
+        shapes = (8192, 8192, 8192, 8, 8192, 1024)
+        out["rvq"] = [tuple(np.ctypeslib.as_array(getattr(desc.rvq[b], name), shape=(n,)).copy()
+                            for name, n in zip(("codebook", "search", "input_weights", "input_bias",
+                                                "output_weights", "output_bias"), shapes))
+                      for b in range(desc.books)]
+        return out
+    finally:
+        library().tsac_hip_prepared_dac_destroy(prepared)
+
+
 class HipModel:
     """Immutable device model (MetalTransformer::from_model, src/metal/transformer.hpp:16)."""
 
@@ -222,6 +383,21 @@ class HipModel:
                                         C.byref(handle)))
         self.handle, self._library = handle, lib
         del keep
+
+    @classmethod
+    def from_source(cls, transformer: SourceFile, dac: SourceFile, limits: Limits | None = None) -> "HipModel":
+        """tsac_hip_model_create_from_source: the original files straight to the device."""
+        from .synthetic import Geometry as GeometryShape
+
+        lib = library()
+        handle = vp()
+        check(lib.tsac_hip_model_create_from_source(transformer.handle, dac.handle,
+                                                    C.byref(limits) if limits else None, C.byref(handle)))
+        self = cls.__new__(cls)
+        channels, books = dac.dac_config()
+        self.geometry = GeometryShape(books=books, channels=channels)
+        self.handle, self._library = handle, lib
+        return self
 
     def __del__(self):
         _release(self, "tsac_hip_model_destroy")
@@ -343,6 +519,17 @@ class HipDac:
     """The DAC codec's device model (tsac_hip_dac_create) from a
     tsac_hip.synthetic.DacModel: convolutions in their source encoding, Snake
     alphas, and the quantizer prepared as the packer prepares it."""
+
+    @classmethod
+    def from_source(cls, dac: SourceFile, limits: Limits | None = None) -> "HipDac":
+        """tsac_hip_dac_create_from_source: an original codec file straight to the device."""
+        lib = library()
+        handle = vp()
+        check(lib.tsac_hip_dac_create_from_source(dac.handle, C.byref(limits) if limits else None, C.byref(handle)))
+        self = cls.__new__(cls)
+        self.channels, self.books = dac.dac_config()
+        self.handle, self._library = handle, lib
+        return self
 
     def __init__(self, model, limits: Limits | None = None):
         self.channels, self.books = model.channels, len(model.codebook)

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import dataclasses
 import math
+import struct
 
 import numpy as np
 
@@ -309,3 +310,155 @@ def synthetic_audio(seconds: float, channels: int = 2, seed: int = 0, rate: int 
         out[:, c] += amplitude * noise
     out /= max(1.0, np.max(np.abs(out)) / 0.99)
     return np.clip(np.round(out * 32767), -32768, 32767).astype(np.int16)
+
+
+# ---------------------------------------------------------------- original model files
+
+#: Storage codes of an original model file's tensor records (src/weights/source_model.hpp:11-17).
+F32, BF16, BF8, BF8L = 0, 1, 0x8000B, 0x8000E
+
+
+@dataclasses.dataclass
+class SourceTensor:
+    """One record of an original model file: dims axis 0 fastest, payload as stored."""
+    name: str
+    storage: int
+    dims: tuple
+    payload: bytes
+
+
+def _padded(data: bytes, alignment: int) -> bytes:
+    return data + bytes(-len(data) % alignment)
+
+
+def f32_tensor(name: str, dims: tuple, values) -> SourceTensor:
+    values = np.ascontiguousarray(values, dtype="<f4").ravel()
+    assert values.size == int(np.prod(dims)), name
+    return SourceTensor(name, F32, tuple(dims), values.tobytes())
+
+
+def bf16_tensor(name: str, dims: tuple, bits) -> SourceTensor:
+    bits = np.ascontiguousarray(bits, dtype="<u2").ravel()
+    assert bits.size == int(np.prod(dims)), name
+    return SourceTensor(name, BF16, tuple(dims), bits.tobytes())
+
+
+def quantized_tensor(name: str, dims: tuple, values, scale_bits, block: int) -> SourceTensor:
+    """BF8 (block 32) or BF8L (block 256): int8 values in storage order, then
+    BF16 scales [outer][dims[0]/block][align8(dims[1])], each plane padded to
+    256 bytes (src/weights/source_model.cpp:18-45,148-160)."""
+    values = np.ascontiguousarray(values, dtype=np.int8).ravel()
+    rows, cols = dims[0], dims[1]
+    outer = int(np.prod(dims)) // rows // cols
+    scale_bits = np.ascontiguousarray(scale_bits, dtype="<u2")
+    assert values.size == int(np.prod(dims)) and scale_bits.shape == (outer, rows // block, (cols + 7) // 8 * 8), name
+    payload = _padded(values.tobytes(), 256) + _padded(scale_bits.tobytes(), 256)
+    return SourceTensor(name, BF8 if block == 32 else BF8L, tuple(dims), payload)
+
+
+def source_file(tensors: list, metadata: bytes = b'{"producer": "tsac_hip.synthetic"}') -> bytes:
+    """The record format of tsac_*_q8.bin / dac_*_q8.bin (src/weights/source_model.cpp:99-166):
+    u32 0x23f4aefb, u32 metadata length, metadata, then per tensor u32 0x23f4aefa,
+    u32 storage, u32 rank, u32 name length, u32 dims[rank], name, payload."""
+    out = bytearray(struct.pack("<II", 0x23F4AEFB, len(metadata)) + metadata)
+    for t in tensors:
+        name = t.name.encode()
+        out += struct.pack("<IIII", 0x23F4AEFA, t.storage, len(t.dims), len(name))
+        out += struct.pack(f"<{len(t.dims)}I", *t.dims) + name + t.payload
+    return bytes(out)
+
+
+def transformer_source(model: Model) -> list:
+    """A reference-geometry Model as the tensors of tsac_*_q8.bin
+    (src/weights/source_model.cpp:215-266): BF8L projections [K][N] with
+    float32 biases (none for the cb_proj tensors), BF16 norms, codebook
+    positions and rotary table. The feedback embeddings are not in this file:
+    the packer derives them from the codec's quantizer."""
+    g = model.geometry
+    assert (g.width, g.heads, g.head_width, g.ffn, g.temporal_layers, g.codebook_layers, g.latent,
+            g.context) == (512, 4, 128, 2048, 12, 3, 1024, 1024), "the file format holds the reference geometry"
+    tensors = []
+
+    def projection(name: str, index: int, with_bias: bool):
+        values, scales, bias = model.projections[index]
+        k, n = g.projection_shape(index)
+        bits = bf16_bits(scales)
+        assert np.array_equal(bf16_float(bits), scales), "block scales must be BF16 values"
+        padded = np.zeros((1, k // 256, (n + 7) // 8 * 8), np.uint16)
+        padded[0, :, :n] = bits
+        tensors.append(quantized_tensor(name, (k, n), values, padded, 256))
+        if with_bias:
+            tensors.append(f32_tensor(name[:-1] + "b", (n,), bias))
+
+    norm = 0
+    for stack, layers, first in (("", g.temporal_layers, 0), ("codebook_decoder.", g.codebook_layers,
+                                                                 4 * g.temporal_layers)):
+        for layer in range(layers):
+            h = f"{stack}h{layer}/"
+            for ln in ("ln_1/", "ln_2/"):
+                tensors.append(bf16_tensor(h + ln + "g", (g.width,), model.norm_gain[norm]))
+                tensors.append(bf16_tensor(h + ln + "b", (g.width,), model.norm_bias[norm]))
+                norm += 1
+            for op, name in enumerate(("attn/c_attn/w", "attn/c_proj/w", "mlp/c_fc/w", "mlp/c_proj/w")):
+                projection(h + name, first + 4 * layer + op, True)
+        tensors.append(bf16_tensor(stack + "ln_f/g", (g.width,), model.norm_gain[norm]))
+        tensors.append(bf16_tensor(stack + "ln_f/b", (g.width,), model.norm_bias[norm]))
+        norm += 1
+    stacked = 4 * (g.temporal_layers + g.codebook_layers)
+    tensors.append(bf16_tensor("codebook_decoder.wpe", (g.width, g.books), model.positions))
+    projection("cb_proj", stacked, False)
+    projection("codebook_decoder.cb_proj", stacked + 1, False)
+    projection("proj_f/w", stacked + 2, True)
+    tensors.append(bf16_tensor("rotary_embed", (g.head_width, g.context), model.rotations))
+    return tensors
+
+
+def dac_graph_names(synthesis: bool) -> tuple[list, list]:
+    """Tensor stems of a DAC graph's 30 convolutions and 29 Snake activations in
+    graph order (src/weights/pack_main.cpp:580-610)."""
+    prefix = "decoder.model." if synthesis else "encoder.block."
+    convolutions, activations = [prefix + "0"], []
+    for stage in range(4):
+        block = f"{prefix}{stage + 1}.block."
+        if synthesis:
+            activations.append(block + "0")
+            convolutions.append(block + "1")
+        for unit in range(3):
+            residual = f"{block}{unit + (2 if synthesis else 0)}.block."
+            activations += [residual + "0", residual + "2"]
+            convolutions += [residual + "1", residual + "3"]
+        if not synthesis:
+            activations.append(block + "3")
+            convolutions.append(block + "4")
+    activations.append(prefix + "5")
+    convolutions.append(prefix + "6")
+    return convolutions, activations
+
+
+def dac_source(dac: DacModel) -> list:
+    """A DacModel as the tensors of dac_*_q8.bin: per convolution weight_v (BF8 or
+    float32, as stored), weight_g, bias; per activation alpha; per codebook the
+    quantizer's codebook, in_proj and out_proj."""
+    tensors = []
+    for synthesis, convs, alphas in ((False, dac.analysis, dac.analysis_alpha),
+                                     (True, dac.synthesis, dac.synthesis_alpha)):
+        conv_names, act_names = dac_graph_names(synthesis)
+        for name, conv in zip(conv_names, convs):
+            if conv.bf8:
+                tensors.append(quantized_tensor(name + ".weight_v", conv.dims, conv.values, conv.scales, 32))
+            else:
+                tensors.append(f32_tensor(name + ".weight_v", conv.dims, conv.values))
+            tensors.append(f32_tensor(name + ".weight_g", (1, 1, conv.dims[2]), conv.gain))
+            tensors.append(f32_tensor(name + ".bias", (conv.bias.size,), conv.bias))
+        for name, alpha in zip(act_names, alphas):
+            tensors.append(f32_tensor(name + ".alpha", (alpha.size, 1, 1), alpha))
+    for book in range(len(dac.codebook)):
+        q = f"quantizer.quantizers.{book}."
+        tensors += [f32_tensor(q + "codebook.weight", (8, 1024), dac.codebook[book]),
+                    f32_tensor(q + "in_proj.weight_v", (1024, 1, 8), dac.in_v[book]),
+                    f32_tensor(q + "in_proj.weight_g", (1, 1, 8), dac.in_g[book]),
+                    f32_tensor(q + "in_proj.bias", (8,), dac.in_bias[book]),
+                    f32_tensor(q + "out_proj.weight_v", (8, 1, 1024), dac.out_v[book]),
+                    f32_tensor(q + "out_proj.weight_g", (1, 1, 1024), dac.out_g[book]),
+                    f32_tensor(q + "out_proj.bias", (1024,), dac.out_bias[book])]
+    return tensors
