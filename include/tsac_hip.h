@@ -333,6 +333,49 @@ int tsac_hip_model_create_from_source(const tsac_hip_source* transformer, const 
                                       const tsac_hip_limits* limits, tsac_hip_model** model);
 int tsac_hip_dac_create_from_source(const tsac_hip_source* dac, const tsac_hip_limits* limits, tsac_hip_dac** model);
 
+/* ---- the command-line codec: audio files, stream headers, options ----------- */
+
+/* pcm16_input (src/audio.cpp:19-38): raw little-endian 16-bit PCM of 1..127
+ * interleaved channels to float (1/32768 per step), an incomplete last frame
+ * dropped, frames padded with zeros to a multiple of 512. `samples` is
+ * library-allocated (release with tsac_hip_free), [frames][channels]. */
+int tsac_hip_pcm16_read(const uint8_t* bytes, size_t length, uint32_t channels, const tsac_hip_limits* limits,
+                        float** samples, size_t* frames);
+/* wave_input (src/audio.cpp:40-72): a RIFF/WAVE file of 16-bit PCM, 1..8
+ * channels at 44100 Hz, read like tsac_hip_pcm16_read from the data chunk to
+ * the end of the file. */
+int tsac_hip_wave_read(const uint8_t* bytes, size_t length, const tsac_hip_limits* limits, float** samples,
+                       size_t* frames, uint32_t* channels);
+/* pcm16_wave (src/audio.cpp:176-246): interleaved float PCM [frames][channels]
+ * to a 44100 Hz 16-bit WAVE file (library-allocated), each sample clamped
+ * after scaling by 32768 and rounded half to even; nonfinite samples fail. */
+int tsac_hip_wave_write(const float* samples, size_t frames, uint32_t channels, const tsac_hip_limits* limits,
+                        uint8_t** bytes, size_t* length);
+/* audio_header (src/common/audio_pipeline.hpp:13, src/common/audio_analyzer.cpp:78-108):
+ * the stream header tsac_hip_audio_encode writes for `frames` sample frames of
+ * `channels`-channel PCM under `options`. */
+int tsac_hip_audio_header(size_t frames, uint32_t channels, const tsac_hip_encode_options* options,
+                          const tsac_hip_limits* limits, tsac_hip_header* header);
+/* parse_header (src/format/container.hpp): the header of a stream. */
+int tsac_hip_parse_header(const uint8_t* stream, size_t length, const tsac_hip_limits* limits,
+                          tsac_hip_header* header);
+
+/* CliOptions (src/cli.hpp:6-15); input and output point into the arguments. */
+typedef struct tsac_hip_cli_options
+{
+    char command; /* 'c', 'd', 't', or 0 when help is set */
+    const char* input;
+    const char* output;
+    int32_t threads, quality, channels, batch;
+    uint32_t verbose;
+    uint8_t fast, separate, help, metal;
+} tsac_hip_cli_options;
+/* parse_cli (src/cli.cpp:7-129) over the arguments after the program name,
+ * each a NUL-terminated string. */
+int tsac_hip_cli_parse(size_t count, const char* const* arguments, tsac_hip_cli_options* options);
+/* cli_help (src/cli.cpp:131-155). */
+const char* tsac_hip_cli_help(void);
+
 /* ---- operators on device memory (hipStream_t passed as void*) -------------- */
 
 typedef struct tsac_hip_device_linear tsac_hip_device_linear;

@@ -488,6 +488,10 @@ class Reference(_Kernels, _DspKernels):
         lib.ref_source_parse.argtypes = [u8p, sz, C.c_uint64, C.c_uint64, C.POINTER(sz)]
         lib.ref_source_dequantize.argtypes = [u8p, sz, C.c_char_p, f32p, sz]
         lib.ref_source_configs.argtypes = [u8p, sz] + [C.POINTER(C.c_uint)] * 3
+        lib.ref_pcm16_input.argtypes = [u8p, sz, C.c_uint, f32p, sz, C.POINTER(sz)]
+        lib.ref_wave_input.argtypes = [u8p, sz, f32p, sz, C.POINTER(sz), C.POINTER(C.c_uint)]
+        lib.ref_pcm16_wave.argtypes = [f32p, sz, C.c_uint, C.c_uint64, u8p, sz, C.POINTER(sz)]
+        lib.ref_parse_cli.argtypes = [sz, C.POINTER(C.c_char_p), C.POINTER(C.c_longlong)]
 
     @staticmethod
     def available() -> bool:
@@ -507,6 +511,48 @@ class Reference(_Kernels, _DspKernels):
         self._check(self.lib.ref_source_dequantize(ptr(b, C.c_uint8), len(data), name.encode(), ptr(out, C.c_float),
                                                    out.size))
         return out[:count]
+
+    # The command-line codec's audio files and options (src/audio.cpp, src/cli.cpp).
+    def pcm16_input(self, data: bytes, channels: int):
+        """Float PCM [frames][channels], or None when the reference rejects it."""
+        b = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+        out = np.zeros(max(1, (len(data) // max(2 * channels, 1) + 512) * max(channels, 1)), np.float32)
+        frames = sz()
+        if self.lib.ref_pcm16_input(ptr(b, C.c_uint8), len(data), channels, ptr(out, C.c_float), out.size,
+                                    C.byref(frames)):
+            return None
+        return out[:frames.value * channels].reshape(frames.value, channels)
+
+    def wave_input(self, data: bytes):
+        b = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+        out = np.zeros(len(data) + 512 * 8, np.float32)
+        frames, channels = sz(), C.c_uint()
+        if self.lib.ref_wave_input(ptr(b, C.c_uint8), len(data), ptr(out, C.c_float), out.size, C.byref(frames),
+                                   C.byref(channels)):
+            return None
+        return out[:frames.value * channels.value].reshape(frames.value, channels.value)
+
+    def pcm16_wave(self, samples, pcm_bytes: int = 0):
+        pcm = np.ascontiguousarray(samples, np.float32)
+        frames, channels = pcm.shape
+        out = np.zeros(44 + 2 * pcm.size, np.uint8)
+        n = sz()
+        if self.lib.ref_pcm16_wave(ptr(pcm, C.c_float), frames, channels, pcm_bytes, ptr(out, C.c_uint8), out.size,
+                                   C.byref(n)):
+            return None
+        return out[:n.value].tobytes()
+
+    def parse_cli(self, arguments: list):
+        """None when the reference rejects the arguments, else its options with
+        input/output as the indices of those arguments."""
+        encoded = [a.encode() for a in arguments]
+        argv = (C.c_char_p * max(len(encoded), 1))(*encoded)
+        fields = (C.c_longlong * 12)()
+        if self.lib.ref_parse_cli(len(encoded), argv, fields):
+            return None
+        names = ("command", "threads", "quality", "channels", "batch", "verbose", "fast", "separate", "help",
+                 "metal", "input", "output")
+        return dict(zip(names, list(fields)))
 
     def source_configs(self, data: bytes) -> tuple:
         """(channels, codebooks) of dac_config and codebooks of transformer_config,

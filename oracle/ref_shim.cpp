@@ -21,6 +21,8 @@
 #include "weights/normalization.hpp"
 #include "weights/preparation.hpp"
 #include "weights/source_model.hpp"
+#include "audio.hpp"
+#include "cli.hpp"
 
 #include "tsac_oracle.h"
 
@@ -669,6 +671,83 @@ int ref_source_configs(const std::uint8_t* bytes, std::size_t length, unsigned* 
             catch (const std::exception&)
             {
             }
+        });
+}
+
+// The command-line codec's audio files and options (src/audio.cpp, src/cli.cpp).
+int ref_pcm16_input(const std::uint8_t* bytes, std::size_t length, unsigned channels, float* out,
+                    std::size_t capacity, std::size_t* frames)
+{
+    return guarded(
+        [&]
+        {
+            const auto signal = pcm16_input(ByteView(bytes, length), channels);
+            detail::require(signal.values.size() <= capacity, "capacity");
+            std::memcpy(out, signal.values.data(), signal.values.size() * sizeof(float));
+            *frames = signal.shape.frames;
+        });
+}
+
+int ref_wave_input(const std::uint8_t* bytes, std::size_t length, float* out, std::size_t capacity,
+                   std::size_t* frames, unsigned* channels)
+{
+    return guarded(
+        [&]
+        {
+            const auto signal = wave_input(ByteView(bytes, length));
+            detail::require(signal.values.size() <= capacity, "capacity");
+            std::memcpy(out, signal.values.data(), signal.values.size() * sizeof(float));
+            *frames = signal.shape.frames;
+            *channels = unsigned(signal.shape.channels);
+        });
+}
+
+int ref_pcm16_wave(const float* samples, std::size_t frames, unsigned channels, std::uint64_t pcm_bytes,
+                   std::uint8_t* out, std::size_t capacity, std::size_t* length)
+{
+    return guarded(
+        [&]
+        {
+            Limits limits;
+            if (pcm_bytes)
+            {
+                limits.pcm_bytes = pcm_bytes;
+            }
+            const auto bytes = pcm16_wave(std::span(samples, frames * channels), {channels, frames, 1}, limits);
+            detail::require(bytes.size() <= capacity, "capacity");
+            std::memcpy(out, bytes.data(), bytes.size());
+            *length = bytes.size();
+        });
+}
+
+// parse_cli: fields [command, threads, quality, channels, batch, verbose, fast,
+// separate, help, metal, input index, output index] (-1 for an absent path).
+int ref_parse_cli(std::size_t count, const char* const* arguments, long long* fields)
+{
+    return guarded(
+        [&]
+        {
+            std::vector<std::string_view> args(arguments, arguments + count);
+            const auto o = parse_cli(args);
+            const auto index = [&](const std::filesystem::path& p) -> long long
+            {
+                if (p.empty())
+                {
+                    return -1;
+                }
+                for (std::size_t i = 0; i < count; ++i)
+                {
+                    if (p == std::filesystem::path(arguments[i]))
+                    {
+                        return (long long)i;
+                    }
+                }
+                return -2;
+            };
+            const long long values[12] = {o.command, o.threads, o.quality, o.channels, o.batch, o.verbose,
+                                          o.fast,    o.separate, o.help,  o.metal,    index(o.input),
+                                          index(o.output)};
+            std::memcpy(fields, values, sizeof values);
         });
 }
 }

@@ -4,6 +4,7 @@
 #include "audio.hpp"
 #include "runtime.hpp"
 #include "source.hpp"
+#include "wave.hpp"
 
 #include <cstdlib>
 #include <cstring>
@@ -517,6 +518,116 @@ int tsac_hip_dac_create_from_source(const tsac_hip_source* dac, const tsac_hip_l
     }
     tsac_hip_prepared_dac_destroy(prepared);
     return status;
+}
+
+int tsac_hip_pcm16_read(const uint8_t* bytes, size_t length, uint32_t channels, const tsac_hip_limits* limits,
+                        float** samples, size_t* frames)
+{
+    return guarded(
+        [&]
+        {
+            require((bytes || !length) && samples && frames, "missing argument");
+            const Pcm pcm = pcm16_input(bytes, length, channels, limits_of(limits));
+            *samples = copy_out(pcm.samples);
+            *frames = pcm.frames;
+        });
+}
+
+int tsac_hip_wave_read(const uint8_t* bytes, size_t length, const tsac_hip_limits* limits, float** samples,
+                       size_t* frames, uint32_t* channels)
+{
+    return guarded(
+        [&]
+        {
+            require((bytes || !length) && samples && frames && channels, "missing argument");
+            const Pcm pcm = wave_input(bytes, length, limits_of(limits));
+            *samples = copy_out(pcm.samples);
+            *frames = pcm.frames;
+            *channels = pcm.channels;
+        });
+}
+
+int tsac_hip_wave_write(const float* samples, size_t frames, uint32_t channels, const tsac_hip_limits* limits,
+                        uint8_t** bytes, size_t* length)
+{
+    return guarded(
+        [&]
+        {
+            require((samples || !frames) && bytes && length, "missing argument");
+            const auto wave = pcm16_wave(samples, frames, channels, limits_of(limits));
+            *bytes = copy_out(wave);
+            *length = wave.size();
+        });
+}
+
+int tsac_hip_audio_header(size_t frames, uint32_t channels, const tsac_hip_encode_options* options,
+                          const tsac_hip_limits* limits, tsac_hip_header* header)
+{
+    return guarded(
+        [&]
+        {
+            require(header, "missing argument");
+            EncodeOptions o;
+            if (options)
+            {
+                o.method = options->method;
+                o.codebooks = options->codebooks;
+                o.separate_channels = options->separate_channels != 0;
+                if (options->entropy_batch)
+                {
+                    o.entropy_batch = options->entropy_batch;
+                }
+            }
+            const Header h = audio_header(frames, channels, o, limits_of(limits));
+            *header = tsac_hip_header{h.method, h.groups, h.model_channels, h.codebooks, h.frames, h.batch};
+        });
+}
+
+int tsac_hip_parse_header(const uint8_t* stream, size_t length, const tsac_hip_limits* limits,
+                          tsac_hip_header* header)
+{
+    return guarded(
+        [&]
+        {
+            require((stream || !length) && header, "missing argument");
+            const Header h = parse_header(stream, length, limits_of(limits));
+            *header = tsac_hip_header{h.method, h.groups, h.model_channels, h.codebooks, h.frames, h.batch};
+        });
+}
+
+int tsac_hip_cli_parse(size_t count, const char* const* arguments, tsac_hip_cli_options* options)
+{
+    return guarded(
+        [&]
+        {
+            require((arguments || !count) && options, "missing argument");
+            std::vector<std::string_view> args;
+            for (size_t i = 0; i < count; ++i)
+            {
+                require(arguments[i] != nullptr, "missing argument");
+                args.emplace_back(arguments[i]);
+            }
+            const CliOptions o = parse_cli(args);
+            *options = tsac_hip_cli_options{};
+            options->command = o.command;
+            // Views of whole arguments, so their data is NUL-terminated.
+            options->input = o.input.empty() ? nullptr : o.input.data();
+            options->output = o.output.empty() ? nullptr : o.output.data();
+            options->threads = o.threads;
+            options->quality = o.quality;
+            options->channels = o.channels;
+            options->batch = o.batch;
+            options->verbose = o.verbose;
+            options->fast = o.fast;
+            options->separate = o.separate;
+            options->help = o.help;
+            options->metal = o.metal;
+        });
+}
+
+const char* tsac_hip_cli_help(void)
+{
+    return cli_help().data();
 }
 
 int tsac_hip_prepare_rvq(const float* codebook, const float* in_v, const float* in_g, const float* out_v,

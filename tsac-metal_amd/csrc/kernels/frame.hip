@@ -2362,9 +2362,20 @@ template <int VW, int VF, int VL, int HW> void launch_frame(const FrameArgs& a, 
     // same grid measured ~20 us less per step on an otherwise idle device, but
     // two concurrent sessions could then each hold part of the device and wait
     // on workgroups that cannot be placed.
-    check_hip(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(frame_kernel<VW, VF, VL, HW>), dim3(grid),
-                                         dim3(frame_threads), params, 0, stream),
-              "frame step launch");
+    hipError_t status = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(frame_kernel<VW, VF, VL, HW>),
+                                                   dim3(grid), dim3(frame_threads), params, 0, stream);
+    if (status == hipErrorIllegalState)
+    {
+        // The device's cooperative-launch resources belong to one process at a
+        // time, and another process holds them. A plain launch of the same
+        // grid is co-resident on an otherwise idle device; every wait of the
+        // kernel is bounded, so where it is not, the step ends with the
+        // "stalled" error instead of hanging.
+        (void)hipGetLastError();
+        status = hipLaunchKernel(reinterpret_cast<const void*>(frame_kernel<VW, VF, VL, HW>), dim3(grid),
+                                 dim3(frame_threads), params, 0, stream);
+    }
+    check_hip(status, "frame step launch");
 }
 } // namespace
 

@@ -39,6 +39,8 @@ EXPORTS = (
     "tsac_hip_source_dequantize", "tsac_hip_source_dac_config", "tsac_hip_source_transformer_config",
     "tsac_hip_prepare_transformer", "tsac_hip_prepared_transformer_destroy", "tsac_hip_prepare_dac",
     "tsac_hip_prepared_dac_destroy", "tsac_hip_model_create_from_source", "tsac_hip_dac_create_from_source",
+    "tsac_hip_pcm16_read", "tsac_hip_wave_read", "tsac_hip_wave_write", "tsac_hip_audio_header",
+    "tsac_hip_parse_header", "tsac_hip_cli_parse", "tsac_hip_cli_help",
 )
 
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_TILES = 0, 1, 2, 3
@@ -111,6 +113,12 @@ class SourceLimits(C.Structure):
 class SourceTensorInfo(C.Structure):
     _fields_ = [("name", C.c_char_p), ("storage", C.c_uint32), ("rank", C.c_uint32), ("dims", C.c_uint64 * 8),
                 ("elements", C.c_uint64)]
+
+
+class CliOptions(C.Structure):
+    _fields_ = [("command", C.c_char), ("input", C.c_char_p), ("output", C.c_char_p), ("threads", C.c_int32),
+                ("quality", C.c_int32), ("channels", C.c_int32), ("batch", C.c_int32), ("verbose", C.c_uint32),
+                ("fast", C.c_uint8), ("separate", C.c_uint8), ("help", C.c_uint8), ("metal", C.c_uint8)]
 
 
 class EncodeOptions(C.Structure):
@@ -191,6 +199,15 @@ def library() -> C.CDLL:
         lib.tsac_hip_prepared_dac_destroy.argtypes = [vp]
         lib.tsac_hip_model_create_from_source.argtypes = [vp, vp, C.POINTER(Limits), C.POINTER(vp)]
         lib.tsac_hip_dac_create_from_source.argtypes = [vp, C.POINTER(Limits), C.POINTER(vp)]
+        lib.tsac_hip_pcm16_read.argtypes = [u8p, sz, C.c_uint32, C.POINTER(Limits), C.POINTER(f32p), C.POINTER(sz)]
+        lib.tsac_hip_wave_read.argtypes = [u8p, sz, C.POINTER(Limits), C.POINTER(f32p), C.POINTER(sz),
+                                           C.POINTER(C.c_uint32)]
+        lib.tsac_hip_wave_write.argtypes = [f32p, sz, C.c_uint32, C.POINTER(Limits), C.POINTER(u8p), C.POINTER(sz)]
+        lib.tsac_hip_audio_header.argtypes = [sz, C.c_uint32, C.POINTER(EncodeOptions), C.POINTER(Limits),
+                                              C.POINTER(Header)]
+        lib.tsac_hip_parse_header.argtypes = [u8p, sz, C.POINTER(Limits), C.POINTER(Header)]
+        lib.tsac_hip_cli_parse.argtypes = [sz, C.POINTER(C.c_char_p), C.POINTER(CliOptions)]
+        lib.tsac_hip_cli_help.restype = C.c_char_p
         _lib = lib
     return _lib
 
@@ -298,6 +315,75 @@ class SourceFile:
         books = C.c_uint32()
         check(library().tsac_hip_source_transformer_config(self.handle, C.byref(books)))
         return books.value
+
+
+def _bytes_arg(data: bytes):
+    return np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+
+
+def pcm16_read(data: bytes, channels: int, limits: Limits | None = None) -> np.ndarray:
+    """tsac_hip_pcm16_read: float PCM [frames][channels], padded to 512 frames."""
+    b, out, frames = _bytes_arg(data), f32p(), sz()
+    check(library().tsac_hip_pcm16_read(_ptr(b, C.c_uint8), len(data), channels, C.byref(limits) if limits else None,
+                                        C.byref(out), C.byref(frames)))
+    pcm = np.ctypeslib.as_array(out, shape=(frames.value * channels,)).copy() if frames.value else np.zeros(0, np.float32)
+    library().tsac_hip_free(out)
+    return pcm.reshape(frames.value, channels)
+
+
+def wave_read(data: bytes, limits: Limits | None = None) -> np.ndarray:
+    """tsac_hip_wave_read: float PCM [frames][channels] of a 44100 Hz 16-bit WAVE file."""
+    b, out, frames, channels = _bytes_arg(data), f32p(), sz(), C.c_uint32()
+    check(library().tsac_hip_wave_read(_ptr(b, C.c_uint8), len(data), C.byref(limits) if limits else None,
+                                       C.byref(out), C.byref(frames), C.byref(channels)))
+    count = frames.value * channels.value
+    pcm = np.ctypeslib.as_array(out, shape=(count,)).copy() if count else np.zeros(0, np.float32)
+    library().tsac_hip_free(out)
+    return pcm.reshape(frames.value, channels.value)
+
+
+def wave_write(samples: np.ndarray, limits: Limits | None = None) -> bytes:
+    """tsac_hip_wave_write of float PCM [frames][channels]."""
+    pcm = np.ascontiguousarray(samples, np.float32)
+    frames, channels = pcm.shape
+    out, n = u8p(), sz()
+    check(library().tsac_hip_wave_write(_ptr(pcm, C.c_float) if pcm.size else None, frames, channels,
+                                        C.byref(limits) if limits else None, C.byref(out), C.byref(n)))
+    data = C.string_at(out, n.value)
+    library().tsac_hip_free(out)
+    return data
+
+
+def audio_header(frames: int, channels: int, method=1, codebooks=0, separate_channels=False, entropy_batch=0,
+                 limits: Limits | None = None) -> Header:
+    options = EncodeOptions(method, codebooks, int(separate_channels), entropy_batch)
+    h = Header()
+    check(library().tsac_hip_audio_header(frames, channels, C.byref(options), C.byref(limits) if limits else None,
+                                          C.byref(h)))
+    return h
+
+
+def parse_header(stream: bytes, limits: Limits | None = None) -> Header:
+    b, h = _bytes_arg(stream), Header()
+    check(library().tsac_hip_parse_header(_ptr(b, C.c_uint8), len(stream), C.byref(limits) if limits else None,
+                                          C.byref(h)))
+    return h
+
+
+def cli_parse(arguments: list) -> dict:
+    """tsac_hip_cli_parse of the arguments after the program name."""
+    encoded = [a.encode() for a in arguments]
+    argv = (C.c_char_p * max(len(encoded), 1))(*encoded)
+    o = CliOptions()
+    check(library().tsac_hip_cli_parse(len(encoded), argv, C.byref(o)))
+    return {"command": o.command.decode() if o.command != b"\0" else "", "input": o.input and o.input.decode(),
+            "output": o.output and o.output.decode(), "threads": o.threads, "quality": o.quality,
+            "channels": o.channels, "batch": o.batch, "verbose": o.verbose, "fast": bool(o.fast),
+            "separate": bool(o.separate), "help": bool(o.help), "metal": bool(o.metal)}
+
+
+def cli_help() -> str:
+    return library().tsac_hip_cli_help().decode()
 
 
 def prepare_transformer(transformer: SourceFile, dac: SourceFile):
