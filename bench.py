@@ -325,32 +325,46 @@ def attention_rates(torch, native, lengths=(256, 1290, 2580), batch=3, heads=16,
         torch.cuda.synchronize()
         prefill_s = start_e.elapsed_time(stop_e) / 1000 / reps
         flops = batch * heads * 4 * head_width * T * (T + 1) / 2
-        # Decode: the last position's query over the T cached keys/values.
-        keys = qkv[:, width:2 * width].contiguous()
-        values = qkv[:, 2 * width:].contiguous()
+        # Decode: the last position's query over the T cached keys/values,
+        # rotating over copies of the caches that together exceed 1 GiB so
+        # every launch reads its keys and values from HBM, not from cache.
+        kv_bytes = batch * 2 * T * width * 2
+        copies = -(-(1 << 30) // kv_bytes)
+        keys = qkv[:, width:2 * width].contiguous().unsqueeze(0).repeat(copies, 1, 1)
+        values = qkv[:, 2 * width:].contiguous().unsqueeze(0).repeat(copies, 1, 1)
         query = qkv.view(batch, T, 3 * width)[:, T - 1, :width].contiguous()
         dout = torch.empty((batch, width), dtype=torch.int16, device="cuda")
-        step = lambda: native.attention(query, keys, values, T * width, batch, T, heads, head_width, scale,
-                                        False, dout)
-        step()
+        # The C ABI called with pointers prepared up front, as a C caller would.
+        lib, vp = native.library(), native.vp
+        pointers = [(vp(keys[c].data_ptr()), vp(values[c].data_ptr())) for c in range(copies)]
+        stream = vp(torch.cuda.current_stream().cuda_stream)
+        q_pointer, out_pointer = vp(query.data_ptr()), vp(dout.data_ptr())
+
+        def step(c):
+            native.check(lib.tsac_hip_attention(q_pointer, *pointers[c], T * width, batch, T, heads, head_width,
+                                                scale, 0, out_pointer, stream))
+        for c in range(copies):
+            step(c)
+        reps = max(50, copies)
+        torch.cuda.synchronize()
         start_e.record()
-        reps = 50
-        for _ in range(reps):
-            step()
+        for i in range(reps):
+            step(i % copies)
         stop_e.record()
         torch.cuda.synchronize()
         decode_s = start_e.elapsed_time(stop_e) / 1000 / reps
-        kv_bytes = batch * 2 * T * width * 2
         rows.append({"T": T, "prefill_us": round(prefill_s * 1e6, 1),
                      "prefill_TFLOPs": round(flops / prefill_s / 1e12, 2),
                      "prefill_frac_fp32_valu": round(flops / prefill_s / 1e12 / FP32_PEAK_TFLOPS, 4),
-                     "decode_us": round(decode_s * 1e6, 2), "decode_GBps": round(kv_bytes / decode_s / 1e9, 1),
+                     "decode_us": round(decode_s * 1e6, 2), "decode_cache_copies": copies,
+                     "decode_GBps": round(kv_bytes / decode_s / 1e9, 1),
                      "decode_frac_hbm": round(kv_bytes / decode_s / 1e9 / HBM_PEAK_GBPS, 4)})
         del qkv, keys, values, out
     torch.cuda.empty_cache()
     return {"heads": heads, "head_width": head_width, "batch": batch, "rows": rows,
             "flops": "batch*heads*4*head_width*T*(T+1)/2 (causal prefill)",
-            "bytes": "batch*2*T*heads*head_width*2 (decode: the BF16 key and value cache)"}
+            "bytes": "batch*2*T*heads*head_width*2 (decode: the BF16 key and value cache, rotated over "
+                     "copies totalling over 1 GiB)"}
 
 
 def frame_roofline(geometry, frames, batch, step_s):

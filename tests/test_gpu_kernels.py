@@ -457,6 +457,46 @@ def test_attention_decode_batched_sequences(torch, native, oracle):
         assert np.array_equal(host(out)[lane], expected)
 
 
+def test_attention_decode_split_scratch_and_capture(torch, native, oracle):
+    """Histories split over several workgroups per (sequence, head), in shapes
+    that grow, shrink and grow the per-stream scratch in turn (its arrival
+    counters must be zero again after every launch), then one such call
+    captured in a graph and replayed with eager calls on the same stream
+    between the replays."""
+    rng = np.random.default_rng(31)
+
+    def case(sequences, heads, hw, frames):
+        w = heads * hw
+        q = bf16_bits(rng.standard_normal((sequences, w)).astype(np.float32) * 2)
+        k = bf16_bits(rng.standard_normal((sequences, frames, w)).astype(np.float32) * 2)
+        v = bf16_bits(rng.standard_normal((sequences, frames, w)).astype(np.float32))
+        scale = np.float32(1 / np.sqrt(hw))
+        expected = np.stack([oracle.attention(q[s], k[s], v[s], heads, hw, scale, False) for s in range(sequences)])
+        args = (dev(torch, q), dev(torch, k), dev(torch, v), frames * w, sequences, frames, heads, hw, scale, False)
+        return args, expected
+
+    shapes = [(1, 2, 64, 1290), (3, 16, 64, 2580), (1, 2, 64, 700), (2, 4, 128, 5000), (3, 16, 64, 2580),
+              (2, 1, 128, 257)]
+    cases = [case(*shape) for shape in shapes]
+    for shape, (args, expected) in zip(shapes, cases):
+        out = empty(torch, expected.shape, torch.int16)
+        native.attention(*args, out)
+        assert np.array_equal(host(out), expected), shape
+    (args, expected), (other, other_expected) = cases[1], cases[3]
+    out = empty(torch, expected.shape, torch.int16)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        native.attention(*args, out)
+    for replay in range(3):
+        out.zero_()
+        other_out = empty(torch, other_expected.shape, torch.int16)
+        native.attention(*other, other_out)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), expected), replay
+        assert np.array_equal(host(other_out), other_expected), replay
+
+
 @pytest.mark.parametrize("heads,hw,rotary", [(4, 128, True), (4, 128, False), (16, 64, True)])
 def test_attention_causal_matches_oracle(torch, native, oracle, heads, hw, rotary):
     """Every query of several causal sequences (one with a replay prefix) against

@@ -6,9 +6,13 @@
 #include "source.hpp"
 #include "wave.hpp"
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <new>
+#include <utility>
 
 using namespace tsac_hip;
 
@@ -131,6 +135,59 @@ struct AsyncScratch
         (void)hipFreeAsync(pointer, stream);
     }
 };
+
+// Decode-attention scratch kept per (device, stream): arrival counters at
+// the start, block records after them. The kernel leaves its counters at
+// zero, so they are cleared when allocated and then serve every later call on
+// that stream, which runs after the earlier ones. Allocation, clearing and
+// the release of an outgrown buffer are all ordered on the stream.
+class DecodeScratch
+{
+  public:
+    struct View
+    {
+        unsigned* arrivals;
+        float* partial;
+    };
+
+    View get(hipStream_t stream, std::size_t counters, std::size_t floats)
+    {
+        int device = 0;
+        check_hip(hipGetDevice(&device), "hipGetDevice");
+        const std::lock_guard<std::mutex> lock(mutex_);
+        Entry& e = entries_[{device, stream}];
+        if (e.counters < counters || e.floats < floats)
+        {
+            const Entry grown{nullptr, std::max(e.counters, (counters + 63) / 64 * 64), std::max(e.floats, floats)};
+            if (e.pointer)
+            {
+                check_hip(hipFreeAsync(e.pointer, stream), "hipFreeAsync");
+                e = Entry{};
+            }
+            check_hip(hipMallocAsync(&e.pointer, grown.counters * 4 + grown.floats * 4, stream), "hipMallocAsync");
+            e.counters = grown.counters;
+            e.floats = grown.floats;
+            clear_arrival_counters(static_cast<unsigned*>(e.pointer), e.counters, stream);
+        }
+        return {static_cast<unsigned*>(e.pointer), reinterpret_cast<float*>(static_cast<unsigned*>(e.pointer) + e.counters)};
+    }
+
+  private:
+    struct Entry
+    {
+        void* pointer = nullptr;
+        std::size_t counters = 0;
+        std::size_t floats = 0;
+    };
+    std::mutex mutex_;
+    std::map<std::pair<int, hipStream_t>, Entry> entries_;
+};
+
+DecodeScratch& decode_scratch()
+{
+    static DecodeScratch* cache = new DecodeScratch; // outlives every static destructor
+    return *cache;
+}
 
 tsac_hip_position position_of(const Position& p)
 {
@@ -925,15 +982,29 @@ int tsac_hip_attention(const uint16_t* query, const uint16_t* keys, const uint16
         {
             const auto s = as_stream(stream);
             const std::size_t floats = decode_partial_floats(sequences, heads, head_width, time);
+            const std::size_t counters = decode_arrival_counters(sequences, heads, time);
             if (floats == 0)
             {
                 attention_decode(query, keys, values, sequence_stride, sequences, time, heads, head_width, scale,
-                                 prefill != 0, nullptr, out, s);
+                                 prefill != 0, nullptr, nullptr, out, s);
                 return;
             }
-            AsyncScratch scratch(floats * 4, s);
-            attention_decode(query, keys, values, sequence_stride, sequences, time, heads, head_width,
-                             scale, prefill != 0, static_cast<float*>(scratch.pointer), out, s);
+            hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+            check_hip(hipStreamIsCapturing(s, &capture), "hipStreamIsCapturing");
+            if (capture != hipStreamCaptureStatusNone)
+            {
+                // A captured call gets scratch of its own, cleared by a kernel
+                // inside the graph.
+                AsyncScratch scratch(counters * 4 + floats * 4, s);
+                const auto arrivals = static_cast<unsigned*>(scratch.pointer);
+                clear_arrival_counters(arrivals, counters, s);
+                attention_decode(query, keys, values, sequence_stride, sequences, time, heads, head_width,
+                                 scale, prefill != 0, reinterpret_cast<float*>(arrivals + counters), arrivals, out, s);
+                return;
+            }
+            const DecodeScratch::View scratch = decode_scratch().get(s, counters, floats);
+            attention_decode(query, keys, values, sequence_stride, sequences, time, heads, head_width, scale,
+                             prefill != 0, scratch.partial, scratch.arrivals, out, s);
         });
 }
 

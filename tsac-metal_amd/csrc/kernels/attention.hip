@@ -7,10 +7,9 @@
 //   * blocks merged in ascending order with the online-softmax recurrence.
 // Matrix cores would reorder those sums, so everything runs on the VALU.
 //
-// Decode (one query per sequence): one workgroup per (sequence, head) computes
-// the block partials into LDS and merges them in order; histories beyond what
-// its LDS holds use one wavefront per (sequence, head, block) and a second
-// launch for the merge.
+// Decode (one query per sequence): each (sequence, head)'s 64-key blocks are
+// spread over several workgroups of one launch, one wave per block; the last
+// workgroup to arrive merges the block records in ascending order.
 // Prefill (encode, all queries known): one workgroup per (sequence, head,
 // 64-query tile) walks the causal key blocks with Q/K/V tiles in LDS.
 #include "attention.hpp"
@@ -64,160 +63,158 @@ __global__ void append_kernel(const uint16_t* __restrict__ qkv, int rows, int wi
     }
 }
 
-// One wavefront per (sequence, head, 64-key block). Partial record layout:
-// [max, block sum, value sums[head_width]].
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Waves per decode workgroup; each wave computes one 64-key block's record.
+constexpr int decode_waves = 4;
+
+// The lane's value, or -inf where DPP control Ctrl gives it no source lane
+// (or its row or bank is masked out).
+template <int Ctrl, int RowMask = 0xf, int BankMask = 0xf> __device__ __forceinline__ float dpp_or_minus_inf(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-__builtin_inff()), __float_as_int(v), Ctrl,
+                                                      RowMask, BankMask, false));
+}
+
+// Inclusive scan of the running maximum over the wave's lanes with the merge
+// recurrence's own update (an earlier value stays unless it is smaller), on
+// DPP row shifts and row broadcasts: within each row of 16 lanes by shifts of
+// 1, 2, 4 and 8, then lane 15 into rows 1 and 3, then lane 31 into rows 2 and
+// 3. Associative for values without NaN.
+__device__ __forceinline__ float running_max_scan(float x)
+{
+    const auto keep = [](float earlier, float later) { return earlier < later ? later : earlier; };
+    x = keep(dpp_or_minus_inf<0x111>(x), x);
+    x = keep(dpp_or_minus_inf<0x112>(x), x);
+    x = keep(dpp_or_minus_inf<0x114>(x), x);
+    x = keep(dpp_or_minus_inf<0x118>(x), x);
+    x = keep(dpp_or_minus_inf<0x142, 0xa>(x), x);
+    x = keep(dpp_or_minus_inf<0x143, 0xc>(x), x);
+    return x;
+}
+
+// The previous lane's value (wave shift right by one); lane 0 gets `first`.
+__device__ __forceinline__ float previous_lane(float v, float first)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(first), __float_as_int(v), 0x138, 0xf, 0xf, false));
+}
+
+// Workgroups per (sequence, head) for a history of `blocks` key blocks.
+constexpr int decode_splits(int blocks)
+{
+    return (blocks + decode_waves - 1) / decode_waves;
+}
+
+// One query per (sequence, head) over its `time` cached keys, split over
+// decode_splits(blocks) workgroups of decode_waves waves: wave w of split s
+// computes the record [max, block sum, value sums[HW]] of block
+// s * decode_waves + w. With one split the records stay in LDS; otherwise
+// they go to `partial` ([sequence * heads + head][blocks][2 + HW]) and each
+// workgroup counts its arrival in `arrivals[sequence * heads + head]` (zero
+// on entry, zero again on exit): the last to arrive copies every record into
+// LDS and merges them in ascending block order, so the counter only hands
+// the merge over and the summation order is the single-workgroup one.
+//
+// A block's key and value rows are read whole (16 bytes per lane, so a load
+// covers 64 / (HW / 8) rows) and pass through LDS: each lane takes its key
+// row, then its value column.
+//
+// The merge's running maxima are a scan with the recurrence's own update
+// (keep the running maximum unless it is smaller: the first of equal values
+// wins), which is associative without NaNs, so every block's factors come at
+// once and only the two-operation total/numerator recurrence stays
+// sequential; with a NaN maximum the merge runs the plain loop.
 template <int HW>
-__global__ __launch_bounds__(64) void decode_blocks_kernel(
+__global__ __launch_bounds__(decode_waves * 64) void decode_attention_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ keys,
     const uint16_t* __restrict__ values, std::size_t sequence_stride, int width, int time,
-    int heads, float scale, int round_values, int max_blocks, float* __restrict__ partial)
+    int heads, float scale, int round_values, float* __restrict__ partial, unsigned* __restrict__ arrivals,
+    uint16_t* __restrict__ out)
 {
-    const int sequence = blockIdx.x / heads, head = blockIdx.x % heads;
-    const int block = blockIdx.y;
-    const int start = block * 64;
-    if (start >= time)
-    {
-        return;
-    }
-    const int lane = threadIdx.x;
-    const int count = time - start < 64 ? time - start : 64;
-    const uint16_t* q = query + std::size_t(sequence) * width + head * HW;
+    constexpr int chunks = HW / 8;            // 16-byte chunks per row
+    constexpr int rows_per_load = 64 / chunks;
+    extern __shared__ float records[];        // [blocks][2 + HW]
+    __shared__ uint4 staged[decode_waves][64 * chunks]; // each wave's key rows, then value rows
+    __shared__ float weights[decode_waves][64];
+    __shared__ float4 factors[64]; // the merge's per-block (old scale, new scale, block sum)
+    __shared__ int merging;
+    const int blocks = (time + 63) / 64;
+    const int splits = decode_splits(blocks);
+    const int pair = blockIdx.x / splits, split = blockIdx.x % splits;
+    const int sequence = pair / heads, head = pair % heads;
+    const int lane = threadIdx.x % wave, warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
     const uint16_t* k = keys + std::size_t(sequence) * sequence_stride + head * HW;
     const uint16_t* v = values + std::size_t(sequence) * sequence_stride + head * HW;
-    __shared__ float qf[HW];
-    __shared__ float weights[64];
-    for (int j = lane; j < HW; j += 64)
+    // Lane l sums value column l (HW = 64) or columns 2l and 2l + 1 (HW = 128).
+    constexpr int per_lane = HW / 64;
+    float* const shared_records = partial + std::size_t(pair) * blocks * (2 + HW);
+    const int block = split * decode_waves + warp;
+    if (block < blocks)
     {
-        qf[j] = bf16_to_float(q[j]);
-    }
-    __syncthreads();
-    float score = -__builtin_inff();
-    if (lane < count)
-    {
-        const uint16_t* row = k + std::size_t(start + lane) * width;
+        const int start = block * 64;
+        const int count = time - start < 64 ? time - start : 64;
+        // The block's key rows and value rows, whole rows at a time (16 bytes
+        // per lane, so a load covers 64 / (HW / 8) rows), all requested
+        // before any is used. Rows past the history lie beyond the buffers'
+        // ends and read zero; their scores are dropped and their values not
+        // used. The row offset goes in the range-checked vector offset (the
+        // scalar offset is not checked).
+        const __amdgpu_buffer_rsrc_t key_rows =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(k), 0, time * width * 2, 0x00020000);
+        const __amdgpu_buffer_rsrc_t value_rows =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(v), 0, time * width * 2, 0x00020000);
+        const int lane_offset = (lane / chunks) * width * 2 + (lane % chunks) * 16;
+        uint4 key_data[chunks], rows[chunks];
+#pragma unroll
+        for (int i = 0; i < chunks; ++i)
+        {
+            const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(
+                key_rows, lane_offset + (start + i * rows_per_load) * width * 2, 0, 0);
+            key_data[i] = make_uint4(r.x, r.y, r.z, r.w);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < chunks; ++i)
+        {
+            const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(
+                value_rows, lane_offset + (start + i * rows_per_load) * width * 2, 0, 0);
+            rows[i] = make_uint4(r.x, r.y, r.z, r.w);
+        }
+        __builtin_amdgcn_sched_barrier(0); // every load issued before the first wait
+        // Keys through LDS to one row per lane; chunk c of row r is kept at
+        // r * chunks + (c ^ (r % 8)), so neither the row-wise writes nor the
+        // lane-per-row reads meet in a bank.
+#pragma unroll
+        for (int i = 0; i < chunks; ++i)
+        {
+            const int r = i * rows_per_load + lane / chunks, c = lane % chunks;
+            staged[warp][r * chunks + (c ^ (r & 7))] = key_data[i];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
+        __builtin_amdgcn_wave_barrier();
+        uint4 key[chunks];
+#pragma unroll
+        for (int c = 0; c < chunks; ++c)
+        {
+            key[c] = staged[warp][lane * chunks + (c ^ (lane & 7))];
+        }
+        // The query, uniform over the workgroup, in scalar registers.
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(query + std::size_t(sequence) * width + head * HW);
         float dot = 0.0f;
 #pragma unroll
-        for (int c = 0; c < HW / 8; ++c)
+        for (int c = 0; c < chunks; ++c)
         {
-            const uint4 u = reinterpret_cast<const uint4*>(row)[c];
+            const uint4 u = key[c];
             const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
             {
-                dot = __builtin_fmaf(qf[8 * c + 2 * i], bf16_to_float(uint16_t(w[i] & 0xffff)), dot);
-                dot = __builtin_fmaf(qf[8 * c + 2 * i + 1], bf16_to_float(uint16_t(w[i] >> 16)), dot);
+                const uint32_t pair_q = __builtin_amdgcn_readfirstlane(q[4 * c + i]);
+                dot = __builtin_fmaf(__uint_as_float(pair_q << 16), __uint_as_float(w[i] << 16), dot);
+                dot = __builtin_fmaf(__uint_as_float(pair_q & 0xffff0000u), __uint_as_float(w[i] & 0xffff0000u), dot);
             }
         }
-        score = dot * scale;
-    }
-    const float maximum = group_max<wave>(score);
-    float e = 0.0f;
-    if (lane < count)
-    {
-        const float shifted = score - maximum;
-        e = original_exp(shifted);
-    }
-    const float sum = tree_sum<wave>(e);
-    weights[lane] = e;
-    __syncthreads();
-    float* record = partial + (std::size_t(blockIdx.x) * max_blocks + block) * (2 + HW);
-    if (lane == 0)
-    {
-        record[0] = maximum;
-        record[1] = sum;
-    }
-    for (int j = lane; j < HW; j += 64)
-    {
-        float s = 0.0f;
-        for (int t = 0; t < count; ++t)
-        {
-            s = __builtin_fmaf(bf16_to_float(v[std::size_t(start + t) * width + j]), weights[t], s);
-        }
-        if (round_values)
-        {
-            s = round_bf16(s);
-        }
-        record[2 + j] = s;
-    }
-}
-
-// Waves per workgroup: 16 for 64-wide heads; 8 for 128-wide ones, whose key
-// rows and value words need twice the registers.
-template <int HW> constexpr int decode_waves = HW == 64 ? 16 : 8;
-constexpr int decode_lds_blocks = 256; // blocks whose records one workgroup's LDS holds
-
-// Records [max, block sum, value sums[HW]] of one (sequence, head) in LDS, wave
-// w computing blocks w, w + decode_waves<HW>, ...; then wave 0 merges them in
-// ascending order. The merge's running maxima are a scan with the recurrence's
-// own update (keep the running maximum unless it is smaller: the first of
-// equal values wins), which is associative without NaNs, so every block's
-// factors come at once and only the two-operation total/numerator recurrence
-// stays sequential; with a NaN maximum the merge runs the plain loop.
-template <int HW>
-__global__ __launch_bounds__(decode_waves<HW> * 64) void decode_attention_kernel(
-    const uint16_t* __restrict__ query, const uint16_t* __restrict__ keys,
-    const uint16_t* __restrict__ values, std::size_t sequence_stride, int width, int time,
-    int heads, float scale, int round_values, uint16_t* __restrict__ out)
-{
-    extern __shared__ float records[]; // [blocks][2 + HW]
-    __shared__ float qf[HW];
-    __shared__ float weights[decode_waves<HW>][64];
-    const int sequence = blockIdx.x / heads, head = blockIdx.x % heads;
-    const int lane = threadIdx.x % wave, warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
-    const int blocks = (time + 63) / 64;
-    const uint16_t* q = query + std::size_t(sequence) * width + head * HW;
-    const uint16_t* k = keys + std::size_t(sequence) * sequence_stride + head * HW;
-    const uint16_t* v = values + std::size_t(sequence) * sequence_stride + head * HW;
-    for (int j = threadIdx.x; j < HW; j += blockDim.x)
-    {
-        qf[j] = bf16_to_float(q[j]);
-    }
-    __syncthreads();
-    // Lane l sums value column l (HW = 64) or columns 2l and 2l + 1 (HW = 128).
-    constexpr int per_lane = HW / 64;
-    for (int block = warp; block < blocks; block += decode_waves<HW>)
-    {
-        const int start = block * 64;
-        const int count = time - start < 64 ? time - start : 64;
-        // This lane's key row, then every row's values, requested before any
-        // is used (rows past the history repeat its last row and are not
-        // used): a load under a per-row branch would be waited for on its own,
-        // and keys requested after the values would wait for all of them.
-        uint4 key[HW / 8];
-        {
-            const uint16_t* row = k + std::size_t(start + lane < time ? start + lane : time - 1) * width;
-#pragma unroll
-            for (int c = 0; c < HW / 8; ++c)
-            {
-                key[c] = reinterpret_cast<const uint4*>(row)[c];
-            }
-        }
-        uint32_t value[64];
-#pragma unroll
-        for (int t = 0; t < 64; ++t)
-        {
-            const int row = start + t < time ? start + t : time - 1;
-            const uint16_t* at = v + std::size_t(row) * width + per_lane * lane;
-            value[t] = per_lane == 2 ? *reinterpret_cast<const uint32_t*>(at) : uint32_t(*at);
-        }
-        float score = -__builtin_inff();
-        if (lane < count)
-        {
-            float dot = 0.0f;
-#pragma unroll
-            for (int c = 0; c < HW / 8; ++c)
-            {
-                const uint4 u = key[c];
-                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                {
-                    dot = __builtin_fmaf(qf[8 * c + 2 * i], bf16_to_float(uint16_t(w[i] & 0xffff)), dot);
-                    dot = __builtin_fmaf(qf[8 * c + 2 * i + 1], bf16_to_float(uint16_t(w[i] >> 16)), dot);
-                }
-            }
-            score = dot * scale;
-        }
+        const float score = lane < count ? dot * scale : -__builtin_inff();
         const float maximum = group_max<wave>(score);
         float e = 0.0f;
         if (lane < count)
@@ -226,112 +223,217 @@ __global__ __launch_bounds__(decode_waves<HW> * 64) void decode_attention_kernel
         }
         const float sum = tree_sum<wave>(e);
         weights[warp][lane] = e;
-        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the wave's weights are in
-        __builtin_amdgcn_wave_barrier();
-        float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 64; ++t)
+        for (int i = 0; i < chunks; ++i)
         {
-            if (t < count)
+            staged[warp][i * 64 + lane] = rows[i];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the wave's weights and values are in
+        __builtin_amdgcn_wave_barrier();
+        const uint16_t* column16 = reinterpret_cast<const uint16_t*>(staged[warp]) + lane;
+        const uint32_t* column32 = reinterpret_cast<const uint32_t*>(staged[warp]) + lane;
+        float s0 = 0.0f, s1 = 0.0f;
+        const auto accumulate = [&](int t)
+        {
+            const float w = weights[warp][t];
+            if constexpr (per_lane == 2)
             {
-                const float w = weights[warp][t];
-                if constexpr (per_lane == 2)
-                {
-                    s0 = __builtin_fmaf(__uint_as_float(value[t] << 16), w, s0);
-                    s1 = __builtin_fmaf(__uint_as_float(value[t] & 0xffff0000u), w, s1);
-                }
-                else
-                {
-                    s0 = __builtin_fmaf(__uint_as_float(value[t] << 16), w, s0);
-                }
+                const uint32_t p = column32[t * 64];
+                s0 = __builtin_fmaf(__uint_as_float(p << 16), w, s0);
+                s1 = __builtin_fmaf(__uint_as_float(p & 0xffff0000u), w, s1);
+            }
+            else
+            {
+                s0 = __builtin_fmaf(__uint_as_float(uint32_t(column16[t * 64]) << 16), w, s0);
+            }
+        };
+        if (count == 64)
+        {
+#pragma unroll
+            for (int t = 0; t < 64; ++t)
+            {
+                accumulate(t);
             }
         }
-        float* record = records + std::size_t(block) * (2 + HW);
+        else
+        {
+            for (int t = 0; t < count; ++t)
+            {
+                accumulate(t);
+            }
+        }
+        const std::size_t at = std::size_t(block) * (2 + HW);
+        // Records for the merge of another workgroup go out as device-coherent
+        // stores, so no cache needs writing back before the arrival is counted.
+        const auto put = [&](int i, float value)
+        {
+            if (splits == 1)
+            {
+                records[at + i] = value;
+            }
+            else
+            {
+                __hip_atomic_store(shared_records + at + i, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        };
         if (lane == 0)
         {
-            record[0] = maximum;
-            record[1] = sum;
+            put(0, maximum);
+            put(1, sum);
         }
-        record[2 + per_lane * lane] = round_values ? round_bf16(s0) : s0;
+        put(2 + per_lane * lane, round_values ? round_bf16(s0) : s0);
         if constexpr (per_lane == 2)
         {
-            record[3 + per_lane * lane] = round_values ? round_bf16(s1) : s1;
+            put(3 + per_lane * lane, round_values ? round_bf16(s1) : s1);
         }
-        __builtin_amdgcn_wave_barrier();
     }
-    __syncthreads();
+    if (splits > 1)
+    {
+        // Every wave's records are written before the workgroup counts its
+        // arrival; the last to arrive resets the counter and merges.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0)
+        {
+            const unsigned before =
+                __hip_atomic_fetch_add(arrivals + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            merging = before == unsigned(splits - 1);
+            if (merging)
+            {
+                __hip_atomic_store(arrivals + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __syncthreads();
+        if (!merging)
+        {
+            return;
+        }
+    }
+    else
+    {
+        __syncthreads();
+    }
     if (warp != 0)
     {
         return;
     }
-    // Ordered merge (src/scalar/attention.cpp:86-101).
-    float numerator[2] = {0.0f, 0.0f};
-    float total = 0.0f;
-    bool nan = false;
-    for (int b = lane; b < blocks; b += wave)
-    {
-        nan = nan || __builtin_isnan(records[std::size_t(b) * (2 + HW)]);
-    }
-    const auto step = [&](const float* record, float old_scale, float new_scale)
-    {
-        total = __builtin_fmaf(record[1], new_scale, total * old_scale);
-#pragma unroll
-        for (int i = 0; i < per_lane; ++i)
-        {
-            numerator[i] = __builtin_fmaf(record[2 + per_lane * lane + i], new_scale, numerator[i] * old_scale);
-        }
-    };
+    // Ordered merge (src/scalar/attention.cpp:86-101) by one wave, over
+    // chunks of 64 blocks: lane b holds block b's maximum and sum, every lane
+    // its value sums of all 64 blocks (read from LDS with one split, with
+    // device-coherent loads from `partial` otherwise, all requested at once).
     const auto scales_of = [](float running, float maximum, float& old_scale, float& new_scale)
     {
         const float factor = original_exp(-__builtin_fabsf(maximum - running));
         old_scale = running > maximum ? 1.0f : factor;
         new_scale = running > maximum ? factor : 1.0f;
     };
-    if (__any(nan))
-    {
-        float running = -__builtin_inff();
-        for (int b = 0; b < blocks; ++b)
-        {
-            const float* record = records + std::size_t(b) * (2 + HW);
-            const float maximum = record[0];
-            float old_scale, new_scale;
-            scales_of(running, maximum, old_scale, new_scale);
-            step(record, old_scale, new_scale);
-            running = running < maximum ? maximum : running;
-        }
-    }
-    else
-    {
-        float carry = -__builtin_inff();
-        for (int chunk = 0; chunk < blocks; chunk += wave)
-        {
-            const int b = chunk + lane;
-            const float maximum = b < blocks ? records[std::size_t(b) * (2 + HW)] : -__builtin_inff();
-            // Inclusive scan of the running maximum over this chunk, from `carry`.
-            float inclusive = maximum;
+    float numerator[per_lane];
 #pragma unroll
-            for (int stride = 1; stride < wave; stride *= 2)
+    for (int c = 0; c < per_lane; ++c)
+    {
+        numerator[c] = 0.0f;
+    }
+    float total = 0.0f;
+    float carry = -__builtin_inff();
+    for (int chunk = 0; chunk < blocks; chunk += wave)
+    {
+        const int here = blocks - chunk < wave ? blocks - chunk : wave;
+        const bool live = lane < here;
+        // Straight-line loads in groups of eight blocks, every one requested
+        // before the first is waited for. A group may read up to seven
+        // records past the last block (the records are followed by that much
+        // padding); those values are replaced below.
+        float first[2];
+        float column[wave][per_lane];
+        const auto gather = [&](auto load)
+        {
+            const int b = chunk + (live ? lane : here - 1);
+            first[0] = load(std::size_t(b) * (2 + HW));
+            first[1] = load(std::size_t(b) * (2 + HW) + 1);
+            const std::size_t base = std::size_t(chunk) * (2 + HW) + 2 + per_lane * lane;
+#pragma unroll
+            for (int g = 0; g < wave / 8; ++g)
             {
-                const float left = __shfl_up(inclusive, stride, wave);
-                if (lane >= stride)
+                if (g * 8 < here)
                 {
-                    inclusive = left < inclusive ? inclusive : left;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                    {
+#pragma unroll
+                        for (int c = 0; c < per_lane; ++c)
+                        {
+                            column[g * 8 + j][c] = load(base + std::size_t(g * 8 + j) * (2 + HW) + c);
+                        }
+                    }
                 }
             }
-            inclusive = carry < inclusive ? inclusive : carry;
-            const float before = __shfl_up(inclusive, 1, wave);
-            const float running = lane == 0 ? carry : before;
-            float old_scale, new_scale;
-            scales_of(running, maximum, old_scale, new_scale);
-            const int here = blocks - chunk < wave ? blocks - chunk : wave;
+        };
+        if (splits == 1)
+        {
+            gather([&](std::size_t at) { return records[at]; });
+        }
+        else
+        {
+            gather([&](std::size_t at)
+                   { return __hip_atomic_load(shared_records + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); });
+        }
+        // Lanes past the last block step with old scale 1, new scale 0 and
+        // sums of -0, which leave the total and numerators exactly as they
+        // are, so the steps need no per-block branch.
+        const float maximum = live ? first[0] : -__builtin_inff();
+        const float block_sum = live ? first[1] : -0.0f;
+        float old_scale = 1.0f, new_scale = 0.0f;
+        if (__any(__builtin_isnan(maximum)))
+        {
+            // The plain running maximum, one block at a time.
+            float running = carry;
             for (int i = 0; i < here; ++i)
             {
-                step(records + std::size_t(chunk + i) * (2 + HW),
-                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(old_scale), i)),
-                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(new_scale), i)));
+                const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(maximum), i));
+                float o, n;
+                scales_of(running, m, o, n);
+                if (lane == i)
+                {
+                    old_scale = o;
+                    new_scale = n;
+                }
+                running = running < m ? m : running;
             }
+            carry = running;
+        }
+        else
+        {
+            const float scanned = running_max_scan(maximum);
+            const float inclusive = carry < scanned ? scanned : carry;
+            scales_of(previous_lane(inclusive, carry), maximum, old_scale, new_scale);
             carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inclusive), here - 1));
         }
+        // Each block's factors go through LDS, so the steps read them as
+        // operands (one broadcast read per block) instead of moving them lane
+        // by lane into scalar registers.
+        factors[lane] = make_float4(live ? old_scale : 1.0f, live ? new_scale : 0.0f, block_sum, 0.0f);
+        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int g = 0; g < wave / 8; ++g)
+        {
+            if (g * 8 < here)
+            {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                {
+                    const float4 f = factors[g * 8 + j];
+                    total = __builtin_fmaf(f.z, f.y, total * f.x);
+#pragma unroll
+                    for (int c = 0; c < per_lane; ++c)
+                    {
+                        const float sum = g * 8 + j < here ? column[g * 8 + j][c] : -0.0f;
+                        numerator[c] = __builtin_fmaf(sum, f.y, numerator[c] * f.x);
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier(); // the factors are read before the next chunk's are written
     }
     const float reciprocal = 1.0f / total;
     uint16_t* o = out + std::size_t(sequence) * width + head * HW + per_lane * lane;
@@ -346,55 +448,6 @@ __global__ __launch_bounds__(decode_waves<HW> * 64) void decode_attention_kernel
     }
 }
 
-template <int HW>
-__global__ __launch_bounds__(64) void decode_combine_kernel(const float* __restrict__ partial,
-                                                            int time, int heads, int max_blocks,
-                                                            int width, uint16_t* __restrict__ out)
-{
-    const int sequence = blockIdx.x / heads, head = blockIdx.x % heads;
-    const int blocks = (time + 63) / 64;
-    const float* records = partial + std::size_t(blockIdx.x) * max_blocks * (2 + HW);
-    constexpr int per_lane = (HW + 63) / 64;
-    float numerator[per_lane];
-#pragma unroll
-    for (int i = 0; i < per_lane; ++i)
-    {
-        numerator[i] = 0.0f;
-    }
-    float running_maximum = -__builtin_inff(), total = 0.0f;
-    for (int b = 0; b < blocks; ++b)
-    {
-        const float* record = records + std::size_t(b) * (2 + HW);
-        const float maximum = record[0];
-        const float difference = maximum - running_maximum;
-        const float factor = original_exp(-__builtin_fabsf(difference));
-        const float old_scale = running_maximum > maximum ? 1.0f : factor;
-        const float new_scale = running_maximum > maximum ? factor : 1.0f;
-        const float old_total = total * old_scale;
-        total = __builtin_fmaf(record[1], new_scale, old_total);
-#pragma unroll
-        for (int i = 0; i < per_lane; ++i)
-        {
-            const int j = threadIdx.x + 64 * i;
-            if (j < HW)
-            {
-                const float old = numerator[i] * old_scale;
-                numerator[i] = __builtin_fmaf(record[2 + j], new_scale, old);
-            }
-        }
-        running_maximum = running_maximum < maximum ? maximum : running_maximum;
-    }
-    const float reciprocal = 1.0f / total;
-#pragma unroll
-    for (int i = 0; i < per_lane; ++i)
-    {
-        const int j = threadIdx.x + 64 * i;
-        if (j < HW)
-        {
-            out[std::size_t(sequence) * width + head * HW + j] = float_to_bf16(numerator[i] * reciprocal);
-        }
-    }
-}
 
 // ------------------------------------------------------------------ prefill
 
@@ -662,69 +715,79 @@ void append_qkv(const uint16_t* qkv, std::size_t rows, std::size_t width, std::s
     check_hip(hipGetLastError(), "append launch");
 }
 
+namespace
+{
+__global__ void clear_arrivals(unsigned* words, std::size_t count)
+{
+    for (std::size_t i = blockIdx.x * std::size_t(blockDim.x) + threadIdx.x; i < count;
+         i += std::size_t(gridDim.x) * blockDim.x)
+    {
+        words[i] = 0;
+    }
+}
+} // namespace
+
 std::size_t decode_partial_floats(std::size_t sequences, std::size_t heads, std::size_t head_width,
                                   std::size_t time)
 {
     const std::size_t blocks = (time + 63) / 64;
-    return blocks <= std::size_t(decode_lds_blocks) ? 0 : sequences * heads * blocks * (2 + head_width);
+    // Seven records of padding: the merge reads whole groups of eight.
+    return decode_splits(int(blocks)) > 1 ? (sequences * heads * blocks + 7) * (2 + head_width) : 0;
+}
+
+std::size_t decode_arrival_counters(std::size_t sequences, std::size_t heads, std::size_t time)
+{
+    return decode_splits(int((time + 63) / 64)) > 1 ? sequences * heads : 0;
+}
+
+void clear_arrival_counters(unsigned* counters, std::size_t count, hipStream_t stream)
+{
+    if (count)
+    {
+        const std::size_t groups = (count + 255) / 256;
+        clear_arrivals<<<unsigned(groups < 1024 ? groups : 1024), 256, 0, stream>>>(counters, count);
+        check_hip(hipGetLastError(), "attention counter clear launch");
+    }
 }
 
 void attention_decode(const uint16_t* query, const uint16_t* keys, const uint16_t* values,
                       std::size_t sequence_stride, std::size_t sequences, std::size_t time,
                       std::size_t heads, std::size_t head_width, float scale, bool replay,
-                      float* partial, uint16_t* out, hipStream_t stream)
+                      float* partial, unsigned* arrivals, uint16_t* out, hipStream_t stream)
 {
     require(time > 0 && sequences > 0, "attention: empty shape");
-    require(time < (std::size_t(1) << 30) && sequences * heads < (std::size_t(1) << 31), "attention: shape too large");
+    require(time < (std::size_t(1) << 30) && sequences * heads < (std::size_t(1) << 24), "attention: shape too large");
+    require(head_width == 64 || head_width == 128, "attention: head width must be 64 or 128");
+    require(time * heads * head_width * 2 < (std::size_t(1) << 31), "attention: history too long for one decode");
     const int max_blocks = int((time + 63) / 64);
     const int width = int(heads * head_width);
     const int round_values = time > 64 || replay;
-    if (max_blocks <= decode_lds_blocks)
+    const std::size_t pairs = sequences * heads;
+    require(!decode_partial_floats(sequences, heads, head_width, time) || partial != nullptr,
+            "attention: this history needs the decode records scratch");
+    require(!decode_arrival_counters(sequences, heads, time) || arrivals != nullptr,
+            "attention: this history needs the decode arrival counters");
+    const int splits = decode_splits(max_blocks);
+    require(pairs * splits < (std::size_t(1) << 31), "attention: too many workgroups for one decode");
+    // Records stay in LDS only with one split (then with the merge's seven
+    // records of padding).
+    const std::size_t lds = splits == 1 ? std::size_t(max_blocks + 7) * (2 + head_width) * 4 : 0;
+    const unsigned grid = unsigned(pairs * splits);
+    const auto launch = [&](auto kernel)
     {
-        const std::size_t lds = std::size_t(max_blocks) * (2 + head_width) * 4;
-        const unsigned grid = unsigned(sequences * heads);
-        switch (head_width)
-        {
-        case 64:
-            check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attention_kernel<64>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)),
-                      "attention decode LDS");
-            decode_attention_kernel<64><<<grid, decode_waves<64> * 64, lds, stream>>>(
-                query, keys, values, sequence_stride, width, int(time), int(heads), scale, round_values, out);
-            break;
-        case 128:
-            check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attention_kernel<128>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)),
-                      "attention decode LDS");
-            decode_attention_kernel<128><<<grid, decode_waves<128> * 64, lds, stream>>>(
-                query, keys, values, sequence_stride, width, int(time), int(heads), scale, round_values, out);
-            break;
-        default:
-            throw Error("attention: head width must be 64 or 128");
-        }
-        check_hip(hipGetLastError(), "attention decode launch");
-        return;
+        check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)),
+                  "attention decode LDS");
+        kernel<<<grid, decode_waves * 64, lds, stream>>>(query, keys, values, sequence_stride, width, int(time),
+                                                        int(heads), scale, round_values, partial, arrivals, out);
+    };
+    if (head_width == 64)
+    {
+        launch(decode_attention_kernel<64>);
     }
-    require(partial != nullptr, "attention: long histories need the partial scratch");
-    const dim3 grid(unsigned(sequences * heads), unsigned(max_blocks));
-    switch (head_width)
+    else
     {
-    case 64:
-        decode_blocks_kernel<64><<<grid, 64, 0, stream>>>(query, keys, values, sequence_stride,
-                                                          width, int(time), int(heads), scale,
-                                                          round_values, max_blocks, partial);
-        decode_combine_kernel<64><<<unsigned(sequences * heads), 64, 0, stream>>>(
-            partial, int(time), int(heads), max_blocks, width, out);
-        break;
-    case 128:
-        decode_blocks_kernel<128><<<grid, 64, 0, stream>>>(query, keys, values, sequence_stride,
-                                                           width, int(time), int(heads), scale,
-                                                           round_values, max_blocks, partial);
-        decode_combine_kernel<128><<<unsigned(sequences * heads), 64, 0, stream>>>(
-            partial, int(time), int(heads), max_blocks, width, out);
-        break;
-    default:
-        throw Error("attention: head width must be 64 or 128");
+        launch(decode_attention_kernel<128>);
     }
     check_hip(hipGetLastError(), "attention decode launch");
 }
