@@ -192,6 +192,26 @@ template <int lanes, bool Ftz, int stride> __device__ __forceinline__ float tree
     }
 }
 
+// Two independent pair trees, level by level, so that their dependency
+// chains interleave.
+template <int lanes, bool Ftz, int stride = 1> __device__ __forceinline__ void tree_levels2(float& a, float& b)
+{
+    if constexpr (stride < lanes)
+    {
+        if constexpr (Ftz)
+        {
+            a = butterfly_ftz_add<stride>(a);
+            b = butterfly_ftz_add<stride>(b);
+        }
+        else
+        {
+            a = butterfly_add<stride>(a);
+            b = butterfly_add<stride>(b);
+        }
+        tree_levels2<lanes, Ftz, 2 * stride>(a, b);
+    }
+}
+
 template <int lanes> __device__ __forceinline__ float tree_sum(float v)
 {
     return tree_levels<lanes, true, 1>(flush(v));

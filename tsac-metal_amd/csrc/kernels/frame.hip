@@ -22,6 +22,13 @@ using word = unsigned long long;
 
 constexpr int frame_waves = 8;
 constexpr int frame_threads = frame_waves * wave;
+// Waves that take, normalise and quantise a projection's spread input row
+// (K = 64 V values): fewer waves mean fewer barriers and no two of them
+// sharing a SIMD, against more values per lane. Measured per frame step of the
+// 2580-frame decode: 2 waves for K <= 512 (no BF8L exchange, one LayerNorm
+// exchange) 704 us, 1 wave 718 us, 8 waves 731 us; 8 waves for K = 2048, 4
+// waves 721 us.
+template <int V> constexpr int spread_waves = V <= 8 ? 2 : 8;
 constexpr int max_lanes = 8;
 constexpr int max_blocks = 16; // 64-key blocks of one attention query (context <= 1024)
 constexpr int max_books = 16;  // codebook positions of one frame
@@ -827,12 +834,17 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
     constexpr bool pipelined = rounds == 1;
     static_assert(I != In::attention || (pipelined && book_attention_fits<V, HW>),
                   "attention rows: one lane at a time, a wave per head");
-    // A pipelined tile spreads each input row over its waves (row_ops.hpp), so
-    // LayerNorm and BF8L run on V / frame_waves values per lane of every wave
-    // instead of V values per lane of one.
-    constexpr int Vw = V / frame_waves;
-    constexpr bool spread = pipelined && V % frame_waves == 0 &&
+    // A pipelined tile spreads each input row over its first SW waves
+    // (row_ops.hpp), Vw = V / SW values per lane; the other waves only keep
+    // the row's barriers.
+    constexpr int SW = spread_waves<V>;
+    constexpr int Vw = V / SW;
+    constexpr bool spread = pipelined && V % SW == 0 &&
                             (I == In::words || I == In::words_norm || I == In::attention);
+    // Barriers inside the spread LayerNorm (one exchange of the wave sums) and
+    // BF8L (one exchange of block maxima when a block spans waves).
+    constexpr int spread_barriers =
+        (I == In::words_norm && SW > 1 ? 1 : 0) + (Vw > 0 && 256 / Vw > wave ? 1 : 0);
     static_assert(I != In::attention || spread, "attention rows are spread");
     int8_t* q = reinterpret_cast<int8_t*>(lds);
     float* scales = reinterpret_cast<float*>(lds + max_lanes * K);
@@ -886,8 +898,11 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
     uint16_t norm_gain[V], norm_bias[V], spread_gain[Vw > 0 ? Vw : 1], spread_bias[Vw > 0 ? Vw : 1];
     if constexpr (I == In::words_norm && spread)
     {
-        load_global_row<Vw>(p.gain + (warp * wave + lane) * Vw, spread_gain);
-        load_global_row<Vw>(p.beta + (warp * wave + lane) * Vw, spread_bias);
+        if (warp < SW)
+        {
+            load_global_row<Vw>(p.gain + (warp * wave + lane) * Vw, spread_gain);
+            load_global_row<Vw>(p.beta + (warp * wave + lane) * Vw, spread_bias);
+        }
     }
     else if constexpr (I == In::words_norm)
     {
@@ -927,19 +942,48 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
                               residual_requested ? p.residual + out_word : nullptr, residual_seen);
             }
             lds_barrier();
-            uint16_t v[Vw];
-            load_row<Vw>(row + (warp * wave + lane) * Vw, v);
-            bf8l_spread<Vw, frame_waves>(v, warp, q + m0 * K, scales + m0 * blocks, error, scale_exchange);
+            if (warp < SW)
+            {
+                uint16_t v[Vw];
+                load_row<Vw>(row + (warp * wave + lane) * Vw, v);
+                bf8l_spread<Vw, SW>(v, warp, q + m0 * K, scales + m0 * blocks, error, scale_exchange);
+            }
+            else
+            {
+#pragma unroll
+                for (int i = 0; i < spread_barriers; ++i)
+                {
+                    lds_barrier();
+                }
+            }
         }
         else if constexpr (spread)
         {
-            uint16_t v[Vw];
-            take_values<Vw>(p.x, std::size_t(m0) * K + (warp * wave + lane) * Vw, x, v);
-            if constexpr (I == In::words_norm)
+            if (warp < SW)
             {
-                layer_norm_spread<Vw, frame_waves>(v, spread_gain, spread_bias, warp, norm_exchange);
+                uint16_t v[Vw];
+                if constexpr (Vw % 8 == 0)
+                {
+                    take_row<Vw>(p.x, std::size_t(m0) * K + (warp * wave + lane) * Vw, x, v);
+                }
+                else
+                {
+                    take_values<Vw>(p.x, std::size_t(m0) * K + (warp * wave + lane) * Vw, x, v);
+                }
+                if constexpr (I == In::words_norm)
+                {
+                    layer_norm_spread<Vw, SW>(v, spread_gain, spread_bias, warp, norm_exchange);
+                }
+                bf8l_spread<Vw, SW>(v, warp, q + m0 * K, scales + m0 * blocks, error, scale_exchange);
             }
-            bf8l_spread<Vw, frame_waves>(v, warp, q + m0 * K, scales + m0 * blocks, error, scale_exchange);
+            else
+            {
+#pragma unroll
+                for (int i = 0; i < spread_barriers; ++i)
+                {
+                    lds_barrier();
+                }
+            }
         }
         else if (warp >= m0 && warp < m1)
         {

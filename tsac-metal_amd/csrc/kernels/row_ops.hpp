@@ -349,30 +349,37 @@ __device__ __forceinline__ void layer_norm_spread(uint16_t (&v)[Vw], const uint1
     float sum, sum_squares;
     if (sums_stay_normal<Vw>(v))
     {
-        sum = plain_tree_sum<wave>(register_tree<Vw, false>(values));
-        sum_squares = plain_tree_sum<wave>(register_tree<Vw, false>(squares));
+        sum = register_tree<Vw, false>(values);
+        sum_squares = register_tree<Vw, false>(squares);
+        tree_levels2<wave, false>(sum, sum_squares);
     }
     else
     {
-        sum = tree_sum<wave>(register_tree<Vw>(values));
-        sum_squares = tree_sum<wave>(register_tree<Vw>(squares));
+        sum = flush(register_tree<Vw>(values));
+        sum_squares = flush(register_tree<Vw>(squares));
+        tree_levels2<wave, true>(sum, sum_squares);
     }
-    if (threadIdx.x % wave == 0)
+    if constexpr (Waves > 1)
     {
-        exchange[warp] = sum;
-        exchange[Waves + warp] = sum_squares;
-    }
-    lds_barrier();
-    float sums[Waves], square_sums[Waves];
+        if (threadIdx.x % wave == 0)
+        {
+            exchange[warp] = sum;
+            exchange[Waves + warp] = sum_squares;
+        }
+        lds_barrier();
+        float sums[Waves], square_sums[Waves];
 #pragma unroll
-    for (int w = 0; w < Waves; ++w)
-    {
-        sums[w] = exchange[w];
-        square_sums[w] = exchange[Waves + w];
+        for (int w = 0; w < Waves; ++w)
+        {
+            sums[w] = exchange[w];
+            square_sums[w] = exchange[Waves + w];
+        }
+        sum = flushed_tree<Waves>(sums);
+        sum_squares = flushed_tree<Waves>(square_sums);
     }
     // The row's probability_sum ends with add(+0, S) (src/format/categorical.cpp:44-74).
-    sum = flushed_add(0.0f, flushed_tree<Waves>(sums));
-    sum_squares = flushed_add(0.0f, flushed_tree<Waves>(square_sums));
+    sum = flushed_add(0.0f, sum);
+    sum_squares = flushed_add(0.0f, sum_squares);
     constexpr int width = Waves * wave * Vw;
     const float reciprocal = 1.0f / float(width);
     const float mean = sum * reciprocal;
