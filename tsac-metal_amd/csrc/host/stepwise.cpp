@@ -17,6 +17,9 @@ namespace tsac_hip
 namespace
 {
 constexpr std::size_t replay_frames = 256;
+// Frame steps per persistent launch: the launches in between cost ~20 us each,
+// and a launch of this many steps holds the device for ~50 ms.
+constexpr std::size_t frame_launch_steps = 64;
 // Projections batch up to `chunk` lanes as their columns; larger lane sets run
 // chunk by chunk, which keeps each (step, book)'s lanes in stream order.
 constexpr std::size_t chunk = 8;
@@ -375,12 +378,22 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
         const std::size_t active = step < lanes.base ? independent : lanes.extra * G;
         if (framed && context_used != g.context)
         {
+            // Consecutive steps with the same lanes and no rollover in one
+            // launch, at most frame_launch_steps of them.
+            std::size_t n = 1;
+            while (n < frame_launch_steps && step + n < lanes.steps() && context_used + n < g.context &&
+                   (step + n < lanes.base) == (step < lanes.base))
+            {
+                ++n;
+            }
             frame.lanes = int(active);
             frame.position = int(context_used);
             frame.step = int(step);
+            frame.steps = int(n);
             frame.epoch = uint32_t(step + 1); // exchange words are cleared for every pass
             frame_step(frame, stream_);
-            ++context_used;
+            context_used += n;
+            step += n - 1;
         }
         else if (context_used == g.context)
         {

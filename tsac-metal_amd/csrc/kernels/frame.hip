@@ -514,15 +514,15 @@ struct Projection
     int alphabet = 0, books = 0, book = 0;
     const uint16_t* tokens = nullptr; // embed_sum: [lanes][token_stride]
     int token_stride = 0;
-    const word* token_words = nullptr; // embed_accumulate: previous book's tokens
+    // embed_accumulate: previous book's tokens; embed_sum: book 0's tokens,
+    // book b's at + b * token_book_words (the previous step's, within a launch)
+    const word* token_words = nullptr;
+    std::size_t token_book_words = 0;
     const word* prefix_in = nullptr;   // embed_accumulate: previous prefix (null for the first)
     word* prefix_out = nullptr;        // embed_accumulate: published by tile 0
     const word* residual = nullptr;
     const uint16_t* residual_row = nullptr;
     word* y = nullptr;
-    uint16_t* keys = nullptr; // qkv: this layer's cache at position 0 of lane 0 (null: no cache)
-    uint16_t* values = nullptr;
-    long long lane_stride = 0;
     int position = 0;
     const uint16_t* rotations = nullptr;
     int width = 0, head_width = 0;
@@ -782,7 +782,7 @@ __device__ __forceinline__ void book_head(const word* qkv, std::size_t book_word
 template <int V, In I, Out O, int HW = 0>
 __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int position, int M, int tile, Exchange exchange,
                                           uint32_t* error, uint8_t* lds, constant_ptr<BookAttention> book_job = nullptr,
-                                          int book_lane = 0)
+                                          int book_lane = 0, uint32_t previous_epoch = 0)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
     lds = in_lds(lds);
@@ -802,14 +802,13 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
     p.tokens = uniform(job->tokens);
     p.token_stride = uniform(job->token_stride);
     p.token_words = uniform(job->token_words);
+    p.token_book_words = uniform(job->token_book_words);
+    previous_epoch = uint32_t(uniform(int(previous_epoch)));
     p.prefix_in = uniform(job->prefix_in);
     p.prefix_out = uniform(job->prefix_out);
     p.residual = uniform(job->residual);
     p.residual_row = uniform(job->residual_row);
     p.y = uniform(job->y);
-    p.keys = uniform(job->keys);
-    p.values = uniform(job->values);
-    p.lane_stride = uniform(job->lane_stride);
     p.position = uniform(position);
     p.rotations = uniform(job->rotations);
     p.width = uniform(job->width);
@@ -1000,12 +999,29 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
             else if constexpr (I == In::embed_sum)
             {
                 // src/common/cpu_transformer.tpp:205-224: copy book 0, add later books in order.
+                // The previous step's tokens: from `tokens` at a launch's first
+                // step (written before the launch), else from that step's
+                // token words.
                 const uint16_t* t = p.tokens + std::size_t(warp) * p.token_stride;
-                const int t0 = min(int(*global(t)), p.alphabet - 1);
+                // Lane b polls book b's token word (all books' at once).
+                uint32_t previous = 0;
+                if (previous_epoch != 0)
+                {
+                    const int b = lane < p.books ? lane : p.books - 1;
+                    previous = take(p.token_words + std::size_t(b) * p.token_book_words, warp,
+                                    Exchange{previous_epoch, x.abort});
+                }
+                const auto token_of = [&](int b)
+                {
+                    const int token = previous_epoch != 0 ? int(__builtin_amdgcn_readlane(previous, b) & 0xffff)
+                                                          : int(*global(t + b));
+                    return min(token, p.alphabet - 1);
+                };
+                const int t0 = token_of(0);
                 load_global_row<V>(p.embeddings + std::size_t(t0) * K + lane * V, v);
                 for (int b = 1; b < p.books; ++b)
                 {
-                    const int tb = min(int(*global(t + b)), p.alphabet - 1);
+                    const int tb = token_of(b);
                     uint16_t e[V];
                     load_global_row<V>(p.embeddings + (std::size_t(b) * p.alphabet + tb) * K + lane * V, e);
 #pragma unroll
@@ -1143,12 +1159,6 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
                 y0 = float_to_bf16(__builtin_fmaf(re, cosine, -im_sine));
                 y1 = float_to_bf16(__builtin_fmaf(im, cosine, re_sine));
             }
-            if (p.keys && n0 >= width)
-            {
-                uint16_t* cache = n0 < 2 * width ? p.keys + (n0 - width) : p.values + (n0 - 2 * width);
-                *global_out(reinterpret_cast<uint32_t*>(cache + std::size_t(m) * p.lane_stride +
-                                                        std::size_t(p.position) * width)) = y0 | (uint32_t(y1) << 16);
-            }
         }
         publish(p.y, out_word, y0 | (uint32_t(y1) << 16), x.epoch);
     };
@@ -1180,10 +1190,10 @@ struct Attend
     float scale = 0.0f;
     int time = 0; // keys 0 .. time-1
     // Temporal: rows before time-1 from the cache (this layer, lane 0, row 0),
-    // row time-1 from `qkv`. Codebook (keys == null): row t from the qkv words
-    // of book t at qkv + t*book_words.
-    const uint16_t* keys = nullptr;
-    const uint16_t* values = nullptr;
+    // row time-1 from `qkv`, then stored into the cache. Codebook (keys ==
+    // null): row t from the qkv words of book t at qkv + t*book_words.
+    uint16_t* keys = nullptr;
+    uint16_t* values = nullptr;
     long long lane_stride = 0;
     const word* qkv = nullptr;
     std::size_t book_words = 0;
@@ -1331,6 +1341,16 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
         }
     }
     lds_barrier();
+    // Temporal: this step's key and value row joins the cache, stored by the
+    // workgroup that owns this (lane, head) in every step, so the later steps
+    // of the launch read it back through the same L2.
+    if (temporal && threadIdx.x < row_words)
+    {
+        const int i = int(threadIdx.x);
+        uint16_t* to = (i < HW / 2 ? a.keys : a.values) + std::size_t(m) * a.lane_stride + std::size_t(cached) * width +
+                       head * HW + 2 * (i % (HW / 2));
+        *global_out(reinterpret_cast<uint32_t*>(to)) = staged[i];
+    }
 
     // The value word of staged row r for this lane's columns.
     const auto staged_value = [&](int r) -> uint32_t
@@ -2177,7 +2197,10 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[frame_lds<VW, VF, VL, HW>()];
     __shared__ DecoderState decoder;
-    const Exchange x{a.epoch, a.abort};
+    // The launch runs a.steps consecutive steps; each has its own epoch,
+    // context position and step index.
+    Exchange x{a.epoch, a.abort};
+    int position = a.position, step_index = a.step;
     const Words L(a.width, a.ffn, a.latent, a.alphabet, a.books, a.temporal_layers, a.codebook_layers);
     const int M = a.lanes, G = int(gridDim.x), me = int(blockIdx.x);
     const int TL = a.temporal_layers, CL = a.codebook_layers, C = a.books, width = a.width;
@@ -2265,7 +2288,7 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
             const auto p = projection(q);
             for (int t = first_tile(Kind::qkv, parity); t < 3 * width_tiles; t += step(Kind::qkv))
             {
-                project_tile<VW, In::words_norm, Out::qkv>(p, a.position, M, t, x, a.error, lds);
+                project_tile<VW, In::words_norm, Out::qkv>(p, position, M, t, x, a.error, lds);
             }
         }
         // Temporal attention is a job of its own; with the fused layout a
@@ -2320,50 +2343,57 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
         }
     };
 
-    // Temporal stack: feedback embeddings of the previous frame, then layers.
-    if (member(Kind::embed))
+    for (int s = 0; s < a.steps; ++s)
     {
-        const auto p = projection(T.embed());
-        for (int t = first_tile(Kind::embed); t < width_tiles; t += group_size[Kind::embed])
+        x.epoch = a.epoch + uint32_t(s);
+        position = a.position + s;
+        step_index = a.step + s;
+        // Temporal stack: feedback embeddings of the previous frame, then layers.
+        if (member(Kind::embed))
         {
-            project_tile<VL, In::embed_sum, Out::plain>(p, 0, M, t, x, a.error, lds);
-        }
-    }
-    for (int l = 0; l < TL; ++l)
-    {
-        run_layer(true, T.temporal(l, 0), T.attend(true, 0, l), a.position + 1, l % 2);
-    }
-    // Book 0's input.
-    if (first_tile(Kind::condition) == 0)
-    {
-        const auto c = constant<Condition>(jobs + T.condition_offset());
-        condition_rows<VW>(c->in, c->gain, c->bias, c->positions, c->out, M, x);
-    }
-    for (int b = 0; b < C; ++b)
-    {
-        if (b > 0 && member(Kind::prefix))
-        {
-            const auto p = projection(T.prefix(b));
-            for (int t = first_tile(Kind::prefix); t < width_tiles; t += group_size[Kind::prefix])
+            const auto p = projection(T.embed());
+            const uint32_t previous_epoch = s > 0 ? x.epoch - 1u : 0u;
+            for (int t = first_tile(Kind::embed); t < width_tiles; t += group_size[Kind::embed])
             {
-                project_tile<VL, In::embed_accumulate, Out::residual_row>(p, 0, M, t, x, a.error, lds);
+                project_tile<VL, In::embed_sum, Out::plain>(p, 0, M, t, x, a.error, lds, nullptr, 0, previous_epoch);
             }
         }
-        for (int l = 0; l < CL; ++l)
+        for (int l = 0; l < TL; ++l)
         {
-            run_layer(false, T.codebook(b, l, 0), T.attend(false, b, l), b + 1, (TL + b * CL + l) % 2);
+            run_layer(true, T.temporal(l, 0), T.attend(true, 0, l), position + 1, l % 2);
         }
-        if (member(Kind::head))
+        // Book 0's input.
+        if (first_tile(Kind::condition) == 0)
         {
-            const auto p = projection(T.head(b));
-            for (int t = first_tile(Kind::head); t < a.alphabet / tile_rows; t += group_size[Kind::head])
+            const auto c = constant<Condition>(jobs + T.condition_offset());
+            condition_rows<VW>(c->in, c->gain, c->bias, c->positions, c->out, M, x);
+        }
+        for (int b = 0; b < C; ++b)
+        {
+            if (b > 0 && member(Kind::prefix))
             {
-                project_tile<VW, In::words_norm, Out::plain>(p, 0, M, t, x, a.error, lds);
+                const auto p = projection(T.prefix(b));
+                for (int t = first_tile(Kind::prefix); t < width_tiles; t += group_size[Kind::prefix])
+                {
+                    project_tile<VL, In::embed_accumulate, Out::residual_row>(p, 0, M, t, x, a.error, lds);
+                }
             }
-        }
-        if (me == sampler)
-        {
-            draw_tokens(constant<Draw>(jobs + T.draw_offset(b)), a.step, M, &decoder, x, a.error, lds);
+            for (int l = 0; l < CL; ++l)
+            {
+                run_layer(false, T.codebook(b, l, 0), T.attend(false, b, l), b + 1, (TL + b * CL + l) % 2);
+            }
+            if (member(Kind::head))
+            {
+                const auto p = projection(T.head(b));
+                for (int t = first_tile(Kind::head); t < a.alphabet / tile_rows; t += group_size[Kind::head])
+                {
+                    project_tile<VW, In::words_norm, Out::plain>(p, 0, M, t, x, a.error, lds);
+                }
+            }
+            if (me == sampler)
+            {
+                draw_tokens(constant<Draw>(jobs + T.draw_offset(b)), step_index, M, &decoder, x, a.error, lds);
+            }
         }
     }
     if (me == sampler && a.known == nullptr)
@@ -2455,9 +2485,6 @@ std::vector<uint8_t> frame_job_table(const FrameArgs& a)
         p.head_width = a.head_width;
         if (temporal)
         {
-            p.keys = a.keys + std::size_t(l) * a.extent * width;
-            p.values = a.values + std::size_t(l) * a.extent * width;
-            p.lane_stride = a.lane_stride;
             p.rotations = model.rotations;
         }
         put(T.projection_offset(q), p);
@@ -2513,6 +2540,8 @@ std::vector<uint8_t> frame_job_table(const FrameArgs& a)
     embed.books = C;
     embed.tokens = a.current;
     embed.token_stride = C;
+    embed.token_words = words + L.c_token(0, CL);
+    embed.token_book_words = L.book;
     embed.y = words + L.t_x(0);
     put(T.projection_offset(T.embed()), embed);
     for (int l = 0; l < TL; ++l)
@@ -2590,7 +2619,8 @@ void frame_step(const FrameArgs& a, hipStream_t stream)
 {
     require(frame_supported(a.width, a.heads, a.head_width, a.ffn, a.latent, a.alphabet, a.lanes),
             "frame step: unsupported geometry");
-    require(a.position >= 0 && a.position < a.extent && a.extent <= max_blocks * 64, "frame step: position");
+    require(a.steps >= 1 && a.position >= 0 && a.position + a.steps <= a.extent && a.extent <= max_blocks * 64,
+            "frame step: position");
     require(a.books >= 1 && a.books <= max_books && a.temporal_layers >= 1 && a.codebook_layers >= 1,
             "frame step: layers");
     require(a.words && a.abort && a.error && a.current && a.tokens && a.row_base && a.jobs && a.epoch != 0,

@@ -18,10 +18,14 @@
 // out-projection tiles, one workgroup per (tile, lane), and the qkv/up/down
 // tiles alternate between two sets of workgroups from layer to layer.
 //
-// Key/value rows of earlier steps come from the temporal cache (written by
-// earlier launches); the current step's rows and the whole codebook stack come
-// from exchange words. Every wait is bounded: a stalled wait raises the abort
-// word, after which all waits return at once and the launch ends.
+// One launch runs several consecutive steps (epochs advance by one per step),
+// so a lane's next step starts as soon as its own tokens are drawn, with no
+// launch in between. Key/value rows of earlier steps come from the temporal
+// cache: rows stored during the launch with device-coherent stores and read
+// back with device-coherent loads; the current step's rows and the whole
+// codebook stack come from exchange words, and so do the previous step's
+// tokens. Every wait is bounded: a stalled wait raises the abort word, after
+// which all waits return at once and the launch ends.
 #pragma once
 
 #include "decode.hpp"
@@ -52,8 +56,9 @@ struct FrameArgs
     uint16_t* values = nullptr;
     long long lane_stride = 0;
     int extent = 0;
-    int position = 0; // context position of this step
-    int step = 0;     // frame step index
+    int position = 0; // context position of the launch's first step
+    int step = 0;     // frame step index of the launch's first step
+    int steps = 1;    // consecutive steps of the launch (position, step and epoch advance by one)
     // tokens
     uint16_t* current = nullptr; // [lanes][books]: previous frame in, this frame out
     const int* row_base = nullptr;
@@ -67,7 +72,7 @@ struct FrameArgs
     uint32_t* error = nullptr;
     // exchange
     unsigned long long* words = nullptr; // frame_exchange_words() words, zero before the first step
-    uint32_t epoch = 0;                  // nonzero, different for every launch over the same words
+    uint32_t epoch = 0;                  // first step's; nonzero, different for every step over the same words
     unsigned* abort = nullptr;           // zero before the first step; nonzero after a stalled wait
     const void* jobs = nullptr;          // device copy of frame_job_table(*this), unchanged during a launch
 };
@@ -79,7 +84,7 @@ std::size_t frame_exchange_words(int width, int ffn, int latent, int alphabet, i
                                  int codebook_layers);
 // Every job's descriptor (weights, norms, exchange-word ranges, caches) for the
 // launches of one pass, built on the host from the pointers in `args` (all but
-// position, step, lanes and epoch, which the launches pass themselves); the
+// position, step, steps, lanes and epoch, which the launches pass themselves); the
 // launches read it from device memory through FrameArgs::jobs.
 std::vector<uint8_t> frame_job_table(const FrameArgs& args);
 void frame_step(const FrameArgs& args, hipStream_t stream);
