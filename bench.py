@@ -368,13 +368,14 @@ def attention_rates(torch, native, lengths=(256, 1290, 2580), batch=3, heads=16,
 
 
 def frame_roofline(geometry, frames, batch, step_s):
-    """The timed region's dominant kernel, one decode frame step per launch:
-    algorithmic bytes per step (every projection's int8 weights, block scales
-    and bias read once per step for all lanes, plus each lane's temporal
-    key/value cache rows at the average context position) over the average
-    step time `step_s` (HIP events around the step loop on the session's
-    stream / steps). It is bound by its ~240 dependent jobs on lane 0's chain,
-    not by memory; the fraction shows how far from HBM-bound that is."""
+    """The timed region's dominant kernel, up to 64 decode frame steps per
+    launch: algorithmic bytes per step (every projection's int8 weights, block
+    scales and bias read once per step for all lanes, plus each lane's
+    temporal key/value cache rows at the average context position) over the
+    average step time `step_s` (HIP events around the step loop on the
+    session's stream / steps); per launch both scale by the launch's steps. It
+    is bound by its ~240 dependent jobs on lane 0's chain, not by memory; the
+    fraction shows how far from HBM-bound that is."""
     g = geometry
     measured, source = (recorded_traffic("frame_step_decode_reference_2580frames.traffic.txt", "bytes_per_step")
                         if g.width == 512 and frames == 2580 and batch == 3 else (None, None))
@@ -395,6 +396,7 @@ def frame_roofline(geometry, frames, batch, step_s):
             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured, "traffic_source": source,
             "limited_by": "dependent-job latency (~240 jobs per step in order on lane 0's chain)",
             "bytes_per_step": int(weights + cache), "avg_step_us": round(step_s * 1e6, 1), "steps": steps,
+            "steps_per_launch": 64,
             "step_time": "GPU time between two HIP events around the frame-step loop on the session's stream, "
                          "divided by the steps"}
 
