@@ -410,7 +410,7 @@ __device__ __forceinline__ void give_row(word* w, std::size_t first, const Excha
 // an N-wide matrix at m*N/2.
 struct Words
 {
-    std::size_t w, qkv, hid, logit, pre, layer, temporal, book, total;
+    std::size_t w, qkv, hid, logit, pre, layer, temporal, book, records, record_layer, total;
 
     __host__ __device__ Words(int width, int ffn, int latent, int alphabet, int books, int temporal_layers,
                                int codebook_layers)
@@ -423,7 +423,16 @@ struct Words
         layer = qkv + w + w + hid + w; // qkv, attention, mid residual, hidden, out
         temporal = w + temporal_layers * layer;
         book = pre + w + codebook_layers * layer + logit + 8;
-        total = temporal + std::size_t(books) * book;
+        // Block records of the temporal attention's second half (blocks 8-15)
+        // per layer: max_lanes lanes x heads x 8 blocks x (2 + head width)
+        // words, with heads <= width / 64.
+        records = temporal + std::size_t(books) * book;
+        record_layer = std::size_t(max_lanes) * 8 * (std::size_t(width) + width / 32);
+        total = records + std::size_t(temporal_layers) * record_layer;
+    }
+    __host__ __device__ std::size_t t_records(int l) const
+    {
+        return records + l * record_layer;
     }
     // Temporal stack: input of layer l (l == layers is its output).
     __host__ __device__ std::size_t t_x(int l) const
@@ -1198,6 +1207,9 @@ struct Attend
     const word* qkv = nullptr;
     std::size_t book_words = 0;
     word* out = nullptr;
+    // Temporal, split in halves: the block records of blocks 8-15, item i's
+    // block b field f at word ((i * 8) + b - 8) * (2 + HW) + f.
+    word* records = nullptr;
 };
 
 template <int HW> constexpr int attend_lds()
@@ -1211,8 +1223,15 @@ template <int HW> constexpr int attend_lds()
 // The rows that come through exchange words (the current position's, or every
 // codebook row) and the query are staged in LDS first, so the block loops read
 // only the cache and LDS.
+// A temporal query may be split in halves over two workgroups: half 1 takes
+// blocks 8-15 (when there are more than 8) and hands their records to half 0
+// in exchange words; half 0 takes blocks 0-7, then those records, and merges
+// every block in ascending order as one workgroup would. Each half stores the
+// cache rows of its own blocks, so a row is read back through the L2 that
+// wrote it. `half` -1 is one workgroup for all blocks.
 template <int HW>
-__device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys, int item, Exchange exchange, uint8_t* lds)
+__device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys, int item, int half, Exchange exchange,
+                                         uint8_t* lds)
 {
     const Exchange x{uint32_t(uniform(int(exchange.epoch))), uniform(exchange.abort)};
     lds = in_lds(lds);
@@ -1227,7 +1246,9 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
     a.qkv = uniform(job->qkv);
     a.book_words = uniform(job->book_words);
     a.out = uniform(job->out);
+    a.records = uniform(job->records);
     item = uniform(item);
+    half = uniform(half);
     constexpr int per_lane = HW / 64; // value columns per lane (adjacent)
     constexpr int row_words = HW;     // staged row: HW/2 key words, then HW/2 value words
     constexpr int key_stride = staged_key_stride<HW>;
@@ -1244,6 +1265,15 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
     const bool round_values = time > 64;
     const int width = a.width;
     const bool temporal = a.keys != nullptr;
+    if (half == 1 && (!temporal || blocks <= frame_waves))
+    {
+        return; // half 0 has every block
+    }
+    // This workgroup's blocks [first_block, end_block) and whether it stores
+    // this step's cache row (the owner of the row's block).
+    const int first_block = half == 1 ? frame_waves : 0;
+    const int end_block = half == 0 ? min(blocks, frame_waves) : blocks;
+    const bool stores_row = half < 0 || half == ((time - 1) / 64 >= frame_waves ? 1 : 0);
     const int cached = temporal ? time - 1 : 0; // rows 0..cached-1 come from the cache
     const int exchanged = time - cached;        // the rest from words (1, or time <= max_books)
     const std::size_t row_values = 3 * std::size_t(width);
@@ -1290,9 +1320,9 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
             }
         }
     };
-    if (temporal && warp < blocks)
+    if (temporal && first_block + warp < end_block)
     {
-        load_cached(warp);
+        load_cached(first_block + warp);
     }
 
     // 1. Stage the query and the exchanged rows: word i of the query is i < HW/2;
@@ -1344,7 +1374,7 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
     // Temporal: this step's key and value row joins the cache, stored by the
     // workgroup that owns this (lane, head) in every step, so the later steps
     // of the launch read it back through the same L2.
-    if (temporal && threadIdx.x < row_words)
+    if (temporal && stores_row && threadIdx.x < row_words)
     {
         const int i = int(threadIdx.x);
         uint16_t* to = (i < HW / 2 ? a.keys : a.values) + std::size_t(m) * a.lane_stride + std::size_t(cached) * width +
@@ -1373,9 +1403,9 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
     // 2. Blocks of 64 keys: wave w owns blocks w, w + waves, ...
     float* block_weights = weights + warp * 64;
     float kept[2 + per_lane]; // the last block's maximum, total and value sums
-    for (int block = warp; block < blocks; block += frame_waves)
+    for (int block = first_block + warp; block < end_block; block += frame_waves)
     {
-        if (block != warp)
+        if (block != first_block + warp)
         {
             load_cached(block);
         }
@@ -1555,6 +1585,41 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
     // is wave 0's own: its record stays in registers, with no barrier.
     if (blocks > 1)
     {
+        lds_barrier();
+    }
+    if (half >= 0 && blocks > frame_waves)
+    {
+        constexpr int record_floats = 2 + HW;
+        const int count = (blocks - frame_waves) * record_floats;
+        word* const records = a.records + std::size_t(item) * frame_waves * record_floats;
+        float* const second = partial + std::size_t(frame_waves) * record_floats;
+        if (half == 1)
+        {
+            // Hand the records of blocks 8.. over, and stop.
+            for (int i = int(threadIdx.x); i < count; i += frame_threads)
+            {
+                publish(records, i, __float_as_uint(second[i]), x.epoch);
+            }
+            return;
+        }
+        constexpr int per_thread = (frame_waves * record_floats + frame_threads - 1) / frame_threads;
+        uint32_t got[per_thread];
+        take_words<per_thread>(
+            [&](int i) -> const word*
+            {
+                const int index = int(threadIdx.x) + i * frame_threads;
+                return records + (index < count ? index : count - 1);
+            },
+            x, got);
+#pragma unroll
+        for (int i = 0; i < per_thread; ++i)
+        {
+            const int index = int(threadIdx.x) + i * frame_threads;
+            if (index < count)
+            {
+                second[index] = __uint_as_float(got[i]);
+            }
+        }
         lds_barrier();
     }
     if (warp != 0)
@@ -2163,6 +2228,7 @@ template <int VW, int VF, int VL, int HW> constexpr int frame_lds()
 struct FrameLayout
 {
     bool fused = false, paired = false;
+    bool split = false; // temporal queries in halves over two workgroups each
     int out_tiles = 0; // tiles of an out job: one per lane when fused
     int workgroups = 0; // workers the layout asks for
 };
@@ -2189,6 +2255,11 @@ __host__ __device__ inline FrameLayout frame_layout(int width, int heads, int ff
     }
     l.out_tiles = l.fused ? lanes * w : w;
     l.workgroups = base + (l.fused ? fused_extra : 0) + (l.paired ? paired_extra : 0);
+    if (l.workgroups + lanes * heads <= workers)
+    {
+        l.split = true;
+        l.workgroups += lanes * heads;
+    }
     return l;
 }
 
@@ -2230,11 +2301,16 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
         kinds
     };
     const FrameLayout layout = frame_layout(width, a.heads, a.ffn, a.alphabet, M, G - 1);
-    const int kind_tiles[kinds] = {width / tile_rows, 3 * width / tile_rows, M * a.heads, layout.out_tiles,
-                                   a.ffn / tile_rows, width / tile_rows, 1, width / tile_rows,
-                                   a.alphabet / tile_rows};
     const auto sets = [&](int kind)
     { return layout.paired && (kind == Kind::qkv || kind == Kind::up || kind == Kind::down) ? 2 : 1; };
+    // With layout.split, temporal queries go to two workgroups each
+    // (attend_item's halves). Tiles [0, M*heads) are the second halves: a
+    // workgroup runs its tiles in ascending order, so one that held both
+    // halves of a query would hand the records over before it waits for them.
+    const bool split_attention = layout.split;
+    const int kind_tiles[kinds] = {width / tile_rows, 3 * width / tile_rows, (split_attention ? 2 : 1) * M * a.heads,
+                                   layout.out_tiles, a.ffn / tile_rows, width / tile_rows, 1, width / tile_rows,
+                                   a.alphabet / tile_rows};
     int group_size[kinds], group_base[kinds];
     {
         const int workers = G - 1;
@@ -2298,9 +2374,11 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
         if (!fused)
         {
             const auto attention = constant<Attend>(jobs + T.attend_offset(att));
-            for (int t = first_tile(Kind::attend); t < M * a.heads; t += group_size[Kind::attend])
+            const int items = M * a.heads;
+            for (int t = first_tile(Kind::attend); t < kind_tiles[Kind::attend]; t += group_size[Kind::attend])
             {
-                attend_item<HW>(attention, time, t, x, lds);
+                const int half = !split_attention ? -1 : t < items ? 1 : 0;
+                attend_item<HW>(attention, time, t % items, half, x, lds);
             }
         }
         if (member(Kind::out))
@@ -2518,6 +2596,7 @@ std::vector<uint8_t> frame_job_table(const FrameArgs& a)
             at.values = a.values + std::size_t(l) * a.extent * width;
             at.lane_stride = a.lane_stride;
             at.qkv = words + qkv;
+            at.records = words + L.t_records(l);
         }
         else
         {
