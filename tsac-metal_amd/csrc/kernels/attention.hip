@@ -68,36 +68,6 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Waves per decode workgroup; each wave computes one 64-key block's record.
 constexpr int decode_waves = 4;
 
-// The lane's value, or -inf where DPP control Ctrl gives it no source lane
-// (or its row or bank is masked out).
-template <int Ctrl, int RowMask = 0xf, int BankMask = 0xf> __device__ __forceinline__ float dpp_or_minus_inf(float v)
-{
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-__builtin_inff()), __float_as_int(v), Ctrl,
-                                                      RowMask, BankMask, false));
-}
-
-// Inclusive scan of the running maximum over the wave's lanes with the merge
-// recurrence's own update (an earlier value stays unless it is smaller), on
-// DPP row shifts and row broadcasts: within each row of 16 lanes by shifts of
-// 1, 2, 4 and 8, then lane 15 into rows 1 and 3, then lane 31 into rows 2 and
-// 3. Associative for values without NaN.
-__device__ __forceinline__ float running_max_scan(float x)
-{
-    const auto keep = [](float earlier, float later) { return earlier < later ? later : earlier; };
-    x = keep(dpp_or_minus_inf<0x111>(x), x);
-    x = keep(dpp_or_minus_inf<0x112>(x), x);
-    x = keep(dpp_or_minus_inf<0x114>(x), x);
-    x = keep(dpp_or_minus_inf<0x118>(x), x);
-    x = keep(dpp_or_minus_inf<0x142, 0xa>(x), x);
-    x = keep(dpp_or_minus_inf<0x143, 0xc>(x), x);
-    return x;
-}
-
-// The previous lane's value (wave shift right by one); lane 0 gets `first`.
-__device__ __forceinline__ float previous_lane(float v, float first)
-{
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(first), __float_as_int(v), 0x138, 0xf, 0xf, false));
-}
 
 // Workgroups per (sequence, head) for a history of `blocks` key blocks.
 constexpr int decode_splits(int blocks)

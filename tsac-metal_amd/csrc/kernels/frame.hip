@@ -1668,10 +1668,56 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
     }
     else
     {
-        for (int b = 0; b < blocks; ++b)
+        // Lane b holds block b's maximum and total. Without NaN maxima the
+        // running maximum before each block is a scan with the recurrence's
+        // own update, so every block's factors come at once (block b's from
+        // lane b) and the ordered chain left is two fmas per block, with the
+        // factors broadcast from their lanes; with a NaN the plain loop runs.
+        const float maximum = lane < blocks ? partial[std::size_t(lane) * (2 + HW)] : -__builtin_inff();
+        const float block_total = lane < blocks ? partial[std::size_t(lane) * (2 + HW) + 1] : 0.0f;
+        if (__any(__builtin_isnan(maximum)))
         {
-            const float* record = partial + std::size_t(b) * (2 + HW);
-            merge(record[0], record[1], record + 2 + per_lane * lane);
+            for (int b = 0; b < blocks; ++b)
+            {
+                const float* record = partial + std::size_t(b) * (2 + HW);
+                merge(record[0], record[1], record + 2 + per_lane * lane);
+            }
+        }
+        else
+        {
+            const float running = previous_lane(running_max_scan(maximum), -__builtin_inff());
+            const float factor = original_exp(-__builtin_fabsf(maximum - running));
+            const float old_scale = running > maximum ? 1.0f : factor;
+            const float new_scale = running > maximum ? factor : 1.0f;
+            float sums[max_blocks][per_lane];
+#pragma unroll
+            for (int b = 0; b < max_blocks; ++b)
+            {
+                if (b < blocks)
+                {
+#pragma unroll
+                    for (int i = 0; i < per_lane; ++i)
+                    {
+                        sums[b][i] = partial[std::size_t(b) * (2 + HW) + 2 + per_lane * lane + i];
+                    }
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < max_blocks; ++b)
+            {
+                if (b < blocks)
+                {
+                    const float os = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(old_scale), b));
+                    const float ns = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(new_scale), b));
+                    const float bt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(block_total), b));
+                    total = __builtin_fmaf(bt, ns, total * os);
+#pragma unroll
+                    for (int i = 0; i < per_lane; ++i)
+                    {
+                        numerator[i] = __builtin_fmaf(sums[b][i], ns, numerator[i] * os);
+                    }
+                }
+            }
         }
     }
     const float reciprocal = 1.0f / total;
