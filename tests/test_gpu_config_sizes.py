@@ -88,7 +88,9 @@ def _stream_order(frames, batch, groups, books):
 @pytest.mark.timeout(900)
 def test_full_forward_reference_geometry_2580_frames(native, oracle, reference_model):
     """12 codebooks x 2580 frames, batch 3: encode pass == decode pass == oracle
-    at every position; GPU stream == oracle pack_normal; decode recovers the tokens."""
+    at every position; GPU stream == oracle pack_normal; decode recovers the tokens.
+    Contexts reach 860 keys, so past 512 the temporal attention runs in halves on
+    two workgroups (blocks 8-13 merged from the second half's records)."""
     from oracle import header
 
     model, hip_model = reference_model
