@@ -220,7 +220,7 @@ def gemm_roofline(torch, native, launches=20):
                      "TOP/s": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)})
         del linear, x, q, s, y
     head = rows[0]
-    return {"kernel": "gemm_kernel<true, Config<128, 2, 2, true>>", "bound": "mfma", "achieved": head["TOP/s"],
+    return {"kernel": "gemm_kernel<true, Config<64, 2, 3, true>> (K <= 512; Config<128, 2, 2, true> above)", "bound": "mfma", "achieved": head["TOP/s"],
             "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": head["frac"], "traffic": None,
             "avg_launch_us": head["us"], "shape": {"M": head["M"], "K": head["K"], "N": head["N"]},
             "shapes": rows}

@@ -198,6 +198,9 @@ template <int StageK, int Ring, int PerCU, bool Preload> struct Config
     static constexpr int lds_bytes = Ring * stage_bytes + scale_slots * scale_bytes + 2 * bias_bytes;
 };
 using Default = Config<128, 2, 2, true>;
+// K <= 512: three workgroups per CU on 64-deep stages, measured 2-5% faster on
+// the M = 30,960 K = 512 shapes (and slower at K = 2048).
+using ShortK = Config<64, 2, 3, true>;
 } // namespace gemm
 
 // One wavefront copies 64 x 16 bytes (or 64 x 4) from per-lane global addresses
@@ -638,7 +641,14 @@ void launch_gemm_config(const DeviceLinear& w, const int8_t* q, const float* sca
 void launch_gemm(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M, uint16_t* y,
                  const uint16_t* residual, Layout layout, hipStream_t stream)
 {
-    launch_gemm_config<gemm::Default>(w, q, scales, M, y, residual, layout, stream);
+    if (w.K <= 512)
+    {
+        launch_gemm_config<gemm::ShortK>(w, q, scales, M, y, residual, layout, stream);
+    }
+    else
+    {
+        launch_gemm_config<gemm::Default>(w, q, scales, M, y, residual, layout, stream);
+    }
 }
 } // namespace
 
