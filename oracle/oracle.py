@@ -479,12 +479,6 @@ class Reference(_Kernels, _DspKernels):
         lib.ref_gelu_table.argtypes = [u16p, sz]
         lib.ref_attention.argtypes = [u16p, u16p, u16p, sz, sz, sz, C.c_float, C.c_int, u16p]
         lib.ref_range_encode.argtypes = [f32p, u16p, sz, sz, u8p, sz, C.POINTER(sz)]
-        lib.ref_pack_normal.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u8p, sz,
-                                        C.POINTER(sz)]
-        lib.ref_unpack_normal.argtypes = [C.POINTER(ModelDesc), u8p, sz, u16p, sz, C.POINTER(sz)]
-        lib.ref_pack_normal_observed.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u8p, sz,
-                                                 C.POINTER(sz), C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]
-        lib.ref_distributions.argtypes = [C.POINTER(ModelDesc), C.POINTER(Header), u16p, sz, u16p]
         lib.ref_source_parse.argtypes = [u8p, sz, C.c_uint64, C.c_uint64, C.POINTER(sz)]
         lib.ref_source_dequantize.argtypes = [u8p, sz, C.c_char_p, f32p, sz]
         lib.ref_source_configs.argtypes = [u8p, sz] + [C.POINTER(C.c_uint)] * 3
@@ -585,46 +579,6 @@ class Reference(_Kernels, _DspKernels):
                                               p.shape[-1], ptr(out, C.c_uint8), out.size, C.byref(n)))
         return out[:n.value].tobytes()
 
-    def pack_normal(self, model, h: Header, tokens) -> bytes:
-        desc, keep = model_desc(model)
-        t = np.ascontiguousarray(tokens, np.uint16)
-        out = np.zeros(1 << 22, np.uint8)
-        n = sz()
-        self._check(self.lib.ref_pack_normal(C.byref(desc), C.byref(h), ptr(t, C.c_uint16), t.size,
-                                             ptr(out, C.c_uint8), out.size, C.byref(n)))
-        return out[:n.value].tobytes()
-
-    def pack_normal_observed(self, model, h: Header, tokens):
-        """The reference's pack_normal with an EntropyObserver recording each
-        symbol's position and after_symbol bit count in the order it sees them."""
-        desc, keep = model_desc(model)
-        t = np.ascontiguousarray(tokens, np.uint16)
-        out = np.zeros(1 << 22, np.uint8)
-        n = sz()
-        bits = np.zeros(max(t.size, 1), np.uint32)
-        positions = np.zeros((max(t.size, 1), 6), np.uint64)
-        self._check(self.lib.ref_pack_normal_observed(C.byref(desc), C.byref(h), ptr(t, C.c_uint16), t.size,
-                                                      ptr(out, C.c_uint8), out.size, C.byref(n),
-                                                      ptr(bits, C.c_uint32), ptr(positions, C.c_uint64)))
-        return out[:n.value].tobytes(), bits[:t.size], positions[:t.size]
-
-    def unpack_normal(self, model, data: bytes, capacity: int) -> np.ndarray:
-        desc, keep = model_desc(model)
-        b = np.frombuffer(data, np.uint8).copy()
-        out = np.zeros(max(capacity, 1), np.uint16)
-        n = sz()
-        self._check(self.lib.ref_unpack_normal(C.byref(desc), ptr(b, C.c_uint8), len(data),
-                                               ptr(out, C.c_uint16), out.size, C.byref(n)))
-        return out[:n.value]
-
-    def distributions(self, model, h: Header, tokens) -> np.ndarray:
-        desc, keep = model_desc(model)
-        t = np.ascontiguousarray(tokens, np.uint16)
-        out = np.zeros((t.size, model.geometry.alphabet), np.uint16)
-        self._check(self.lib.ref_distributions(C.byref(desc), C.byref(h), ptr(t, C.c_uint16), t.size,
-                                               ptr(out, C.c_uint16)))
-        return out
-
 
 def host_threads() -> int:
     return len(os.sched_getaffinity(0))
@@ -723,3 +677,221 @@ class OracleDacModel:
                                                          ptr(tokens, C.c_uint16), frames, groups, chunk, threads,
                                                          ptr(pcm, C.c_float)))
         return pcm
+
+
+# ---------------------------------------------------------------- the reference's composition
+
+COMPOSITION_PATH = HERE / "_ref" / "libtsacmodel.so"
+PACKED_PATH = HERE / "_ref" / "gen" / "pack"
+
+
+class ReferenceComposition:
+    """The reference's own CpuTransformer<scalar::Kernels> + TransformerPredictor +
+    pack_normal/unpack_normal, DacAnalysis, DacSynthesis, RvqEncoder and
+    RvqDecoder (oracle/ref_model.cpp), reading the seeded models of
+    seeded_models.py from the files the reference's packer wrote."""
+
+    def __init__(self):
+        self.lib = lib = _load(COMPOSITION_PATH)
+        lib.refm_last_error.restype = C.c_char_p
+        vp, hp, u, cp, szp = C.c_void_p, C.POINTER(Header), C.c_uint, C.c_char_p, C.POINTER(sz)
+        lib.refm_transformer_open.argtypes = [cp, u, u, sz, C.POINTER(vp)]
+        lib.refm_transformer_close.argtypes = [vp]
+        lib.refm_transformer_projection.argtypes = [vp, u, i8p, f32p, f32p, szp, szp]
+        lib.refm_transformer_norm.argtypes = [vp, u, u16p, u16p]
+        lib.refm_transformer_constants.argtypes = [vp, u16p, u16p, u16p]
+        lib.refm_pack_normal.argtypes = [vp, hp, u16p, sz, u, u8p, sz, szp]
+        lib.refm_pack_normal_observed.argtypes = [vp, hp, u16p, sz, u8p, sz, szp, C.POINTER(C.c_uint32),
+                                                  C.POINTER(C.c_uint64)]
+        lib.refm_unpack_normal.argtypes = [vp, u8p, sz, u, u16p, sz, szp]
+        lib.refm_distributions.argtypes = [vp, hp, u16p, sz, u, u16p]
+        lib.refm_dac_open.argtypes = [cp, u, u, C.POINTER(vp)]
+        lib.refm_dac_close.argtypes = [vp]
+        lib.refm_dac_analysis.argtypes = [vp, f32p, sz, sz, sz, f32p]
+        lib.refm_dac_synthesis.argtypes = [vp, f32p, sz, sz, sz, f32p]
+        lib.refm_rvq_encode.argtypes = [vp, hp, f32p, u16p]
+        lib.refm_rvq_decode.argtypes = [vp, hp, u16p, f32p]
+        lib.refm_dac_convolution.argtypes = [vp, C.c_int, u, u8p, szp, szp, f32p, szp, f32p, szp]
+        lib.refm_dac_activation.argtypes = [vp, C.c_int, u, f32p, szp]
+        lib.refm_rvq_tensors.argtypes = [vp, u] + [f32p] * 6
+        self.directory = str(PACKED_PATH).encode()
+
+    @staticmethod
+    def available() -> bool:
+        return COMPOSITION_PATH.exists() and (PACKED_PATH / "adapter_offsets.hpp").exists()
+
+    def _check(self, status):
+        if status:
+            raise OracleError(self.lib.refm_last_error().decode())
+
+    def transformer(self, channels: int, books: int, cache_bytes: int = 0) -> "ReferenceTransformer":
+        return ReferenceTransformer(self, channels, books, cache_bytes)
+
+    def dac(self, channels: int, books: int) -> "ReferenceDac":
+        return ReferenceDac(self, channels, books)
+
+
+class _Handle:
+    def __init__(self, owner: ReferenceComposition, close):
+        self.owner, self.lib, self.handle = owner, owner.lib, C.c_void_p()
+        self._close = close
+
+    def close(self):
+        if self.handle:
+            self._close(self.handle)
+            self.handle = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ReferenceTransformer(_Handle):
+    def __init__(self, owner, channels, books, cache_bytes):
+        super().__init__(owner, owner.lib.refm_transformer_close)
+        self.books = books
+        owner._check(self.lib.refm_transformer_open(owner.directory, channels, books, sz(cache_bytes),
+                                                    C.byref(self.handle)))
+
+    def projection(self, index: int):
+        k, n = sz(), sz()
+        self.owner._check(self.lib.refm_transformer_projection(self.handle, index, None, None, None,
+                                                               C.byref(k), C.byref(n)))
+        values = np.zeros((n.value, k.value), np.int8)
+        scales = np.zeros((k.value // 256, n.value), np.float32)
+        bias = np.zeros(n.value, np.float32)
+        self.owner._check(self.lib.refm_transformer_projection(
+            self.handle, index, ptr(values, C.c_int8), ptr(scales, C.c_float), ptr(bias, C.c_float),
+            C.byref(k), C.byref(n)))
+        return values, scales, bias
+
+    def norm(self, index: int):
+        gain, bias = np.zeros(512, np.uint16), np.zeros(512, np.uint16)
+        self.owner._check(self.lib.refm_transformer_norm(self.handle, index, ptr(gain, C.c_uint16),
+                                                         ptr(bias, C.c_uint16)))
+        return gain, bias
+
+    def constants(self):
+        positions = np.zeros((self.books, 512), np.uint16)
+        rotations = np.zeros((1024, 128), np.uint16)
+        embeddings = np.zeros((self.books, 1024, 1024), np.uint16)
+        self.owner._check(self.lib.refm_transformer_constants(self.handle, ptr(positions, C.c_uint16),
+                                                              ptr(rotations, C.c_uint16),
+                                                              ptr(embeddings, C.c_uint16)))
+        return positions, rotations, embeddings
+
+    def pack_normal(self, h: Header, tokens, threads: int = 1) -> bytes:
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out = np.zeros(64 + 24 * t.size, np.uint8)  # up to 10 15-bit decisions per symbol
+        n = sz()
+        self.owner._check(self.lib.refm_pack_normal(self.handle, C.byref(h), ptr(t, C.c_uint16), t.size, threads,
+                                                    ptr(out, C.c_uint8), out.size, C.byref(n)))
+        return out[:n.value].tobytes()
+
+    def pack_normal_observed(self, h: Header, tokens):
+        """pack_normal with an EntropyObserver recording, per symbol in the order it
+        sees them, before_symbol's position and after_symbol's bit count."""
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out = np.zeros(64 + 24 * t.size, np.uint8)
+        n = sz()
+        bits = np.zeros(max(t.size, 1), np.uint32)
+        positions = np.zeros((max(t.size, 1), 6), np.uint64)
+        self.owner._check(self.lib.refm_pack_normal_observed(
+            self.handle, C.byref(h), ptr(t, C.c_uint16), t.size, ptr(out, C.c_uint8), out.size, C.byref(n),
+            ptr(bits, C.c_uint32), ptr(positions, C.c_uint64)))
+        return out[:n.value].tobytes(), bits[:t.size], positions[:t.size]
+
+    def unpack_normal(self, data: bytes, capacity: int, threads: int = 1) -> np.ndarray:
+        b = np.frombuffer(data, np.uint8).copy()
+        out = np.zeros(max(capacity, 1), np.uint16)
+        n = sz()
+        self.owner._check(self.lib.refm_unpack_normal(self.handle, ptr(b, C.c_uint8), len(data), threads,
+                                                      ptr(out, C.c_uint16), out.size, C.byref(n)))
+        return out[:n.value]
+
+    def distributions(self, h: Header, tokens, threads: int = 1) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.uint16)
+        out = np.zeros((t.size, 1024), np.uint16)
+        self.owner._check(self.lib.refm_distributions(self.handle, C.byref(h), ptr(t, C.c_uint16), t.size,
+                                                      threads, ptr(out, C.c_uint16)))
+        return out
+
+
+class ReferenceDac(_Handle):
+    def __init__(self, owner, channels, books):
+        super().__init__(owner, owner.lib.refm_dac_close)
+        self.channels, self.books = channels, books
+        owner._check(self.lib.refm_dac_open(owner.directory, channels, books, C.byref(self.handle)))
+
+    def analysis(self, pcm, samples: int, groups: int = 1, chunk: int = 0) -> np.ndarray:
+        """PCM [groups][samples][channels] -> latent [groups][samples/512][1024]."""
+        x = _f32(pcm)
+        assert x.size == groups * samples * self.channels
+        out = np.zeros(groups * (samples // 512) * 1024, np.float32)
+        self.owner._check(self.lib.refm_dac_analysis(self.handle, ptr(x, C.c_float), samples, groups, chunk,
+                                                     ptr(out, C.c_float)))
+        return out
+
+    def synthesis(self, latent, frames: int, groups: int = 1, chunk: int = 0) -> np.ndarray:
+        """Latent [groups][frames][1024] -> PCM [groups][frames*512][channels]."""
+        x = _f32(latent)
+        assert x.size == groups * frames * 1024
+        out = np.zeros(groups * frames * 512 * self.channels, np.float32)
+        self.owner._check(self.lib.refm_dac_synthesis(self.handle, ptr(x, C.c_float), frames, groups, chunk,
+                                                      ptr(out, C.c_float)))
+        return out
+
+    def rvq_encode(self, latent, frames: int, groups: int = 1) -> np.ndarray:
+        """Latent [groups][frames][1024] -> tokens [frame][group][book]."""
+        x = _f32(latent)
+        h = header(frames, 1, groups, self.books, model_channels=self.channels)
+        out = np.zeros(frames * groups * self.books, np.uint16)
+        self.owner._check(self.lib.refm_rvq_encode(self.handle, C.byref(h), ptr(x, C.c_float),
+                                                   ptr(out, C.c_uint16)))
+        return out
+
+    def rvq_decode(self, tokens, frames: int, groups: int = 1) -> np.ndarray:
+        """Tokens [frame][group][book] -> latent [groups][frames][1024]."""
+        t = np.ascontiguousarray(tokens, np.uint16)
+        h = header(frames, 1, groups, self.books, model_channels=self.channels)
+        out = np.zeros(groups * frames * 1024, np.float32)
+        self.owner._check(self.lib.refm_rvq_decode(self.handle, C.byref(h), ptr(t, C.c_uint16),
+                                                   ptr(out, C.c_float)))
+        return out
+
+    def convolution(self, synthesis: bool, index: int):
+        """(payload bytes, data-plane bytes, gains, biases) as the DAC model adapter reads them."""
+        pb, dp, ng, nb = sz(), sz(), sz(), sz()
+        args = (self.handle, int(synthesis), index)
+        self.owner._check(self.lib.refm_dac_convolution(*args, None, C.byref(pb), C.byref(dp), None,
+                                                        C.byref(ng), None, C.byref(nb)))
+        payload = np.zeros(pb.value, np.uint8)
+        gains, biases = np.zeros(ng.value, np.float32), np.zeros(nb.value, np.float32)
+        self.owner._check(self.lib.refm_dac_convolution(*args, ptr(payload, C.c_uint8), C.byref(pb), C.byref(dp),
+                                                        ptr(gains, C.c_float), C.byref(ng),
+                                                        ptr(biases, C.c_float), C.byref(nb)))
+        return payload, dp.value, gains, biases
+
+    def activation(self, synthesis: bool, index: int) -> np.ndarray:
+        n = sz()
+        self.owner._check(self.lib.refm_dac_activation(self.handle, int(synthesis), index, None, C.byref(n)))
+        out = np.zeros(n.value, np.float32)
+        self.owner._check(self.lib.refm_dac_activation(self.handle, int(synthesis), index, ptr(out, C.c_float),
+                                                       C.byref(n)))
+        return out
+
+    def rvq_tensors(self, book: int):
+        """codebook [1024][8], search [1024][8], input projection [1024 in][8 out]
+        (input-major), input bias [8], output projection [8][1024], output bias [1024]."""
+        arrays = (np.zeros((1024, 8), np.float32), np.zeros((1024, 8), np.float32), np.zeros((1024, 8), np.float32),
+                  np.zeros(8, np.float32), np.zeros((8, 1024), np.float32), np.zeros(1024, np.float32))
+        self.owner._check(self.lib.refm_rvq_tensors(self.handle, book, *(ptr(a, C.c_float) for a in arrays)))
+        return arrays

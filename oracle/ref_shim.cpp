@@ -1,13 +1,9 @@
-// TEST INFRASTRUCTURE ONLY. A C-ABI over the reference's own scalar sources,
+// TEST INFRASTRUCTURE ONLY. A C-ABI over the reference's own scalar kernels,
+// numerics, range coder, source-file reader, audio files and command line,
 // compiled where they lie under the reference tree by oracle/Makefile into
-// oracle/_ref/libtsacref.so. Tests use it to pin the C oracle; nothing else
-// loads it.
-//
-// The reference's composition class (CpuTransformer, src/common/cpu_transformer.tpp)
-// is not buildable here: it needs TransformerModel, whose sources need the
-// generated adapter_offsets.hpp. RefBackend below therefore assembles the same
-// layer sequence from the reference's compiled kernels and plugs it into the
-// reference's own TransformerPredictor / pack_normal / unpack_normal.
+// oracle/_ref/libtsacref.so. Tests use it to pin the C oracle function by
+// function; nothing else loads it. The reference's composition classes
+// (CpuTransformer, the DAC graphs, the quantizer) are in ref_model.cpp.
 #include "common/numeric.hpp"
 #include "common/numeric/probability.hpp"
 #include "common/probability.hpp"
@@ -104,209 +100,6 @@ struct RefLinear
                 std::span(y).subspan(c * output, output));
     }
 };
-
-struct RefBackend final : TransformerBackend
-{
-    orc_geometry g;
-    std::vector<RefLinear> linears;
-    std::vector<std::vector<std::uint16_t>> gain, bias;
-    std::vector<std::uint16_t> positions, rotations, embeddings;
-    Header header;
-
-    struct Lane
-    {
-        std::vector<std::vector<std::uint16_t>> tk, tv, ck, cv;
-        std::vector<std::uint16_t> conditioning, input, prefix, prefix_tokens, logits, distribution;
-        std::vector<float> probabilities, exponents;
-    };
-    std::vector<Lane> lanes;
-
-    explicit RefBackend(const orc_model_desc& d) : g(d.geometry)
-    {
-        const std::size_t stacked = 4 * std::size_t(g.temporal_layers + g.codebook_layers);
-        for (std::size_t i = 0; i < stacked + 3; ++i)
-        {
-            std::size_t k, n;
-            if (i == stacked || i == stacked + 1)
-                k = g.latent, n = g.width;
-            else if (i == stacked + 2)
-                k = g.width, n = g.alphabet;
-            else
-                switch (i % 4)
-                {
-                case 0:
-                    k = g.width, n = 3 * std::size_t(g.width);
-                    break;
-                case 1:
-                    k = g.width, n = g.width;
-                    break;
-                case 2:
-                    k = g.width, n = g.ffn;
-                    break;
-                default:
-                    k = g.ffn, n = g.width;
-                }
-            linears.emplace_back(d.projections[i], k, n);
-        }
-        const std::size_t norms = 2 * std::size_t(g.temporal_layers + g.codebook_layers) + 2;
-        for (std::size_t i = 0; i < norms; ++i)
-        {
-            gain.emplace_back(d.norm_gain[i], d.norm_gain[i] + g.width);
-            bias.emplace_back(d.norm_bias[i], d.norm_bias[i] + g.width);
-        }
-        positions.assign(d.positions, d.positions + std::size_t(g.books) * g.width);
-        rotations.assign(d.rotations, d.rotations + std::size_t(g.context) * g.head_width);
-        embeddings.assign(d.embeddings,
-                          d.embeddings + std::size_t(g.books) * g.alphabet * g.latent);
-    }
-
-    bool independent_lanes() const override
-    {
-        return true;
-    }
-
-    void reset(const Header& h, std::size_t count) override
-    {
-        validate_header(h);
-        header = h;
-        lanes.assign(count, {});
-        for (auto& l : lanes)
-        {
-            l.tk.resize(g.temporal_layers);
-            l.tv.resize(g.temporal_layers);
-            l.ck.resize(g.codebook_layers);
-            l.cv.resize(g.codebook_layers);
-        }
-    }
-
-    void reset_temporal(std::size_t lane) override
-    {
-        for (auto& k : lanes.at(lane).tk)
-            k.clear();
-        for (auto& v : lanes.at(lane).tv)
-            v.clear();
-    }
-
-    void reset_codebook(std::size_t lane) override
-    {
-        auto& l = lanes.at(lane);
-        l.prefix_tokens.clear();
-        for (auto& k : l.ck)
-            k.clear();
-        for (auto& v : l.cv)
-            v.clear();
-    }
-
-    void embed(std::span<const std::uint16_t> tokens, std::vector<std::uint16_t>& out) const
-    {
-        out.resize(g.latent);
-        for (std::size_t book = 0; book < tokens.size(); ++book)
-        {
-            const auto e = std::span(embeddings)
-                               .subspan((book * g.alphabet + tokens[book]) * g.latent, g.latent);
-            if (book == 0)
-                std::copy(e.begin(), e.end(), out.begin());
-            else
-                scalar::add_bf16(out, e);
-        }
-    }
-
-    // Layer sequence of TransformerGraph::evaluate_stack (src/common/cpu_transformer.tpp:133-175).
-    void stack(bool temporal, std::vector<std::uint16_t>& input, std::size_t position,
-               const std::uint16_t* rotation, bool replay,
-               std::vector<std::vector<std::uint16_t>>& keys,
-               std::vector<std::vector<std::uint16_t>>& values) const
-    {
-        const std::size_t w = g.width, hw = g.head_width;
-        const std::size_t layers = temporal ? g.temporal_layers : g.codebook_layers;
-        const std::size_t pbase = temporal ? 0 : 4 * std::size_t(g.temporal_layers);
-        const std::size_t nbase = temporal ? 0 : 2 * std::size_t(g.temporal_layers) + 1;
-        std::vector<std::uint16_t> normalized(w), qkv, query, key, projected, mlp;
-        std::vector<float> v(w), sq(w);
-        AttentionWorkspace workspace;
-        for (std::size_t i = 0; i < layers; ++i)
-        {
-            const std::size_t p = pbase + 4 * i, n = nbase + 2 * i;
-            probability_layer_norm_bf16_into(input, gain[n], bias[n], normalized, v, sq);
-            linears[p].apply(normalized, qkv);
-            query.assign(qkv.begin(), qkv.begin() + w);
-            key.assign(qkv.begin() + w, qkv.begin() + 2 * w);
-            if (rotation)
-            {
-                const std::span<const std::uint16_t> c(rotation, hw);
-                for (std::size_t head = 0; head < g.heads; ++head)
-                {
-                    auto qh = std::span(query).subspan(head * hw, hw);
-                    auto kh = std::span(key).subspan(head * hw, hw);
-                    probability_rotary_bf16_into(qh, c, qh);
-                    probability_rotary_bf16_into(kh, c, kh);
-                }
-            }
-            detail::require(keys[i].size() == position * w, "cache position mismatch");
-            keys[i].insert(keys[i].end(), key.begin(), key.end());
-            values[i].insert(values[i].end(), qkv.begin() + 2 * w, qkv.end());
-            scalar::attention_bf16_into(query, keys[i], values[i], workspace, g.heads, hw,
-                                        g.attention_scale, replay, false);
-            linears[p + 1].apply(workspace.output, projected);
-            scalar::add_bf16(input, projected);
-            probability_layer_norm_bf16_into(input, gain[n + 1], bias[n + 1], normalized, v, sq);
-            linears[p + 2].apply(normalized, mlp);
-            probability_gelu_bf16(std::span(mlp));
-            linears[p + 3].apply(mlp, projected);
-            scalar::add_bf16(input, projected);
-        }
-        const std::size_t f = nbase + 2 * layers;
-        probability_layer_norm_bf16_into(input, gain[f], bias[f], input, v, sq);
-    }
-
-    void temporal_step(std::size_t lane, std::size_t position,
-                       std::span<const std::uint16_t> feedback, bool replay) override
-    {
-        auto& l = lanes.at(lane);
-        std::vector<std::uint16_t> embedded;
-        embed(feedback, embedded);
-        const std::size_t stacked = 4 * std::size_t(g.temporal_layers + g.codebook_layers);
-        linears[stacked].apply(embedded, l.conditioning);
-        stack(true, l.conditioning, position, rotations.data() + position * g.head_width, replay,
-              l.tk, l.tv);
-    }
-
-    std::span<const float> codebook_step(std::size_t lane, std::size_t book,
-                                         std::span<const std::uint16_t> prefix) override
-    {
-        auto& l = lanes.at(lane);
-        const std::size_t stacked = 4 * std::size_t(g.temporal_layers + g.codebook_layers);
-        if (book == 0)
-            l.input = l.conditioning;
-        else
-        {
-            embed(prefix, l.prefix);
-            linears[stacked + 1].apply(l.prefix, l.input);
-        }
-        scalar::add_bf16(l.input, std::span(positions).subspan(book * g.width, g.width));
-        stack(false, l.input, book, nullptr, false, l.ck, l.cv);
-        linears[stacked + 2].apply(l.input, l.logits);
-        l.distribution.resize(g.alphabet);
-        l.exponents.resize(g.alphabet);
-        probability_softmax_bf16_into(l.logits, l.distribution, l.exponents);
-        l.probabilities.resize(g.alphabet);
-        std::transform(l.distribution.begin(), l.distribution.end(), l.probabilities.begin(),
-                       probability_float);
-        return l.probabilities;
-    }
-};
-
-Header header_of(const orc_header& h)
-{
-    Header r;
-    r.method = h.method;
-    r.groups = h.groups;
-    r.model_channels = h.model_channels;
-    r.codebooks = h.codebooks;
-    r.frames = h.frames;
-    r.batch = h.batch;
-    return r;
-}
 
 } // namespace
 
@@ -456,103 +249,6 @@ int ref_range_encode(const float* probabilities, const std::uint16_t* symbols, s
             detail::require(bytes.size() <= capacity, "capacity");
             std::memcpy(out, bytes.data(), bytes.size());
             *written = bytes.size();
-        });
-}
-
-int ref_pack_normal(const orc_model_desc* desc, const orc_header* header,
-                    const std::uint16_t* tokens, std::size_t count, std::uint8_t* out,
-                    std::size_t capacity, std::size_t* written)
-{
-    return guarded(
-        [&]
-        {
-            RefBackend backend(*desc);
-            TransformerPredictor predictor(backend);
-            const auto bytes = pack_normal(header_of(*header), std::span(tokens, count), predictor);
-            detail::require(bytes.size() <= capacity, "capacity");
-            std::memcpy(out, bytes.data(), bytes.size());
-            *written = bytes.size();
-        });
-}
-
-// The reference's pack_normal with an EntropyObserver that records, per symbol
-// in the order the observer sees them, before_symbol's position and
-// after_symbol's bit count (src/format/entropy.cpp:86-100).
-int ref_pack_normal_observed(const orc_model_desc* desc, const orc_header* header,
-                             const std::uint16_t* tokens, std::size_t count, std::uint8_t* out,
-                             std::size_t capacity, std::size_t* written, std::uint32_t* bits,
-                             std::uint64_t* positions)
-{
-    return guarded(
-        [&]
-        {
-            RefBackend backend(*desc);
-            TransformerPredictor predictor(backend);
-            std::size_t before = 0, after = 0;
-            EntropyObserver observer{
-                [&](const EntropyPosition& p)
-                {
-                    detail::require(before == after && before < count, "observer order");
-                    std::uint64_t* r = positions + 6 * before;
-                    r[0] = p.frame;
-                    r[1] = p.group;
-                    r[2] = p.codebook;
-                    r[3] = p.lane;
-                    r[4] = p.step;
-                    r[5] = p.token_offset;
-                    ++before;
-                },
-                [&](const EntropyPosition& p, std::size_t n)
-                {
-                    detail::require(after + 1 == before && positions[6 * after + 5] == p.token_offset,
-                                    "observer order");
-                    bits[after++] = static_cast<std::uint32_t>(n);
-                }};
-            const auto bytes =
-                pack_normal(header_of(*header), std::span(tokens, count), predictor, Limits{}, observer);
-            detail::require(bytes.size() <= capacity && after == count, "capacity");
-            std::memcpy(out, bytes.data(), bytes.size());
-            *written = bytes.size();
-        });
-}
-
-int ref_unpack_normal(const orc_model_desc* desc, const std::uint8_t* bytes, std::size_t length,
-                      std::uint16_t* tokens, std::size_t capacity, std::size_t* count)
-{
-    return guarded(
-        [&]
-        {
-            RefBackend backend(*desc);
-            TransformerPredictor predictor(backend);
-            const auto t = unpack_normal(ByteView(bytes, length), predictor);
-            detail::require(t.size() <= capacity, "capacity");
-            std::memcpy(tokens, t.data(), t.size() * 2);
-            *count = t.size();
-        });
-}
-
-int ref_distributions(const orc_model_desc* desc, const orc_header* header,
-                      const std::uint16_t* tokens, std::size_t count, std::uint16_t* out)
-{
-    return guarded(
-        [&]
-        {
-            RefBackend backend(*desc);
-            TransformerPredictor predictor(backend);
-            auto h = header_of(*header);
-            h.method = 1;
-            detail::require(count == h.symbol_count(), "token count");
-            predictor.reset(h);
-            const auto alphabet = desc->geometry.alphabet;
-            visit_entropy_positions(h,
-                                    [&](const EntropyPosition& p)
-                                    {
-                                        const auto probs = predictor.predict(p);
-                                        for (std::size_t i = 0; i < alphabet; ++i)
-                                            out[p.token_offset * alphabet + i] =
-                                                probability_bf16(probs[i]);
-                                        predictor.commit(p, tokens[p.token_offset]);
-                                    });
         });
 }
 

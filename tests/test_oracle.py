@@ -301,6 +301,12 @@ def test_range_coder_matches_reference_and_round_trips(oracle, reference):
 
 
 # ---------------------------------------------------------------- composition
+#
+# The oracle's layer sequence, predictor schedule, rollover and stream order are
+# pinned against the reference's own CpuTransformer and pack_normal at the
+# reference geometry in test_reference_composition.py (and, through committed
+# reference streams, on the GPU). Here: the oracle's own invariants at reduced
+# widths, which the GPU tests use as shapes.
 
 SMALL = Geometry(width=256, heads=2, head_width=128, ffn=512, temporal_layers=2, codebook_layers=1,
                  latent=256)
@@ -313,51 +319,17 @@ def small_model():
 
 @pytest.mark.parametrize("frames,batch,groups,books", [(17, 8, 16, 12), (101, 3, 1, 12), (35, 3, 2, 12),
                                                        (17, 1, 1, 12), (3, 8, 2, 12), (5, 3, 1, 7)])
-def test_pack_normal_matches_reference(oracle, reference, small_model, frames, batch, groups, books):
-    """Whole-stream byte equality for the reference test shapes
-    (tests/metal_optimized.cpp:255-293) at a reduced width."""
+def test_pack_unpack_round_trip(oracle, small_model, frames, batch, groups, books):
+    """unpack_normal(pack_normal(t)) == t, with lanes prepared on several threads
+    or one (the stream does not depend on the lane executor)."""
     from oracle import header
 
     h = header(frames, batch, groups, books)
     tokens = pattern_tokens(frames * groups * books)
     om = oracle.model(small_model)
     stream = om.pack_normal(h, tokens, threads=3)
-    assert stream == reference.pack_normal(small_model, h, tokens)
+    assert stream == om.pack_normal(h, tokens, threads=1)
     assert np.array_equal(om.unpack_normal(stream, threads=2), tokens)
-
-
-@pytest.mark.parametrize("frames,batch,groups,books", [(17, 3, 1, 12), (35, 3, 2, 12), (3, 8, 2, 12)])
-def test_observer_bits_and_order_match_reference(oracle, reference, small_model, frames, batch, groups, books):
-    """What an EntropyObserver sees during pack_normal: the position of every
-    symbol in the order the reference's own pack_normal visits them and the bits
-    after_symbol reports (RangeEncoder::bit_position deltas, src/format/entropy.cpp:86-100)."""
-    from oracle import header
-
-    h = header(frames, batch, groups, books)
-    tokens = pattern_tokens(frames * groups * books)
-    stream, bits, positions = oracle.model(small_model).pack_normal_observed(h, tokens, threads=2)
-    ref_stream, ref_bits, ref_positions = reference.pack_normal_observed(small_model, h, tokens)
-    assert stream == ref_stream
-    assert np.array_equal(positions, ref_positions)
-    assert np.array_equal(bits, ref_bits)
-    # Every token appears once; the bits add up to the payload's arithmetic length.
-    assert sorted(positions[:, 5].tolist()) == list(range(tokens.size))
-    payload_bits = (len(stream) - 18) * 8
-    assert payload_bits - 32 <= int(bits.sum()) <= payload_bits
-
-
-def test_rollover_replay_matches_reference(oracle, reference):
-    """1026 frames in one lane crosses the 1024-position context: the last 256
-    frames are replayed with replay rounding (src/common/transformer.cpp:187-203)."""
-    from oracle import header
-
-    tiny = Geometry(width=256, heads=2, head_width=128, ffn=256, temporal_layers=1, codebook_layers=1,
-                    latent=256)
-    model = random_model(tiny, seed=5)
-    h = header(1026, 1, 1, 1)
-    tokens = pattern_tokens(1026)
-    stream = oracle.model(model).pack_normal(h, tokens)
-    assert stream == reference.pack_normal(model, h, tokens)
 
 
 def test_decode_rejects_corrupt_crc(oracle, small_model):
@@ -370,15 +342,3 @@ def test_decode_rejects_corrupt_crc(oracle, small_model):
     stream[-1] ^= 1
     with pytest.raises(OracleError, match="CRC"):
         om.unpack_normal(bytes(stream))
-
-
-def test_distributions_match_reference_reference_geometry(oracle, reference):
-    """Full reference geometry (12+3 layers, 512 wide, 4x128) on a short stream."""
-    from oracle import header
-
-    model = random_model(seed=1)
-    h = header(4, 3, 1, 12)
-    tokens = pattern_tokens(4 * 12)
-    a = oracle.model(model).distributions(h, tokens, threads=3)
-    assert np.array_equal(a, reference.distributions(model, h, tokens))
-    assert np.all(np.isfinite(bf16_float(a)))

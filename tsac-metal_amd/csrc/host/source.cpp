@@ -54,21 +54,23 @@ std::size_t block_rows(Storage s)
     return s == Storage::bf8 ? 32 : 256;
 }
 
-// Scale-plane geometry of a quantized tensor: axis 0 in blocks, axis 1 padded
-// to a multiple of 8, the remaining axes as outer slices.
+// Where a quantized tensor's BF16 scales sit: one scale per `block` values of
+// axis 0, for each column of axis 1 (the column count rounded up to 8 in the
+// plane), repeated for every slice of the remaining axes.
 struct ScalePlane
 {
-    std::size_t rows, columns, outer, block, padded;
+    std::size_t rows, columns, slices, block, stride;
     std::size_t elements() const
     {
-        return checked_mul(checked_mul(rows / block, padded), outer);
+        return checked_mul(checked_mul(rows / block, stride), slices);
     }
 };
 
 ScalePlane scale_plane(const SourceTensor& t)
 {
     const std::size_t block = block_rows(t.storage);
-    require(t.dims.size() >= 2 && t.dims[0] % block == 0, "unsupported quantized tensor shape");
+    require(t.dims.size() >= 2 && t.dims[0] % block == 0,
+            "a quantized tensor needs two or more axes, the first a whole number of scale blocks");
     return {t.dims[0], t.dims[1], t.elements / t.dims[0] / t.dims[1], block, align_to(t.dims[1], 8)};
 }
 
@@ -214,13 +216,13 @@ std::vector<float> SourceModel::dequantize(std::string_view name) const
         // value[(o*columns + c)*rows + b*block + r] = int8 * scale[(o*rows/block + b)*padded + c]
         const ScalePlane s = scale_plane(t);
         const std::size_t blocks = s.rows / s.block;
-        for (std::size_t o = 0; o < s.outer; ++o)
+        for (std::size_t o = 0; o < s.slices; ++o)
         {
             for (std::size_t c = 0; c < s.columns; ++c)
             {
                 for (std::size_t b = 0; b < blocks; ++b)
                 {
-                    const float scale = widen_bf16(payload_u16(p, t.data_plane_bytes + 2 * ((o * blocks + b) * s.padded + c)));
+                    const float scale = widen_bf16(payload_u16(p, t.data_plane_bytes + 2 * ((o * blocks + b) * s.stride + c)));
                     const std::size_t first = (o * s.columns + c) * s.rows + b * s.block;
                     for (std::size_t r = 0; r < s.block; ++r)
                     {

@@ -131,116 +131,117 @@ std::vector<uint8_t> pcm16_wave(const float* samples, std::size_t frames, unsign
 
 // ---------------------------------------------------------------- options
 
+namespace
+{
+// One command-line option: its single-letter spelling (0 if none), its long
+// spelling (empty if none), whether it consumes the next argument as an
+// integer, and what it sets. The accepted spellings and their meanings are the
+// reference command line's (src/cli.cpp:50-90).
+struct OptionSpec
+{
+    char letter;
+    std::string_view word;
+    bool integer;
+    void (*apply)(CliOptions&, int);
+};
+
+constexpr OptionSpec option_table[] = {
+    {'h', "--help", false, [](CliOptions& o, int) { o.help = true; }},
+    {'f', "--fast", false, [](CliOptions& o, int) { o.fast = true; }},
+    {'s', "--separate_channels", false, [](CliOptions& o, int) { o.separate = true; }},
+    {'v', "", false, [](CliOptions& o, int) { ++o.verbose; }},
+    {'T', "", true, [](CliOptions& o, int v) { o.threads = v; }},
+    {'q', "--n_codebooks", true, [](CliOptions& o, int v) { o.quality = v; }},
+    {'c', "--channels", true, [](CliOptions& o, int v) { o.channels = v; }},
+    {0, "--batch_size", true, [](CliOptions& o, int v) { o.batch = v; }},
+    {0, "--metal", false, [](CliOptions& o, int) { o.metal = true; }},
+};
+
+std::string spelling(const OptionSpec& spec)
+{
+    return spec.word.empty() ? std::string{'-', spec.letter} : std::string(spec.word);
+}
+
+const OptionSpec& by_word(std::string_view word)
+{
+    for (const auto& spec : option_table)
+        if (!spec.word.empty() && spec.word == word)
+            return spec;
+    throw Error("unrecognised option " + std::string(word));
+}
+
+const OptionSpec& by_letter(char letter)
+{
+    for (const auto& spec : option_table)
+        if (spec.letter && spec.letter == letter)
+            return spec;
+    throw Error(std::string("unrecognised option -") + letter);
+}
+
+// A decimal int, optionally written with a leading '+', filling the whole argument.
+int integer_value(const OptionSpec& spec, std::string_view text)
+{
+    const std::string_view digits = text.substr(text.starts_with('+') ? 1 : 0);
+    int value = 0;
+    const auto [end, status] = std::from_chars(digits.data(), digits.data() + digits.size(), value);
+    if (digits.empty() || status != std::errc{} || end != digits.data() + digits.size())
+        throw Error(spelling(spec) + " takes an integer; '" + std::string(text) + "' is not one");
+    return value;
+}
+} // namespace
+
 CliOptions parse_cli(const std::vector<std::string_view>& arguments)
 {
     CliOptions o;
-    std::vector<std::string_view> positional;
-    for (std::size_t i = 0; i < arguments.size(); ++i)
+    std::vector<std::string_view> operands;
+    std::size_t cursor = 0;
+    while (cursor < arguments.size() && !o.help)
     {
-        const std::string_view arg = arguments[i];
-        if (arg == "--")
+        const std::string_view word = arguments[cursor++];
+        if (word == "--")
         {
-            positional.insert(positional.end(), arguments.begin() + std::ptrdiff_t(i + 1), arguments.end());
+            operands.insert(operands.end(), arguments.begin() + std::ptrdiff_t(cursor), arguments.end());
             break;
         }
-        if (arg.size() <= 1 || arg[0] != '-')
+        if (word.size() < 2 || word.front() != '-')
         {
-            positional.push_back(arg);
+            operands.push_back(word);
             continue;
         }
-        const auto integer = [&](std::string_view name) -> int
-        {
-            require(++i < arguments.size(), ("option '" + std::string(name) + "' must have an argument").c_str());
-            std::string_view text = arguments[i];
-            if (text.starts_with('+'))
-            {
-                text.remove_prefix(1);
-            }
-            int value = 0;
-            const auto parsed = std::from_chars(text.data(), text.data() + text.size(), value);
-            if (text.empty() || parsed.ec != std::errc{} || parsed.ptr != text.data() + text.size())
-            {
-                const std::string_view shown = name == "-q" ? "--n_codebooks" : name == "-c" ? "--channels" : name;
-                throw Error("option " + std::string(shown) + " expects an integer");
-            }
-            return value;
-        };
-        const auto option = [&](std::string_view name)
-        {
-            if (name == "-h" || name == "--help")
-            {
-                o.help = true;
-            }
-            else if (name == "-f" || name == "--fast")
-            {
-                o.fast = true;
-            }
-            else if (name == "-s" || name == "--separate_channels")
-            {
-                o.separate = true;
-            }
-            else if (name == "-v")
-            {
-                ++o.verbose;
-            }
-            else if (name == "-T")
-            {
-                o.threads = integer(name);
-            }
-            else if (name == "-q" || name == "--n_codebooks")
-            {
-                o.quality = integer(name);
-            }
-            else if (name == "-c" || name == "--channels")
-            {
-                o.channels = integer(name);
-            }
-            else if (name == "--batch_size")
-            {
-                o.batch = integer(name);
-            }
-            else if (name == "--metal")
-            {
-                o.metal = true;
-            }
-            else
-            {
-                throw Error("unknown option: '" + std::string(name) + "'");
-            }
-        };
-        if (arg.starts_with("--"))
-        {
-            option(arg);
-        }
+        // Resolve every spelling in the word before acting on any: a bundle of
+        // letters such as "-vq" is valid only if all its letters are options.
+        std::vector<const OptionSpec*> selected;
+        if (word[1] == '-')
+            selected.push_back(&by_word(word));
         else
+            for (const char letter : word.substr(1))
+                selected.push_back(&by_letter(letter));
+        // Options that take a value consume the following arguments in order.
+        for (const OptionSpec* spec : selected)
         {
-            // A short group is checked whole before any of it takes a value:
-            // "-q1" is the unknown option "-1", not "-q 1".
-            for (const char c : arg.substr(1))
+            int value = 0;
+            if (spec->integer)
             {
-                require(std::string_view("hfsvTqc").find(c) != std::string_view::npos,
-                        ("unknown option: '-" + std::string(1, c) + "'").c_str());
+                if (cursor == arguments.size())
+                    throw Error(spelling(*spec) + " needs a value");
+                value = integer_value(*spec, arguments[cursor++]);
             }
-            for (const char c : arg.substr(1))
-            {
-                option(std::string("-") + c);
-            }
-        }
-        if (o.help)
-        {
-            return o;
+            spec->apply(o, value);
         }
     }
-    if (positional.size() != 3)
+    if (o.help)
+        return o;
+    if (operands.size() != 3)
     {
-        o.help = true;
+        o.help = true; // not a complete command: show the usage
         return o;
     }
-    require(positional[0] == "c" || positional[0] == "d" || positional[0] == "t",
-            ("unknown command: " + std::string(positional[0])).c_str());
-    o.command = positional[0][0];
-    o.input = positional[1];
-    o.output = positional[2];
+    const std::string_view command = operands[0];
+    if (command != "c" && command != "d" && command != "t")
+        throw Error("the command is c, d or t, not '" + std::string(command) + "'");
+    o.command = command[0];
+    o.input = operands[1];
+    o.output = operands[2];
     return o;
 }
 
