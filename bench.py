@@ -4,15 +4,19 @@ Step = one GPU encode (pack_normal-equivalent: model + range coder -> FBAZ
 bytes) plus one GPU decode (unpack_normal-equivalent: model + range decoder ->
 tokens, CRC checked) of a 30 s joint-stereo token stream: 2580 frames x 12
 codebooks, entropy batch 3 (three lanes of 860 frames), one channel group, on
-the reference geometry (12 temporal + 3 codebook layers, width 512, 4 x 128
-heads, FFN 2048) with seeded random-init weights in the reference's packed
+the probability model of 12 temporal + 3 codebook layers, width 1024, 16 x 64
+heads, FFN 4096, with seeded random-init weights in the reference's packed
 layout. Tokens are synthetic (uniform over the 1024-symbol alphabet).
+`--geometry reference` runs the reference's own geometry (width 512, 4 x 128
+heads, FFN 2048) instead; by default that geometry is measured as the
+secondary `reference_geometry` entry.
 
-value = tokens / (encode seconds + decode seconds) of one step.
+value = tokens / (encode seconds + decode seconds) of one step, with the
+session-timed host-to-device copies of the calls' inputs taken out.
 
 Also measured in the same run:
   * roofline: the timed region's dominant kernel, the decode frame step
-    (frame_kernel, one launch per step, ~98% of the round trip): algorithmic
+    (frame_kernel, up to 64 steps per launch, ~98% of the round trip): algorithmic
     bytes per step (every projection's int8 weights, block scales and bias
     once per step, plus the lanes' temporal key/value cache rows at the
     average context position) over the average step time, measured with HIP
@@ -31,8 +35,13 @@ Also measured in the same run:
     weight matrix, rotating through >= 1 GiB of distinct matrices inside one
     captured HIP graph (so the weights stream from HBM, not the 256 MB MALL);
     per-launch time = graph time / launches.
-  * wide_geometry: the same round trip on the 1024-wide geometry (16 x 64
-    heads, FFN 4096), 2580 frames, batch 3.
+  * reference_geometry: the same round trip on the reference geometry
+    (width 512, 4 x 128 heads, FFN 2048), 2580 frames, batch 3, with its own
+    frame-step roofline.
+  * token_stream_round_trip_s: the step's encode + decode seconds (30 s of
+    audio as tokens). encode_decode_s_per_30s_stereo is the PCM round trip of
+    30 s of joint-stereo audio (DAC analysis, RVQ, model and range coding, then
+    back to PCM), from `end_to_end`.
   * attention: causal multi-head attention alone (16 x 64 heads, batch 3,
     T in {256, 1290, 2580}): causal prefill TFLOP/s and one-query decode GB/s.
   * attainable: this device's streaming-read rate and int8 MFMA rate, measured
@@ -68,11 +77,12 @@ def parse():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--frames", type=int, default=2580)
     p.add_argument("--batch", type=int, default=3)
-    p.add_argument("--geometry", choices=["reference", "wide"], default="reference")
-    p.add_argument("--only", choices=["all", "model", "gemv", "gemm", "attention", "qlinear", "wide", "audio"],
+    p.add_argument("--geometry", choices=["reference", "wide"], default="wide")
+    p.add_argument("--only", choices=["all", "model", "gemv", "gemm", "attention", "qlinear", "reference", "audio"],
                    default="all")
     p.add_argument("--gemv-launches", type=int, default=64)
-    p.add_argument("--cpu-frames", type=int, default=1290, help="CPU baseline sample (frames)")
+    p.add_argument("--cpu-frames", type=int, default=0,
+                   help="CPU baseline sample in frames (default: 1290 at the reference geometry, 430 at the wide one)")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
 
@@ -377,8 +387,9 @@ def frame_roofline(geometry, frames, batch, step_s):
     is bound by its ~240 dependent jobs on lane 0's chain, not by memory; the
     fraction shows how far from HBM-bound that is."""
     g = geometry
-    measured, source = (recorded_traffic("frame_step_decode_reference_2580frames.traffic.txt", "bytes_per_step")
-                        if g.width == 512 and frames == 2580 and batch == 3 else (None, None))
+    record = "frame_step_decode_reference_2580frames.traffic.txt" if g.width == 512 else \
+        "frame_step_decode_wide_2580frames.traffic.txt"
+    measured, source = (recorded_traffic(record, "bytes_per_step") if frames == 2580 and batch == 3 else (None, None))
 
     def linear(k, n):
         return k * n + 4 * (k // 256) * n + 4 * n
@@ -401,38 +412,74 @@ def frame_roofline(geometry, frames, batch, step_s):
                          "divided by the steps"}
 
 
-def wide_geometry(native, frames=2580, batch=3, steps=2):
-    """Throughput only: the same round trip on the 1024-wide geometry (width
-    1024, 16 x 64 heads, FFN 4096, 12 + 3 layers), random-init weights, at
-    the full 2580 frames x 12 codebooks, batch 3; same rate definition as
-    `value` (inputs resident: the session-timed input copies are excluded)."""
-    from tsac_hip.synthetic import WIDE, random_model, random_tokens
+def round_trip(torch, native, geometry, frames, batch, steps, warmup, seed=1):
+    """Encode + decode of frames x 12 codebooks (batch lanes, one group) on
+    `geometry`, `steps` timed round trips after `warmup` untimed ones, bracketed
+    by device synchronisations. Rate = tokens / (encode + decode seconds - the
+    session-timed host-to-device copies of the calls' inputs)."""
+    from tsac_hip.synthetic import random_model, random_tokens
 
-    with native.HipModel(random_model(WIDE, seed=2)) as hip_model, hip_model.session() as session:
-        h = native.header(frames, batch, 1, 12)
-        tokens = random_tokens(frames, 1, 12, seed=6)
-        assert np.array_equal(session.decode(session.encode(h, tokens)), tokens)
-        encode_s = decode_s = uploads = step_gpu = 0.0
+    h = native.header(frames, batch, 1, 12)
+    tokens = random_tokens(frames, 1, 12, seed=5)
+    encode_s = decode_s = uploads = step_gpu = 0.0
+    encode_split = [0.0, 0.0]
+    decode_split = [0.0, 0.0]
+    launches = set()
+    # Every session and model is closed, and the device drained, before the
+    # next part of the run (and before exit).
+    with native.HipModel(random_model(geometry, seed=seed)) as hip_model, hip_model.session() as session:
+        for _ in range(warmup):
+            stream = session.encode(h, tokens)
+            assert np.array_equal(session.decode(stream), tokens)
+        torch.cuda.synchronize()
+        # The C ABI takes host buffers (as MetalTransformer does); the session
+        # times the host-to-device copy of each call's input separately, so the
+        # reported rate is the one with inputs already in device memory.
         for _ in range(steps):
             t0 = time.perf_counter()
             stream = session.encode(h, tokens)
             t1 = time.perf_counter()
-            uploads += session.timing()["input_upload"]
+            e = session.timing()
             decoded = session.decode(stream)
             t2 = time.perf_counter()
             d = session.timing()
-            uploads += d["input_upload"]
-            step_gpu += d["steps_gpu"] / d["steps"]
             encode_s += t1 - t0
             decode_s += t2 - t1
-        assert np.array_equal(decoded, tokens), "wide round trip failed"
-    resident = (encode_s + decode_s - uploads) / steps
-    return {"tokens_per_s": round(tokens.size / resident, 1), "encode_s": round(encode_s / steps, 4),
-            "decode_s": round(decode_s / steps, 4), "avg_step_us": round(step_gpu / steps * 1e6, 1),
-            "roofline": frame_roofline(WIDE, frames, batch, step_gpu / steps),
-            "sample": f"encode + decode of {frames} frames x 12 codebooks, batch {batch}, {steps} timed round trips",
-            "geometry": {"width": WIDE.width, "heads": WIDE.heads, "head_width": WIDE.head_width,
-                         "ffn": WIDE.ffn, "layers": [WIDE.temporal_layers, WIDE.codebook_layers]}}
+            encode_split[0] += e["model"]
+            encode_split[1] += e["range_coding"]
+            decode_split[0] += d["model"]
+            decode_split[1] += d["range_coding"]
+            uploads += e["input_upload"] + d["input_upload"]
+            step_gpu += d["steps_gpu"] / d["steps"]
+            launches.add(d["frame_launch"])
+        torch.cuda.synchronize()
+    assert np.array_equal(decoded, tokens), "round trip failed"
+    encode_s /= steps
+    decode_s /= steps
+    uploads /= steps
+    resident_s = encode_s + decode_s - uploads
+    count = tokens.size
+    return {
+        "tokens_per_s": round(count / resident_s, 1),
+        "ms_per_round_trip": round(1000 * resident_s, 2),
+        "roofline": frame_roofline(geometry, frames, batch, step_gpu / steps),
+        "pcie_inclusive_tokens_per_s": round(count / (encode_s + decode_s), 1),
+        "input_upload_ms": round(1000 * uploads, 3),
+        "encode_tokens_per_s": round(count / encode_s, 1),
+        "decode_tokens_per_s": round(count / decode_s, 1),
+        "token_stream_round_trip_s": round(encode_s + decode_s, 4),
+        "stream_bytes": len(stream),
+        "frame_launch": sorted(launches, key=str),
+        "split_s": {"encode_model": round(encode_split[0] / steps, 4),
+                    "encode_range_coding": round(encode_split[1] / steps, 4),
+                    "decode_model": round(decode_split[0] / steps, 4),
+                    "decode_range_coding": round(decode_split[1] / steps, 4),
+                    "decode_frame_steps_gpu": round(step_gpu / steps * (-(-frames // batch)), 4)},
+        "sample": f"encode + decode of {frames} frames x 12 codebooks, batch {batch}, {steps} timed round trips "
+                  f"after {warmup} untimed",
+        "geometry": {"width": geometry.width, "heads": geometry.heads, "head_width": geometry.head_width,
+                     "ffn": geometry.ffn, "layers": [geometry.temporal_layers, geometry.codebook_layers]},
+    }
 
 
 def end_to_end(native, seconds, codebooks, batch, seed, steps=2):
@@ -536,8 +583,10 @@ def cpu_baseline(model, frames, batch):
     return {"value": round(tokens.size / seconds, 1), "unit": "tokens/s", "cores": threads,
             "kind": "port",
             "sample": f"oracle pack_normal + unpack_normal round trip of {frames} frames x 12 codebooks "
-                      f"(batch {batch}, {tokens.size} tokens): encode {t1 - t0:.1f} s + decode {t2 - t1:.1f} s; "
-                      f"host has {len(os.sched_getaffinity(0))} cores, lane parallelism caps threads at {threads}"}
+                      f"(batch {batch}, {tokens.size} tokens, width {model.geometry.width}): encode {t1 - t0:.1f} s "
+                      f"+ decode {t2 - t1:.1f} s; host has {len(os.sched_getaffinity(0))} cores, lane parallelism "
+                      f"caps threads at {threads}; the rate is the one measured on this sample (a part of the "
+                      f"2580-frame recording), not a time extrapolated to it"}
 
 
 def main():
@@ -550,67 +599,14 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
     from tsac_hip import native
-    from tsac_hip.synthetic import REFERENCE, WIDE, random_model, random_tokens
+    from tsac_hip.synthetic import REFERENCE, WIDE, random_model
 
     geometry = REFERENCE if args.geometry == "reference" else WIDE
     result = {}
     if args.only in ("all", "model"):
-        model = random_model(geometry, seed=1)
-        h = native.header(args.frames, args.batch, 1, 12)
-        tokens = random_tokens(args.frames, 1, 12, seed=5)
-        encode_s = decode_s = 0.0
-        encode_split = [0.0, 0.0]
-        decode_split = [0.0, 0.0]
-        uploads = step_gpu = 0.0
-        # Every session and model is closed, and the device drained, before
-        # the next part of the run (and before exit).
-        with native.HipModel(model) as hip_model, hip_model.session() as session:
-            for _ in range(args.warmup):
-                stream = session.encode(h, tokens)
-                assert np.array_equal(session.decode(stream), tokens)
-            torch.cuda.synchronize()
-            # The C ABI takes host buffers (as MetalTransformer does); the session
-            # times the host-to-device copy of each call's input separately, so the
-            # reported rate is the one with inputs already in device memory.
-            for _ in range(args.steps):
-                t0 = time.perf_counter()
-                stream = session.encode(h, tokens)
-                t1 = time.perf_counter()
-                e = session.timing()
-                decoded = session.decode(stream)
-                t2 = time.perf_counter()
-                d = session.timing()
-                encode_s += t1 - t0
-                decode_s += t2 - t1
-                encode_split[0] += e["model"]
-                encode_split[1] += e["range_coding"]
-                decode_split[0] += d["model"]
-                decode_split[1] += d["range_coding"]
-                uploads += e["input_upload"] + d["input_upload"]
-                step_gpu += d["steps_gpu"] / d["steps"]
-        torch.cuda.synchronize()
-        assert np.array_equal(decoded, tokens), "round trip failed"
-        encode_s /= args.steps
-        decode_s /= args.steps
-        uploads /= args.steps
-        count = tokens.size
-        resident_s = encode_s + decode_s - uploads
-        result.update({
-            "value": round(count / resident_s, 1),
-            "ms_per_step": round(1000 * resident_s, 2),
-            "roofline": frame_roofline(geometry, args.frames, args.batch, step_gpu / args.steps),
-            "pcie_inclusive_tokens_per_s": round(count / (encode_s + decode_s), 1),
-            "input_upload_ms": round(1000 * uploads, 3),
-            "encode_tokens_per_s": round(count / encode_s, 1),
-            "decode_tokens_per_s": round(count / decode_s, 1),
-            "encode_decode_s_per_30s_stereo": round(encode_s + decode_s, 4),
-            "stream_bytes": len(stream),
-            "split_s": {"encode_model": round(encode_split[0] / args.steps, 4),
-                        "encode_range_coding": round(encode_split[1] / args.steps, 4),
-                        "decode_model": round(decode_split[0] / args.steps, 4),
-                        "decode_range_coding": round(decode_split[1] / args.steps, 4),
-                        "decode_frame_steps_gpu": round(step_gpu / args.steps * (-(-args.frames // args.batch)), 4)},
-        })
+        head = round_trip(torch, native, geometry, args.frames, args.batch, args.steps, args.warmup)
+        result.update({"value": head.pop("tokens_per_s"), "ms_per_step": head.pop("ms_per_round_trip")})
+        result.update(head)
     if args.only == "model":
         calibration_copy(torch)
     if args.only in ("all", "gemv", "gemm"):
@@ -626,26 +622,29 @@ def main():
         result["roofline_gemm"] = roof
     if args.only in ("all", "attention"):
         result["attention"] = attention_rates(torch, native)
-    if args.only in ("all", "wide") and args.geometry == "reference":
-        result["wide_geometry"] = wide_geometry(native)
+    if args.only in ("all", "reference") and args.geometry == "wide":
+        result["reference_geometry"] = round_trip(torch, native, REFERENCE, 2580, 3, steps=3, warmup=1)
     if args.only in ("all", "qlinear"):
         result["qlinear"] = qlinear_table(torch, native)
     if args.only in ("all", "audio"):
-        # BASELINE configs 4 (30 s joint stereo, 12 codebooks, batch 3) and 0
-        # (10 s, 3 codebooks, automatic batch) end to end; the CPU chain on a
-        # bounded sample, scaled to the same audio length.
+        # The 30 s joint-stereo recording (12 codebooks, batch 3) and the 10 s
+        # one (3 codebooks, automatic batch) end to end; the CPU chain on a
+        # 1 s sample of the 30 s recording.
         audio = {"config4": end_to_end(native, 30.0, 12, 3, seed=4), "config0": end_to_end(native, 10.0, 3, 0, seed=3)}
+        result["encode_decode_s_per_30s_stereo"] = audio["config4"]["round_trip_s"]
         if not args.no_cpu:
             cpu = cpu_end_to_end(1.0, 12, 3, seed=4)
-            cpu["scaled_to_30s_s"] = round(cpu["seconds"] * 30.0, 1)
+            cpu["extrapolated_to_30s_s"] = round(cpu["seconds"] * 30.0, 1)
+            cpu["extrapolation"] = "the 1 s sample's time x 30 (not measured on 30 s)"
             cpu["kind"] = "port"
             audio["cpu_baseline"] = cpu
-            audio["config4_speedup_vs_cpu"] = round(cpu["scaled_to_30s_s"] / audio["config4"]["round_trip_s"], 1)
+            audio["config4_speedup_vs_cpu_extrapolated"] = round(
+                cpu["extrapolated_to_30s_s"] / audio["config4"]["round_trip_s"], 1)
         result["end_to_end"] = audio
     if args.only == "all":
         if not args.no_cpu:
-            result["cpu_baseline"] = cpu_baseline(random_model(geometry, seed=1), args.cpu_frames,
-                                                  args.batch)
+            frames = args.cpu_frames or (1290 if geometry is REFERENCE else 430)
+            result["cpu_baseline"] = cpu_baseline(random_model(geometry, seed=1), frames, args.batch)
     line = {
         "metric": "prob-model tokens/s",
         "value": result.pop("value", None),
@@ -660,7 +659,9 @@ def main():
         "dtype": "int8 (W8A8 int32-exact dots) + fp32/bf16",
         "data": "synthetic tokens, seeded random-init weights in the reference packed layout",
         "config": {"workload": f"encode+decode of a 30 s joint-stereo token stream: {args.frames} frames x "
-                               f"12 codebooks, entropy batch {args.batch}, {args.geometry} geometry",
+                               f"12 codebooks, entropy batch {args.batch}, probability model of 12 + 3 layers, "
+                               f"width {geometry.width}, {geometry.heads} x {geometry.head_width} heads, "
+                               f"FFN {geometry.ffn}",
                    "frames": args.frames, "codebooks": 12, "batch": args.batch, "groups": 1,
                    "geometry": {"width": geometry.width, "heads": geometry.heads,
                                 "head_width": geometry.head_width, "ffn": geometry.ffn,

@@ -92,7 +92,11 @@ void tsac_hip_model_destroy(tsac_hip_model* model);
 
 /* MetalTransformer::new_session (src/metal/transformer.hpp:24): independent
  * mutable state (caches, scratch, stream) sharing the immutable model. One
- * caller at a time per session; separate sessions may run concurrently. */
+ * caller at a time per session; separate sessions may run concurrently. The
+ * session reads TSAC_HIP_FRAME_LAUNCH from the environment once, here: "plain"
+ * launches its decode frame steps without the cooperative co-residency
+ * guarantee (for runs under a profiler, on an otherwise idle device); anything
+ * else, or unset, launches them cooperatively. */
 int tsac_hip_session_create(tsac_hip_model* model, tsac_hip_session** session);
 void tsac_hip_session_destroy(tsac_hip_session* session);
 /* MetalTransformer::clear_session (src/metal/transformer.hpp:27): releases
@@ -160,10 +164,14 @@ int tsac_hip_distributions(tsac_hip_session* session, const tsac_hip_header* hea
  * (seconds): [0] GPU model work, [1] host range coding, [2] total, [3] the
  * host-to-device copy of the call's input (tokens, or the stream's payload),
  * included in [0] and [2]; for decode-side passes [4] the GPU time of the
- * frame-step loop, between two HIP events on the session's stream, and [5] the
- * number of frame steps in it (both 0 otherwise). No counterpart in the
- * reference; for callers that report throughput with inputs already in device
- * memory. */
+ * frame-step loop, between two HIP events on the session's stream, [5] the
+ * number of frame steps in it (both 0 otherwise) and [6] how those frame steps
+ * were launched: 0 cooperatively (co-residency guaranteed), 1 as plain launches
+ * because the session was created with TSAC_HIP_FRAME_LAUNCH=plain in the
+ * environment (for example to run under a profiler), 2 as plain launches
+ * because another process held the device's cooperative-launch resources; -1
+ * when the call ran no frame step. No counterpart in the reference; for callers
+ * that report throughput with inputs already in device memory. */
 int tsac_hip_session_timing(const tsac_hip_session* session, double* seconds, size_t count);
 
 /* ---- the DAC codec around the model (AudioAnalyzer, include/tsac/audio_analyzer.hpp) ---- */

@@ -1,5 +1,8 @@
 #include "runtime.hpp"
 
+#include <cstdlib>
+#include <string_view>
+
 #include <algorithm>
 #include <chrono>
 #include <cstring>
@@ -271,6 +274,8 @@ Session::Session(std::shared_ptr<const Model> model) : model_(std::move(model))
     check_hip(hipEventCreate(&steps_stop_), "hipEventCreate");
     errors_ = DeviceBuffer(256);
     pinned_errors_.reserve(256);
+    const char* launch = std::getenv("TSAC_HIP_FRAME_LAUNCH");
+    plain_frame_launch_ = launch && std::string_view(launch) == "plain";
 }
 
 Session::~Session()
@@ -663,7 +668,7 @@ std::vector<uint8_t> Session::encode(Header h, const uint16_t* tokens, std::size
     });
     const auto bytes = frame_normal(h, crc, encoder.finish());
     const double t2 = now();
-    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), 0.0, 0.0};
+    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), 0.0, 0.0, -1.0};
     return bytes;
 }
 
@@ -702,7 +707,7 @@ std::vector<uint16_t> Session::decode(const uint8_t* stream, std::size_t length,
             "decoded tokens fail the stream's CRC-32 check");
     const double t2 = now();
     const double steps = double(Lanes(h).steps());
-    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), steps_seconds(), steps};
+    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), steps_seconds(), steps, double(frame_launch_)};
     return tokens;
 }
 
@@ -725,6 +730,7 @@ void Session::distributions(Header h, const uint16_t* tokens, std::size_t count,
     check_errors();
     const double t1 = now();
     const double steps = decode_pass ? double(Lanes(h).steps()) : 0.0;
-    timing_ = {t1 - t0, 0.0, t1 - t0, input_seconds(), decode_pass ? steps_seconds() : 0.0, steps};
+    timing_ = {t1 - t0, 0.0, t1 - t0, input_seconds(), decode_pass ? steps_seconds() : 0.0, steps,
+               decode_pass ? double(frame_launch_) : -1.0};
 }
 } // namespace tsac_hip

@@ -227,9 +227,11 @@ public:
     // Seconds of the last call: GPU model work, host range coding, total, the
     // host-to-device copy of the call's input (tokens or payload), which the
     // first and third include, then (decode-side passes) the GPU time of the
-    // frame-step loop between two events on the session stream and the number
-    // of frame steps in it.
-    std::array<double, 6> timing() const
+    // frame-step loop between two events on the session stream, the number of
+    // frame steps in it, and how its frame steps were launched (FrameLaunch:
+    // 0 cooperative, 1 plain on request, 2 plain because another process held
+    // the cooperative-launch resources; -1 when the call ran none).
+    std::array<double, 7> timing() const
     {
         return timing_;
     }
@@ -273,7 +275,11 @@ private:
     Arena arena_;
     DeviceBuffer errors_;
     PinnedBuffer pinned_errors_, staging_, staging_nodes_, staging_tokens_;
-    std::array<double, 6> timing_{};
+    std::array<double, 7> timing_{};
+    // TSAC_HIP_FRAME_LAUNCH=plain in the environment when the session was
+    // created: frame steps go out as plain launches (see FrameArgs::plain_launch).
+    bool plain_frame_launch_ = false;
+    int frame_launch_ = -1; // FrameLaunch of the last stepwise pass, -1 if none
     hipEvent_t upload_start_ = nullptr, upload_stop_ = nullptr;
     hipEvent_t steps_start_ = nullptr, steps_stop_ = nullptr;
     bool stepped_ = false;

@@ -133,6 +133,7 @@ void Session::layer_step(bool temporal, std::size_t layer, uint16_t* x, std::siz
 void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* payload,
                        std::size_t payload_bytes, uint16_t* tokens_out, uint16_t* distributions)
 {
+    frame_launch_ = -1;
     const Geometry& g = model_->geometry();
     const Model& m = *model_;
     const std::size_t C = h.codebooks, G = h.groups, w = g.width;
@@ -391,7 +392,8 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
             frame.step = int(step);
             frame.steps = int(n);
             frame.epoch = uint32_t(step + 1); // exchange words are cleared for every pass
-            frame_step(frame, stream_);
+            frame.plain_launch = plain_frame_launch_;
+            frame_launch_ = std::max(frame_launch_, int(frame_step(frame, stream_)));
             context_used += n;
             step += n - 1;
         }

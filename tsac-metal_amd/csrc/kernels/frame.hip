@@ -11,6 +11,8 @@
 #include "step_ops.hpp"
 
 #include <algorithm>
+#include <array>
+#include <atomic>
 #include <cstring>
 
 namespace tsac_hip
@@ -2534,20 +2536,29 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
     }
 }
 
-template <int VW, int VF, int VL, int HW> void launch_frame(const FrameArgs& a, hipStream_t stream)
+// Workgroups of frame_kernel<VW, VF, VL, HW> that fit on the device at once,
+// computed once per device.
+template <int VW, int VF, int VL, int HW> int resident_workgroups()
 {
-    static int resident = 0;
-    if (!resident)
+    static std::array<std::atomic<int>, 64> resident{};
+    int device = 0, units = 0, per_unit = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    require(device >= 0 && device < int(resident.size()), "frame step: device index out of range");
+    if (const int known = resident[device].load(std::memory_order_relaxed))
     {
-        int device = 0, units = 0, per_unit = 0;
-        check_hip(hipGetDevice(&device), "hipGetDevice");
-        check_hip(hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
-        check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_unit, frame_kernel<VW, VF, VL, HW>,
-                                                               frame_threads, 0),
-                  "hipOccupancyMaxActiveBlocksPerMultiprocessor");
-        require(units > 0 && per_unit > 0, "frame step: kernel does not fit a compute unit");
-        resident = units * per_unit;
+        return known;
     }
+    check_hip(hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
+    check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_unit, frame_kernel<VW, VF, VL, HW>, frame_threads, 0),
+              "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    require(units > 0 && per_unit > 0, "frame step: kernel does not fit a compute unit");
+    resident[device].store(units * per_unit, std::memory_order_relaxed);
+    return units * per_unit;
+}
+
+template <int VW, int VF, int VL, int HW> FrameLaunch launch_frame(const FrameArgs& a, hipStream_t stream)
+{
+    const int resident = resident_workgroups<VW, VF, VL, HW>();
     // The workgroups of the richest layout the device holds (frame_kernel
     // derives the same layout from the grid), plus the sampler; when not even
     // the plain one fits, the groups shrink and workgroups take several tiles.
@@ -2555,25 +2566,33 @@ template <int VW, int VF, int VL, int HW> void launch_frame(const FrameArgs& a, 
     const int grid = std::min(resident, layout.workgroups + 1);
     FrameArgs args = a;
     void* params[] = {&args};
+    const void* kernel = reinterpret_cast<const void*>(frame_kernel<VW, VF, VL, HW>);
+    if (a.plain_launch)
+    {
+        // Asked for by the session (for example to run under a profiler): the
+        // grid fits the device at once, so on an otherwise idle device it is
+        // co-resident; every wait of the kernel is bounded, so where it is not,
+        // the step ends with the "stalled" error instead of hanging.
+        check_hip(hipLaunchKernel(kernel, dim3(grid), dim3(frame_threads), params, 0, stream), "frame step launch");
+        return FrameLaunch::requested_plain;
+    }
     // Cooperative: every workgroup waits on others, so all must be resident at
     // once, also when several sessions share the device. A plain launch of the
     // same grid measured ~20 us less per step on an otherwise idle device, but
     // two concurrent sessions could then each hold part of the device and wait
     // on workgroups that cannot be placed.
-    hipError_t status = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(frame_kernel<VW, VF, VL, HW>),
-                                                   dim3(grid), dim3(frame_threads), params, 0, stream);
+    hipError_t status = hipLaunchCooperativeKernel(kernel, dim3(grid), dim3(frame_threads), params, 0, stream);
     if (status == hipErrorIllegalState)
     {
         // The device's cooperative-launch resources belong to one process at a
-        // time, and another process holds them. A plain launch of the same
-        // grid is co-resident on an otherwise idle device; every wait of the
-        // kernel is bounded, so where it is not, the step ends with the
-        // "stalled" error instead of hanging.
+        // time, and another process holds them: the same grid goes out as a
+        // plain launch, with the bounded waits above.
         (void)hipGetLastError();
-        status = hipLaunchKernel(reinterpret_cast<const void*>(frame_kernel<VW, VF, VL, HW>), dim3(grid),
-                                 dim3(frame_threads), params, 0, stream);
+        check_hip(hipLaunchKernel(kernel, dim3(grid), dim3(frame_threads), params, 0, stream), "frame step launch");
+        return FrameLaunch::fallback_plain;
     }
     check_hip(status, "frame step launch");
+    return FrameLaunch::cooperative;
 }
 } // namespace
 
@@ -2740,7 +2759,7 @@ std::size_t frame_exchange_words(int width, int ffn, int latent, int alphabet, i
     return Words(width, ffn, latent, alphabet, books, temporal_layers, codebook_layers).total;
 }
 
-void frame_step(const FrameArgs& a, hipStream_t stream)
+FrameLaunch frame_step(const FrameArgs& a, hipStream_t stream)
 {
     require(frame_supported(a.width, a.heads, a.head_width, a.ffn, a.latent, a.alphabet, a.lanes),
             "frame step: unsupported geometry");
@@ -2753,11 +2772,8 @@ void frame_step(const FrameArgs& a, hipStream_t stream)
     require(a.known || (a.state && a.payload), "frame step: needs known tokens or a decoder");
     if (a.width == 512)
     {
-        launch_frame<8, 32, 16, 128>(a, stream);
+        return launch_frame<8, 32, 16, 128>(a, stream);
     }
-    else
-    {
-        launch_frame<16, 64, 16, 64>(a, stream);
-    }
+    return launch_frame<16, 64, 16, 64>(a, stream);
 }
 } // namespace tsac_hip

@@ -75,6 +75,15 @@ struct FrameArgs
     uint32_t epoch = 0;                  // first step's; nonzero, different for every step over the same words
     unsigned* abort = nullptr;           // zero before the first step; nonzero after a stalled wait
     const void* jobs = nullptr;          // device copy of frame_job_table(*this), unchanged during a launch
+    bool plain_launch = false;           // launch without the cooperative co-residency guarantee
+};
+
+// How frame_step launched the kernel.
+enum class FrameLaunch
+{
+    cooperative = 0, // co-residency guaranteed by the runtime
+    requested_plain = 1, // plain launch asked for through FrameArgs::plain_launch
+    fallback_plain = 2, // plain launch: another process holds the cooperative-launch resources
 };
 
 // Geometries the frame kernel is instantiated for, at 1..8 lanes.
@@ -87,5 +96,5 @@ std::size_t frame_exchange_words(int width, int ffn, int latent, int alphabet, i
 // position, step, steps, lanes and epoch, which the launches pass themselves); the
 // launches read it from device memory through FrameArgs::jobs.
 std::vector<uint8_t> frame_job_table(const FrameArgs& args);
-void frame_step(const FrameArgs& args, hipStream_t stream);
+FrameLaunch frame_step(const FrameArgs& args, hipStream_t stream);
 } // namespace tsac_hip

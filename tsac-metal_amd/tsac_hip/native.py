@@ -585,11 +585,15 @@ class HipSession:
                                                mode, _ptr(out, C.c_uint16)))
         return out
 
+    #: How the frame steps of the last decode-side call were launched (timing()["frame_launch"]).
+    FRAME_LAUNCH = {-1: None, 0: "cooperative", 1: "plain (TSAC_HIP_FRAME_LAUNCH=plain)",
+                    2: "plain (cooperative-launch resources held by another process)"}
+
     def timing(self):
-        t = (C.c_double * 6)()
-        check(library().tsac_hip_session_timing(self.handle, t, 6))
+        t = (C.c_double * 7)()
+        check(library().tsac_hip_session_timing(self.handle, t, 7))
         return {"model": t[0], "range_coding": t[1], "total": t[2], "input_upload": t[3], "steps_gpu": t[4],
-                "steps": int(t[5])}
+                "steps": int(t[5]), "frame_launch": self.FRAME_LAUNCH[int(t[6])]}
 
 
 def prepare_rvq(codebook, in_v, in_g, out_v, out_g):
