@@ -29,9 +29,12 @@ constexpr int frame_threads = frame_waves * wave;
 // sharing a SIMD, against more values per lane. Measured per frame step of the
 // 2580-frame decode: 2 waves for K <= 512 (no BF8L exchange, one LayerNorm
 // exchange) 704 us, 1 wave 718 us, 8 waves 731 us; 8 waves for K = 2048, 4
-// waves 721 us.
-template <int V> constexpr int spread_waves = V <= 8 ? 2 : 8;
+// waves 721 us. K = 1024 (the 1024-wide geometry): 4 waves of 4 values, one
+// BF8L block per wave, 1,195.6 us; 8 waves 1,210.5 us; 2 waves 1,228.4 us.
+template <int V> constexpr int spread_waves = V <= 8 ? 2 : V <= 16 ? 4 : 8;
 constexpr int max_lanes = 8;
+// Output rows of a narrow projection tile (project_tile, FrameLayout::narrow_down).
+constexpr int narrow_rows = tile_rows / 2;
 constexpr int max_blocks = 16; // 64-key blocks of one attention query (context <= 1024)
 constexpr int max_books = 16;  // codebook positions of one frame
 // Polls of one word before a wait is declared stalled (each poll sleeps ~64
@@ -789,8 +792,13 @@ __device__ __forceinline__ void book_head(const word* qkv, std::size_t book_word
     }
 }
 
-// One 64-row tile of a projection for M lanes (decode.hip fused_linear_kernel).
-template <int V, In I, Out O, int HW = 0>
+// One tile of R output rows of a projection for M lanes (decode.hip
+// fused_linear_kernel). R is tile_rows, or narrow_rows for a K of 2 *
+// frame_waves blocks: each half-wave then holds one whole block of 32 rows,
+// block `warp` in lanes 0-31 and block `warp + frame_waves` in lanes 32-63, so
+// every wave keeps its weights in registers for all lanes. A narrow tile t is
+// rows [32 (t % 2), 32 (t % 2) + 32) of the 64-row weight tile t / 2.
+template <int V, In I, Out O, int HW = 0, int R = tile_rows>
 __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int position, int M, int tile, Exchange exchange,
                                           uint32_t* error, uint8_t* lds, constant_ptr<BookAttention> book_job = nullptr,
                                           int book_lane = 0, uint32_t previous_epoch = 0)
@@ -837,9 +845,11 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
     tile = uniform(tile);
     error = uniform(error);
     constexpr int K = wave * V, blocks = K / 256;
+    constexpr bool narrow = R == narrow_rows;
+    static_assert(R == tile_rows || (narrow && blocks == 2 * frame_waves), "narrow tiles hold two blocks per wave");
     constexpr int waves_per_block = blocks >= frame_waves ? 1 : frame_waves / blocks;
     constexpr int wave_segments = segments / waves_per_block;
-    constexpr int rounds = blocks > frame_waves ? blocks / frame_waves : 1;
+    constexpr int rounds = narrow ? 1 : blocks > frame_waves ? blocks / frame_waves : 1;
     // Lanes one at a time whenever the weights fit registers for all of them.
     constexpr bool pipelined = rounds == 1;
     static_assert(I != In::attention || (pipelined && book_attention_fits<V, HW>),
@@ -864,19 +874,22 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
     const int N = int(p.w.N);
 
     // 1. Weight loads first, then the chain constants and the residual word.
-    const int first_block = rounds > 1 ? warp : warp / waves_per_block;
-    const int first_segment = rounds > 1 ? 0 : (warp % waves_per_block) * wave_segments;
+    const int first_block = narrow ? warp + (lane / narrow_rows) * frame_waves
+                            : rounds > 1 ? warp : warp / waves_per_block;
+    const int first_segment = rounds > 1 || narrow ? 0 : (warp % waves_per_block) * wave_segments;
     uint4 w[wave_segments];
     {
-        const int8_t* base = p.w.values + tile_offset(tile, first_block, first_segment, blocks) + lane * 16;
+        const int8_t* base = narrow ? p.w.values + tile_offset(tile / 2, first_block, 0, blocks) +
+                                          ((tile % 2) * narrow_rows + lane % narrow_rows) * 16
+                                    : p.w.values + tile_offset(tile, first_block, first_segment, blocks) + lane * 16;
 #pragma unroll
         for (int s = 0; s < wave_segments; ++s)
         {
             w[s] = load16(base + s * tile_rows * 16);
         }
     }
-    const int pair = threadIdx.x % 32, column = threadIdx.x / 32;
-    const int n0 = tile * tile_rows + 2 * pair;
+    const int pair = threadIdx.x % (R / 2), column = threadIdx.x / (R / 2);
+    const int n0 = tile * R + 2 * pair;
     const float2 bias = load_float2(p.w.bias + n0);
     const float bias0 = bias.x, bias1 = bias.y;
     // A fixed residual row (the codebook position row) is known before any wait.
@@ -1088,7 +1101,7 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
                     w[s] = load16(base + s * tile_rows * 16);
                 }
             }
-            const int slot = b * waves_per_block + (rounds > 1 ? 0 : warp % waves_per_block);
+            const int slot = b * waves_per_block + (rounds > 1 || narrow ? 0 : warp % waves_per_block);
             for (int m = m0; m < m1; ++m)
             {
                 // Four independent accumulators: the block dot is an exact
@@ -1110,7 +1123,7 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
                     part[2] = __builtin_amdgcn_sdot4(int(w[s].z), int(u[s].z), part[2], false);
                     part[3] = __builtin_amdgcn_sdot4(int(w[s].w), int(u[s].w), part[3], false);
                 }
-                dots[(slot * max_lanes + m) * tile_rows + lane] = (part[0] + part[1]) + (part[2] + part[3]);
+                dots[(slot * max_lanes + m) * R + lane % R] = (part[0] + part[1]) + (part[2] + part[3]);
             }
         }
         lds_barrier();
@@ -1129,7 +1142,7 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
 #pragma unroll
             for (int s = 0; s < waves_per_block; ++s)
             {
-                const int* d = dots + ((b * waves_per_block + s) * max_lanes + m) * tile_rows + 2 * pair;
+                const int* d = dots + ((b * waves_per_block + s) * max_lanes + m) * R + 2 * pair;
                 d0 += d[0];
                 d1 += d[1];
             }
@@ -2277,7 +2290,13 @@ struct FrameLayout
 {
     bool fused = false, paired = false;
     bool split = false; // temporal queries in halves over two workgroups each
-    int out_tiles = 0; // tiles of an out job: one per lane when fused
+    // Down projections in tiles of narrow_rows output rows: their 64-row tiles
+    // would hold more weight blocks than the waves can keep in registers, and a
+    // tile that streams them in rounds takes all lanes at once. The embedding
+    // job then runs on the prefix group's workgroups.
+    bool narrow_down = false;
+    int out_tiles = 0;  // tiles of an out job: one per lane when fused
+    int down_tiles = 0; // tiles of a down job
     int workgroups = 0; // workers the layout asks for
 };
 
@@ -2285,10 +2304,13 @@ __host__ __device__ inline FrameLayout frame_layout(int width, int heads, int ff
 {
     const bool fusable = heads <= frame_waves; // a wave per head (book_attention_fits)
     const int w = width / tile_rows, f = ffn / tile_rows;
-    // embed, qkv, attend, out, up, down, condition, prefix, head
-    const int base = w + 3 * w + lanes * heads + w + f + w + 1 + w + alphabet / tile_rows;
-    const int fused_extra = (lanes - 1) * w, paired_extra = 3 * w + f + w;
     FrameLayout l;
+    l.narrow_down = ffn / 256 > frame_waves;
+    l.down_tiles = l.narrow_down ? width / narrow_rows : w;
+    // embed, qkv, attend, out, up, down, condition, prefix, head
+    const int base = (l.narrow_down ? 0 : w) + 3 * w + lanes * heads + w + f + l.down_tiles + 1 + w +
+                     alphabet / tile_rows;
+    const int fused_extra = (lanes - 1) * w, paired_extra = 3 * w + f + l.down_tiles;
     if (fusable && base + fused_extra + paired_extra <= workers)
     {
         l.fused = l.paired = true;
@@ -2357,23 +2379,41 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
     // halves of a query would hand the records over before it waits for them.
     const bool split_attention = layout.split;
     const int kind_tiles[kinds] = {width / tile_rows, 3 * width / tile_rows, (split_attention ? 2 : 1) * M * a.heads,
-                                   layout.out_tiles, a.ffn / tile_rows, width / tile_rows, 1, width / tile_rows,
+                                   layout.out_tiles, a.ffn / tile_rows, layout.down_tiles, 1, width / tile_rows,
                                    a.alphabet / tile_rows};
+    // With narrow down tiles the embedding job runs on the prefix group (both
+    // take width / tile_rows tiles): a prefix workgroup's embedding job of the
+    // next step comes after its last prefix job of this step, in the order of
+    // their inputs.
+    const auto own_group = [&](int kind) { return !(layout.narrow_down && kind == Kind::embed); };
     int group_size[kinds], group_base[kinds];
     {
         const int workers = G - 1;
-        int total = 0;
+        int total = 0, owners = 0;
         for (int k = 0; k < kinds; ++k)
         {
-            total += kind_tiles[k] * sets(k);
+            if (own_group(k))
+            {
+                total += kind_tiles[k] * sets(k);
+                ++owners;
+            }
         }
         int base = 1;
         for (int k = 0; k < kinds; ++k)
         {
+            if (!own_group(k))
+            {
+                continue;
+            }
             group_size[k] = total <= workers ? kind_tiles[k] * sets(k)
-                                             : max(1, kind_tiles[k] * (workers - kinds) / total);
+                                             : max(1, kind_tiles[k] * (workers - owners) / total);
             group_base[k] = base;
             base += group_size[k];
+        }
+        if (!own_group(Kind::embed))
+        {
+            group_size[Kind::embed] = group_size[Kind::prefix];
+            group_base[Kind::embed] = group_base[Kind::prefix];
         }
     }
     // This workgroup's first tile of a job of `kind` (>= any tile count if
@@ -2462,9 +2502,19 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
         if (member(Kind::down, parity))
         {
             const auto p = projection(q + 3);
-            for (int t = first_tile(Kind::down, parity); t < width_tiles; t += step(Kind::down))
+            for (int t = first_tile(Kind::down, parity); t < layout.down_tiles; t += step(Kind::down))
             {
-                project_tile<VF, In::words, Out::residual_words>(p, 0, M, t, x, a.error, lds);
+                if (layout.narrow_down)
+                {
+                    if constexpr (VF * wave / 256 == 2 * frame_waves)
+                    {
+                        project_tile<VF, In::words, Out::residual_words, 0, narrow_rows>(p, 0, M, t, x, a.error, lds);
+                    }
+                }
+                else
+                {
+                    project_tile<VF, In::words, Out::residual_words>(p, 0, M, t, x, a.error, lds);
+                }
             }
         }
     };
