@@ -299,7 +299,8 @@ def qlinear_table(torch, native, rotate_bytes=1 << 30):
                 seconds = start.elapsed_time(stop) / 1000 / reps
                 how = "plain launches over 4 rotating weight copies"
             traffic = K * n + 20 * n + m * K + 16 * m + 2 * m * n
-            table.append({"N": n, "M": m, "path": "gemv" if m <= 8 else "gemm", "us": round(seconds * 1e6, 2),
+            table.append({"N": n, "M": m, "path": "gemv" if m <= 8 else "small-M MFMA" if m <= 64 else "gemm",
+                          "us": round(seconds * 1e6, 2),
                           "GB/s": round(traffic / seconds / 1e9, 1),
                           "frac_hbm": round(traffic / seconds / 1e9 / HBM_PEAK_GBPS, 4),
                           "TOP/s": round(2 * m * n * K / seconds / 1e12, 2), "method": how})

@@ -394,14 +394,17 @@ int tsac_hip_linear_create(const tsac_hip_linear* weights, size_t K, size_t N,
                            tsac_hip_device_linear** linear);
 void tsac_hip_linear_destroy(tsac_hip_device_linear* linear);
 
-/* path: 0 automatic (GEMV for M <= 8, else MFMA GEMM), 1 GEMV, 2 GEMM; the GEMM
- * needs y and residual 16-byte aligned.
+/* path: 0 automatic (GEMV for M <= 8, the small-M MFMA GEMM for M <= 64 when
+ * K <= 2048, else the MFMA GEMM), 1 GEMV, 2 GEMM, 4 small-M MFMA GEMM (row-major
+ * activations, M <= 64, K <= 2048); the GEMM needs y and residual 16-byte
+ * aligned.
  * 3 = GEMM on activations in MFMA operand tiles (tsac_hip_bf8l_tiles);
  * accepted by tsac_hip_linear_apply_quantized only. */
 #define TSAC_HIP_PATH_AUTO 0
 #define TSAC_HIP_PATH_GEMV 1
 #define TSAC_HIP_PATH_GEMM 2
 #define TSAC_HIP_PATH_GEMM_TILES 3
+#define TSAC_HIP_PATH_SMALL 4
 
 /* PackedLinear::apply_into (src/common/packed_linear.tpp:264-302) on device
  * memory: x [M][K] BF16 -> y [M][N] BF16. Quantisation scratch comes from the

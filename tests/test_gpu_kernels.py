@@ -54,14 +54,14 @@ def _activations(rng, m, k, pattern=False):
 @pytest.mark.parametrize("n", [1024, 4096])
 @pytest.mark.parametrize("m", [1, 3, 64, 1024, 4096])
 def test_qlinear_config_shapes_match_oracle(torch, native, oracle, n, m):
-    """K=1024 qlinear, GEMV and GEMM paths, against the oracle (rows sampled for large M)."""
+    """K=1024 qlinear, GEMV, small-M and GEMM paths, against the oracle (rows sampled for large M)."""
     rng = np.random.default_rng(n * 7 + m)
     values, scales, bias = random_linear(rng, 1024, n, bias_std=0.1, row_scales=True)
     x = _activations(rng, m, 1024)
     linear = native.DeviceLinear(values, scales, bias)
     dx = dev(torch, x)
     outputs = {}
-    paths = [native.PATH_GEMM] + ([native.PATH_GEMV] if m <= 8 else [])
+    paths = [native.PATH_GEMM] + ([native.PATH_GEMV] if m <= 8 else []) + ([native.PATH_SMALL] if m <= 64 else [])
     for path in paths:
         y = empty(torch, (m, n), torch.int16)
         linear.apply(dx, y, path)
@@ -72,6 +72,8 @@ def test_qlinear_config_shapes_match_oracle(torch, native, oracle, n, m):
             linear.apply(dx[r:r + 8], y[r:r + 8], native.PATH_GEMV)
         outputs[native.PATH_GEMV] = host(y)
     assert np.array_equal(outputs[native.PATH_GEMM], outputs[native.PATH_GEMV])
+    if m <= 64:
+        assert np.array_equal(outputs[native.PATH_GEMM], outputs[native.PATH_SMALL])
     rows = np.arange(m) if m <= 64 else np.unique(np.r_[0, 1, 127, 128, m - 1, rng.integers(0, m, 40)])
     expected = oracle.qlinear(values, scales, bias, x[rows])
     assert np.array_equal(outputs[native.PATH_GEMM][rows], expected)
@@ -79,7 +81,7 @@ def test_qlinear_config_shapes_match_oracle(torch, native, oracle, n, m):
 
 @pytest.mark.parametrize("k,n", [(512, 1536), (512, 512), (512, 2048), (2048, 512), (1024, 512), (512, 1024),
                                  (256, 256), (4096, 1024)])
-@pytest.mark.parametrize("columns", [1, 2, 3, 6, 8, 14, 96])
+@pytest.mark.parametrize("columns", [1, 2, 3, 6, 8, 14, 33, 64, 96])
 def test_qlinear_reference_projection_shapes(torch, native, oracle, k, n, columns):
     """Projection shapes of the reference model at the column counts of
     tests/metal_optimized.cpp:96-146, with the integer-pattern activations."""
@@ -94,6 +96,10 @@ def test_qlinear_reference_projection_shapes(torch, native, oracle, k, n, column
     if columns <= 8:
         linear.apply(dev(torch, x), y, native.PATH_GEMV)
         assert np.array_equal(host(y), expected)
+    if columns <= 64 and k <= 2048:
+        y.zero_()
+        linear.apply(dev(torch, x), y, native.PATH_SMALL)
+        assert np.array_equal(host(y), expected)
 
 
 def test_qlinear_edge_bits_and_zero_blocks(torch, native, oracle):
@@ -105,7 +111,7 @@ def test_qlinear_edge_bits_and_zero_blocks(torch, native, oracle):
         x = np.where((i // 256) % 3 == 0, 0, EDGE_BITS[i % EDGE_BITS.size]).astype(np.uint16).reshape(columns, 1024)
         expected = oracle.qlinear(values, scales, bias, x)
         linear = native.DeviceLinear(values, scales, bias)
-        for path in (native.PATH_GEMM,) + ((native.PATH_GEMV,) if columns <= 8 else ()):
+        for path in (native.PATH_GEMM, native.PATH_SMALL) + ((native.PATH_GEMV,) if columns <= 8 else ()):
             y = empty(torch, (columns, 512), torch.int16)
             linear.apply(dev(torch, x), y, path)
             assert np.array_equal(host(y), expected)
@@ -125,7 +131,7 @@ def test_qlinear_rejects_nonfinite(torch, native):
 def test_qlinear_fused_residual(torch, native, oracle):
     rng = np.random.default_rng(3)
     values, scales, bias = random_linear(rng, 2048, 512)
-    for m in (3, 77):
+    for m, path in ((3, native.PATH_AUTO), (77, native.PATH_AUTO), (40, native.PATH_SMALL), (64, native.PATH_AUTO)):
         x = _activations(rng, m, 2048)
         skip = bf16_bits(((np.arange(m * 512) % 31) - 15).astype(np.float32) / 32).reshape(m, 512)
         q = empty(torch, (m, 2048), torch.int8)
@@ -133,7 +139,7 @@ def test_qlinear_fused_residual(torch, native, oracle):
         native.bf8l(dev(torch, x), m, 2048, q, s)
         linear = native.DeviceLinear(values, scales, bias)
         y = dev(torch, skip)
-        linear.apply_quantized(q, s, m, y, residual=y)
+        linear.apply_quantized(q, s, m, y, residual=y, path=path)
         plain = oracle.qlinear(values, scales, bias, x)
         expected = np.array([[oracle.add_bf16(int(a), int(b)) for a, b in zip(r1, r2)]
                              for r1, r2 in zip(skip, plain)], np.uint16)

@@ -263,10 +263,11 @@ void fill_dac_desc(const PreparedDac& d, tsac_hip_dac_desc* desc)
 
 LinearPath path_of(int path)
 {
-    require(path >= 0 && path <= 2, "invalid linear path");
-    return path == TSAC_HIP_PATH_GEMV ? LinearPath::gemv
-           : path == TSAC_HIP_PATH_GEMM ? LinearPath::gemm
-                                        : LinearPath::automatic;
+    require(path >= 0 && path <= 4 && path != TSAC_HIP_PATH_GEMM_TILES, "invalid linear path");
+    return path == TSAC_HIP_PATH_GEMV    ? LinearPath::gemv
+           : path == TSAC_HIP_PATH_GEMM  ? LinearPath::gemm
+           : path == TSAC_HIP_PATH_SMALL ? LinearPath::small
+                                         : LinearPath::automatic;
 }
 } // namespace
 
@@ -844,9 +845,9 @@ int tsac_hip_linear_apply(const tsac_hip_device_linear* linear, const uint16_t* 
             const auto s = as_stream(stream);
             const std::size_t K = linear->linear.K;
             const LinearPath chosen = path_of(path);
-            // The GEMM reads MFMA operand tiles; the GEMV reads rows.
+            // The GEMM reads MFMA operand tiles; the GEMV and the small-M GEMM read rows.
             const bool tiles = chosen == LinearPath::gemm ||
-                               (chosen == LinearPath::automatic && M > gemv_max_rows());
+                               (chosen == LinearPath::automatic && M > small_gemm_max_rows());
             const Layout layout = tiles ? Layout::tiles : Layout::rows;
             const std::size_t rows = tiles ? tile_padded_rows(M) : M;
             AsyncScratch scratch(rows * K + rows * (K / 256) * 4 + 256 + 8, s);

@@ -30,7 +30,7 @@ bool supported_width(std::size_t k)
 // rows stays row-major for the GEMV.
 Layout activation_layout(std::size_t rows)
 {
-    return rows > gemv_max_rows() ? Layout::tiles : Layout::rows;
+    return rows > small_gemm_max_rows() ? Layout::tiles : Layout::rows;
 }
 } // namespace
 

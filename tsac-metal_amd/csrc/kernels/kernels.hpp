@@ -87,7 +87,8 @@ enum class LinearPath
 {
     automatic,
     gemv,
-    gemm
+    gemm,
+    small // MFMA on row-major activations, at most 64 rows, K <= 2048
 };
 
 // y[m][n] = bf16(chain_b fma(dot_b, ws[b][n]*as[m][b]) + bias[n]); with a residual,
@@ -97,6 +98,10 @@ void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::si
             uint16_t* y, const uint16_t* residual, LinearPath path, hipStream_t stream,
             Layout layout = Layout::rows);
 std::size_t gemv_max_rows();
+// Rows up to which the automatic path reads row-major activations (GEMV up to
+// gemv_max_rows(), then the small-M MFMA GEMM where K <= 2048); above it the
+// GEMM reads MFMA operand tiles.
+std::size_t small_gemm_max_rows();
 
 // x [M][K] BF16 -> y [M][N] like quantize_rows + linear, with the BF8L buffer in
 // a fixed per-device array (static_linear.hip) instead of caller or allocator

@@ -149,6 +149,116 @@ void launch_gemv(const DeviceLinear& w, const int8_t* q, const float* scales, st
 #undef TSAC_GEMV
 }
 
+// ------------------------------------------------------------------ small M (MFMA)
+//
+// 8 < M <= 64 row-major rows and K <= 2048: one workgroup per 32 output columns
+// and 32-row group, one wave per 256-value block. A wave loads its block's
+// 32 x 256 weights from the row tile straight into registers in the MFMA's
+// operand order (one 512-byte run per half-wave and 32-value k-slice) and its
+// rows' block activations the same way, runs the block's exact int32 dots as
+// 8 MFMAs (32 x 32 x 32), and leaves them in LDS; the ordered chain then runs
+// per (row, column) as in the GEMV, with the scales staged in LDS while the
+// operands arrive. No row is padded to a large tile, and the launch has
+// N / 32 x ceil(M / 32) workgroups (measured: one workgroup per 32 columns for
+// both row groups took 7.9 us at M = 64, K = 1024, N = 1024; split by row
+// group, 5.5 us).
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int small_max_rows = 64;
+constexpr int small_max_blocks = 8;
+constexpr int small_columns = 32;
+constexpr int small_rows = 32;        // rows of a workgroup
+constexpr int small_stride = small_columns + 1; // LDS row stride of the dots, conflict-free writes
+
+__device__ __forceinline__ v4i load_fragment(const int8_t* p)
+{
+    return *reinterpret_cast<const v4i*>(p);
+}
+
+__global__ __launch_bounds__(small_max_blocks * wave) void small_gemm_kernel(
+    const int8_t* __restrict__ weights, const float* __restrict__ weight_scales,
+    const float* __restrict__ bias, int N, int K, const int8_t* __restrict__ q,
+    const float* __restrict__ activation_scales, int M, uint16_t* y, const uint16_t* residual)
+{
+    __shared__ int dots[small_max_blocks * small_rows * small_stride]; // [block][row][column]
+    __shared__ float ws[small_max_blocks * small_columns];              // [block][column]
+    __shared__ float as[small_rows * small_max_blocks];                 // [row][block]
+    __shared__ float bs[small_columns];
+    const int blocks = K / 256;
+    const int tile = blockIdx.x / 2, half = blockIdx.x % 2; // 32 of the 64 rows of a weight row tile
+    const int n0 = blockIdx.x * small_columns, m0 = blockIdx.y * small_rows;
+    const int rows = min(small_rows, M - m0);
+    const int lane = threadIdx.x % wave;
+    const int b = __builtin_amdgcn_readfirstlane(threadIdx.x / wave); // one wave per block
+    // Operands first. A: lane l holds weight row l % 32 of this half, k-slice
+    // values 16 (l / 32) .. +15; the 16-byte segments of a row tile are 1 KiB
+    // apart, two per 32-value slice. B: lane l holds activation row m0 + l % 32
+    // (the last row stands in for rows past M, whose results are not read),
+    // the same values.
+    const int8_t* w = weights + tile_offset(tile, b, lane / 32, blocks) + (half * 32 + lane % 32) * 16;
+    const int8_t* x = q + std::size_t(m0 + min(lane % 32, rows - 1)) * K + b * 256 + (lane / 32) * 16;
+    v4i a[8], u[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+    {
+        a[j] = load_fragment(w + 2 * j * tile_rows * 16);
+        u[j] = load_fragment(x + 32 * j);
+    }
+    for (int i = threadIdx.x; i < blocks * small_columns; i += blockDim.x)
+    {
+        ws[i] = weight_scales[std::size_t(i / small_columns) * N + n0 + i % small_columns];
+    }
+    for (int i = threadIdx.x; i < rows * blocks; i += blockDim.x)
+    {
+        as[i] = activation_scales[std::size_t(m0) * blocks + i];
+    }
+    if (threadIdx.x < small_columns)
+    {
+        bs[threadIdx.x] = bias[n0 + threadIdx.x];
+    }
+    const v16i zero = {};
+    v16i acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], u[0], zero, 0, 0, 0);
+#pragma unroll
+    for (int j = 1; j < 8; ++j)
+    {
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], u[j], acc, 0, 0, 0);
+    }
+    // Lane l, register r: row l % 32, column 8 (r / 4) + 4 (l / 32) + r % 4.
+    int* d = dots + (b * small_rows + lane % 32) * small_stride + 4 * (lane / 32);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+    {
+        d[8 * (r / 4) + r % 4] = acc[r];
+    }
+    __syncthreads();
+    // Ordered chain per (row, column): ascending blocks, one fma each.
+    for (int i = threadIdx.x; i < rows * small_columns; i += blockDim.x)
+    {
+        const int m = i / small_columns, c = i % small_columns;
+        float sum = 0.0f;
+        for (int k = 0; k < blocks; ++k)
+        {
+            const float scale = ws[k * small_columns + c] * as[m * blocks + k];
+            sum = __builtin_fmaf(float(dots[(k * small_rows + m) * small_stride + c]), scale, sum);
+        }
+        const std::size_t index = std::size_t(m0 + m) * N + n0 + c;
+        y[index] = finish(sum, bs[c], residual, index);
+    }
+}
+
+void launch_small_gemm(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M, uint16_t* y,
+                       const uint16_t* residual, hipStream_t stream)
+{
+    require(M >= 1 && M <= std::size_t(small_max_rows) && w.K <= std::size_t(small_max_blocks) * 256,
+            "small-M GEMM: at most 64 rows and K <= 2048");
+    const dim3 grid(unsigned(w.N / small_columns), unsigned((M + small_rows - 1) / small_rows));
+    const unsigned threads = unsigned(w.K / 256) * wave;
+    small_gemm_kernel<<<grid, threads, 0, stream>>>(w.values, w.scales, w.bias, int(w.N), int(w.K), q, scales,
+                                                    int(M), y, residual);
+}
+
 // ------------------------------------------------------------------ GEMM (MFMA)
 //
 // Persistent workgroups (two per CU) walk 128 x 128 output tiles. The tiles of
@@ -163,9 +273,6 @@ void launch_gemv(const DeviceLinear& w, const int8_t* q, const float* scales, st
 // The MFMA's first operand is the weight tile and its second the activations:
 // lane l, register r of a 32 x 32 result holds column n = 8*(r/4) + 4*(l/32) + r%4
 // of row m = l%32, so each lane owns runs of four consecutive outputs of a row.
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 
 namespace gemm
 {
@@ -652,6 +759,11 @@ void launch_gemm(const DeviceLinear& w, const int8_t* q, const float* scales, st
 }
 } // namespace
 
+std::size_t small_gemm_max_rows()
+{
+    return small_max_rows;
+}
+
 std::size_t gemv_max_rows()
 {
     return gemv_max_columns;
@@ -687,13 +799,22 @@ void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::si
     }
     if (path == LinearPath::automatic)
     {
-        path = M <= gemv_max_columns && layout == Layout::rows ? LinearPath::gemv : LinearPath::gemm;
+        path = layout != Layout::rows                          ? LinearPath::gemm
+               : M <= gemv_max_columns                         ? LinearPath::gemv
+               : M <= std::size_t(small_max_rows) && w.K <= std::size_t(small_max_blocks) * 256
+                   ? LinearPath::small
+                   : LinearPath::gemm;
     }
     if (path == LinearPath::gemv)
     {
         require(M <= gemv_max_columns, "gemv: at most 8 columns");
         require(layout == Layout::rows, "gemv: activations must be row-major");
         launch_gemv(w, q, scales, M, y, residual, stream);
+    }
+    else if (path == LinearPath::small)
+    {
+        require(layout == Layout::rows, "small-M GEMM: activations must be row-major");
+        launch_small_gemm(w, q, scales, M, y, residual, stream);
     }
     else
     {

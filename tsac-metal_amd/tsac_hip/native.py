@@ -43,7 +43,7 @@ EXPORTS = (
     "tsac_hip_parse_header", "tsac_hip_cli_parse", "tsac_hip_cli_help",
 )
 
-PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_TILES = 0, 1, 2, 3
+PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GEMM_TILES, PATH_SMALL = 0, 1, 2, 3, 4
 PASS_ENCODE, PASS_DECODE = 0, 1
 
 
