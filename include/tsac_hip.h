@@ -170,7 +170,10 @@ int tsac_hip_distributions(tsac_hip_session* session, const tsac_hip_header* hea
  * because the session was created with TSAC_HIP_FRAME_LAUNCH=plain in the
  * environment (for example to run under a profiler), 2 as plain launches
  * because another process held the device's cooperative-launch resources; -1
- * when the call ran no frame step. No counterpart in the reference; for callers
+ * when the call ran no frame step (an encode runs frame steps only when its
+ * batched pass would not fit Limits::cache_bytes), and [7] 1 when the call's
+ * model work ran step by step (every decode; an encode whose batched pass
+ * would not fit Limits::cache_bytes), else 0. No counterpart in the reference; for callers
  * that report throughput with inputs already in device memory. */
 int tsac_hip_session_timing(const tsac_hip_session* session, double* seconds, size_t count);
 

@@ -647,7 +647,7 @@ std::vector<uint8_t> Session::encode_audio(const DacModel& dac, const float* sam
                                                : encode(h, tokens.data(), tokens.size(), observer);
     const auto model = timing_;
     timing_ = {t1 - t0 + (h.method ? model[0] : 0.0), h.method ? model[1] : 0.0, now() - t0, model[3], 0.0, 0.0,
-               -1.0};
+               h.method ? model[6] : -1.0, h.method ? model[7] : 0.0};
     return bytes;
 }
 
@@ -666,7 +666,7 @@ std::vector<float> Session::decode_audio(const DacModel& dac, const uint8_t* str
     std::vector<float> pcm(h.frames * 512 * *channels);
     synthesize(dac, tokens.data(), h.frames, h.groups, h.codebooks, pcm.data());
     timing_ = {now() - t1 + (h.method ? model[0] : 0.0), 0.0, now() - t0, 0.0, model[4], model[5],
-               h.method ? model[6] : -1.0};
+               h.method ? model[6] : -1.0, h.method ? model[7] : 0.0};
     return pcm;
 }
 

@@ -375,6 +375,14 @@ void Session::validate(const Header& h, const uint16_t* tokens, std::size_t coun
     }
     const std::size_t independent = checked_mul(std::min<std::size_t>(h.batch, h.frames), h.groups);
     require(independent <= limits.tensor_elements, "independent lane count is above Limits::tensor_elements");
+    require(persistent_cache_bytes(h) <= limits.cache_bytes,
+            "key/value caches would exceed Limits::cache_bytes: lower the entropy batch or the channel count");
+}
+
+std::size_t Session::persistent_cache_bytes(const Header& h) const
+{
+    const Geometry& g = model_->geometry();
+    const std::size_t independent = checked_mul(std::min<std::size_t>(h.batch, h.frames), h.groups);
     const std::size_t base = h.frames / h.batch, extra = h.frames % h.batch;
     const std::size_t contexts = checked_mul(
         h.groups, checked_add(checked_mul(h.batch - extra, std::min<std::size_t>(base, g.context)),
@@ -383,8 +391,62 @@ void Session::validate(const Header& h, const uint16_t* tokens, std::size_t coun
         checked_mul(contexts, std::size_t(g.temporal_layers) * g.width * 2 * sizeof(uint16_t));
     const std::size_t codebook_bytes = checked_mul(
         checked_mul(independent, h.codebooks), std::size_t(g.codebook_layers) * g.width * 2 * sizeof(uint16_t));
-    require(checked_add(temporal_bytes, codebook_bytes) <= limits.cache_bytes,
-            "key/value caches would exceed Limits::cache_bytes: lower the entropy batch or the channel count");
+    return checked_add(temporal_bytes, codebook_bytes);
+}
+
+Session::KnownPlan Session::plan_known(const Header& h) const
+{
+    const Geometry& g = model_->geometry();
+    const std::size_t C = h.codebooks, w = g.width, steps = h.frames * h.groups;
+    const std::size_t widest = std::max<std::size_t>({w, g.ffn, g.latent});
+    // Device scratch of the batched pass (the arena entries of temporal_rows,
+    // batched and stack_rows), per batch of `rows` rows.
+    const auto quantised = [&](std::size_t rows) { return tile_padded_rows(rows) * (widest + widest / 64); };
+    const auto temporal = [&](std::size_t rows)
+    { return rows * (2 * C + 2 * g.latent + 10 * w + 2 * g.ffn + 8) + quantised(rows); };
+    const auto codebook = [&](std::size_t rows)
+    { return rows * (2 * g.latent + 10 * w + 4 * g.alphabet + 2 * g.ffn + 32) + quantised(rows); };
+    const std::size_t limit = model_->limits().cache_bytes;
+    const std::size_t used = checked_add(persistent_cache_bytes(h), steps * (2 * w + 2 * C)); // + conditioning, tokens
+    const Lanes lanes(h);
+    const std::size_t longest = std::min<std::size_t>(lanes.length(0), g.context); // longest sequence
+    // Temporal rows of the whole pass: every (frame, group), plus 256 replayed
+    // frames per rollover.
+    std::size_t all_rows = 0;
+    for (std::size_t lane = 0; lane < lanes.count; ++lane)
+    {
+        const std::size_t length = lanes.length(lane);
+        const std::size_t rollovers = length > g.context ? (length - g.context - 1) / (g.context - replay_frames) + 1 : 0;
+        all_rows += h.groups * (length + rollovers * replay_frames);
+    }
+    KnownPlan plan;
+    for (const std::size_t t : {std::min(all_rows, std::max(batch_rows, longest)), longest})
+    {
+        std::size_t n = std::min(steps, std::max<std::size_t>(1, batch_rows / C));
+        const auto fits = [&](std::size_t chunk) { return used + temporal(t) + codebook(chunk * C) <= limit; };
+        if (!fits(1))
+        {
+            continue;
+        }
+        std::size_t lo = 1, hi = n; // the largest chunk that fits
+        while (lo < hi)
+        {
+            const std::size_t mid = (lo + hi + 1) / 2;
+            if (fits(mid))
+            {
+                lo = mid;
+            }
+            else
+            {
+                hi = mid - 1;
+            }
+        }
+        plan.temporal_rows = t;
+        plan.codebook_steps = lo;
+        return plan;
+    }
+    plan.stepwise = true;
+    return plan;
 }
 
 // One transformer stack over rows with causal prefill attention
@@ -427,7 +489,8 @@ void Session::stack_rows(bool temporal, uint16_t* x, std::size_t rows, const int
 // Temporal conditioning of every (frame, group) for known tokens: each lane's
 // context positions form causal sequences; a rollover starts a new sequence
 // with the last 256 complete frames replayed (src/common/transformer.cpp:184-211).
-void Session::temporal_rows(const Header& h, const uint16_t* tokens, uint16_t* conditioning)
+void Session::temporal_rows(const Header& h, const uint16_t* tokens, uint16_t* conditioning,
+                            std::size_t batch_rows)
 {
     const Geometry& g = model_->geometry();
     const Model& m = *model_;
@@ -547,7 +610,7 @@ void Session::temporal_rows(const Header& h, const uint16_t* tokens, uint16_t* c
 }
 
 void Session::batched(const Header& h, const uint16_t* tokens, uint16_t* distributions,
-                      uint16_t* splits)
+                      uint16_t* splits, const KnownPlan& plan)
 {
     const Geometry& g = model_->geometry();
     const Model& m = *model_;
@@ -559,10 +622,10 @@ void Session::batched(const Header& h, const uint16_t* tokens, uint16_t* distrib
     }
     auto* err = errors_.as<uint32_t>();
     auto* conditioning = arena_.get<uint16_t>("cond", steps * w);
-    temporal_rows(h, tokens, conditioning);
+    temporal_rows(h, tokens, conditioning, plan.temporal_rows);
     auto* d_tokens = arena_.get<uint16_t>("tokens", steps * C);
     upload_input(d_tokens, tokens, steps * C * 2);
-    const std::size_t chunk_steps = std::max<std::size_t>(1, batch_rows / C);
+    const std::size_t chunk_steps = plan.codebook_steps;
     // Codebook sequences: step i of a chunk is rows i*C .. i*C+C-1.
     {
         std::vector<int> info(3 * chunk_steps);
@@ -629,7 +692,16 @@ std::vector<uint8_t> Session::encode(Header h, const uint16_t* tokens, std::size
     const uint32_t crc = token_crc32(tokens, count);
     std::vector<uint16_t> splits(count * 16);
     reset_errors();
-    batched(h, tokens, nullptr, splits.data());
+    const KnownPlan plan = plan_known(h);
+    frame_launch_ = -1;
+    if (plan.stepwise)
+    {
+        stepwise(h, tokens, nullptr, 0, nullptr, nullptr, splits.data());
+    }
+    else
+    {
+        batched(h, tokens, nullptr, splits.data(), plan);
+    }
     check_errors();
     const double t1 = now();
     // Host range coding in stream order (src/format/entropy.cpp:57-100): the ten
@@ -668,7 +740,8 @@ std::vector<uint8_t> Session::encode(Header h, const uint16_t* tokens, std::size
     });
     const auto bytes = frame_normal(h, crc, encoder.finish());
     const double t2 = now();
-    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), 0.0, 0.0, -1.0};
+    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), 0.0, 0.0, double(frame_launch_),
+               plan.stepwise ? 1.0 : 0.0};
     return bytes;
 }
 
@@ -707,7 +780,7 @@ std::vector<uint16_t> Session::decode(const uint8_t* stream, std::size_t length,
             "decoded tokens fail the stream's CRC-32 check");
     const double t2 = now();
     const double steps = double(Lanes(h).steps());
-    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), steps_seconds(), steps, double(frame_launch_)};
+    timing_ = {t1 - t0, t2 - t1, t2 - t0, input_seconds(), steps_seconds(), steps, double(frame_launch_), 1.0};
     return tokens;
 }
 
@@ -723,14 +796,19 @@ void Session::distributions(Header h, const uint16_t* tokens, std::size_t count,
     {
         stepwise(h, tokens, nullptr, 0, nullptr, out);
     }
+    else if (const KnownPlan plan = plan_known(h); plan.stepwise)
+    {
+        stepwise(h, tokens, nullptr, 0, nullptr, out);
+        decode_pass = true;
+    }
     else
     {
-        batched(h, tokens, out, nullptr);
+        batched(h, tokens, out, nullptr, plan);
     }
     check_errors();
     const double t1 = now();
     const double steps = decode_pass ? double(Lanes(h).steps()) : 0.0;
     timing_ = {t1 - t0, 0.0, t1 - t0, input_seconds(), decode_pass ? steps_seconds() : 0.0, steps,
-               decode_pass ? double(frame_launch_) : -1.0};
+               decode_pass ? double(frame_launch_) : -1.0, decode_pass ? 1.0 : 0.0};
 }
 } // namespace tsac_hip

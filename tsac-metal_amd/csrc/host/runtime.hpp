@@ -230,8 +230,10 @@ public:
     // frame-step loop between two events on the session stream, the number of
     // frame steps in it, and how its frame steps were launched (FrameLaunch:
     // 0 cooperative, 1 plain on request, 2 plain because another process held
-    // the cooperative-launch resources; -1 when the call ran none).
-    std::array<double, 7> timing() const
+    // the cooperative-launch resources; -1 when the call ran none), and 1 when
+    // the call's model work ran step by step (decode; an encode whose batched
+    // pass would not fit Limits::cache_bytes), else 0.
+    std::array<double, 8> timing() const
     {
         return timing_;
     }
@@ -251,20 +253,38 @@ private:
     // GPU seconds between the events around the last stepwise loop.
     double steps_seconds();
     void validate(const Header& h, const uint16_t* tokens, std::size_t count) const;
+    // Bytes of the persistent key/value caches the header's lanes need
+    // (src/common/cpu_transformer.tpp:285-305), which Limits::cache_bytes bounds.
+    std::size_t persistent_cache_bytes(const Header& h) const;
+    // How a known-token pass runs within Limits::cache_bytes: the batched pass
+    // computes whole sequences and many frames of codebook rows ahead, and its
+    // scratch (with the persistent caches) must fit the limit, as the lookahead
+    // of the reference's Metal encoder must (src/metal/transformer/encoding.mm:139-150);
+    // it shrinks its batches to fit, and where not even one sequence and one
+    // step fit, the pass runs step by step on the frame-step path instead.
+    struct KnownPlan
+    {
+        bool stepwise = false;
+        std::size_t temporal_rows = 0; // rows per temporal batch (whole sequences)
+        std::size_t codebook_steps = 0; // frame steps per codebook chunk
+    };
+    KnownPlan plan_known(const Header& h) const;
     // Batched known-token pass. Writes either the BF16 distributions of every
     // token (distributions != null) or its ten Q15 splits (splits != null).
     void batched(const Header& h, const uint16_t* tokens, uint16_t* distributions,
-                 uint16_t* splits);
-    void temporal_rows(const Header& h, const uint16_t* tokens, uint16_t* conditioning);
+                 uint16_t* splits, const KnownPlan& plan);
+    void temporal_rows(const Header& h, const uint16_t* tokens, uint16_t* conditioning, std::size_t batch_rows);
     void stack_rows(bool temporal, uint16_t* x, std::size_t rows, const int* starts,
                     const int* lengths, const int* replays, std::size_t sequences,
                     std::size_t max_length, const std::string& tag);
     // Stepwise pass, enqueued without host round trips. `known` tokens are
     // teacher-forced when non-null; otherwise symbols are range-decoded on the
     // GPU from `payload`. Writes tokens (and, if requested, the BF16
-    // distributions) in token order.
+    // distributions, or with known tokens each token's ten Q15 splits,
+    // [symbols][16]) in token order.
     void stepwise(const Header& h, const uint16_t* known, const uint8_t* payload,
-                  std::size_t payload_bytes, uint16_t* tokens_out, uint16_t* distributions);
+                  std::size_t payload_bytes, uint16_t* tokens_out, uint16_t* distributions,
+                  uint16_t* splits = nullptr);
     // position: host value, or read from device_position when that is non-null.
     void layer_step(bool temporal, std::size_t layer, uint16_t* x, std::size_t rows,
                     std::size_t first_lane, std::size_t position, const int* device_position,
@@ -275,7 +295,7 @@ private:
     Arena arena_;
     DeviceBuffer errors_;
     PinnedBuffer pinned_errors_, staging_, staging_nodes_, staging_tokens_;
-    std::array<double, 7> timing_{};
+    std::array<double, 8> timing_{};
     // TSAC_HIP_FRAME_LAUNCH=plain in the environment when the session was
     // created: frame steps go out as plain launches (see FrameArgs::plain_launch).
     bool plain_frame_launch_ = false;

@@ -131,7 +131,8 @@ void Session::layer_step(bool temporal, std::size_t layer, uint16_t* x, std::siz
 }
 
 void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* payload,
-                       std::size_t payload_bytes, uint16_t* tokens_out, uint16_t* distributions)
+                       std::size_t payload_bytes, uint16_t* tokens_out, uint16_t* distributions,
+                       uint16_t* splits)
 {
     frame_launch_ = -1;
     const Geometry& g = model_->geometry();
@@ -204,6 +205,8 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
     {
         d_distributions = arena_.get<uint16_t>("s.distributions", symbols * g.alphabet);
     }
+    require(!splits || known, "stepwise: splits need known tokens");
+    uint16_t* d_splits = splits ? arena_.get<uint16_t>("s.splits", symbols * 16) : nullptr;
     // Host data above must reach the device before the host buffers go away.
     check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
 
@@ -298,6 +301,7 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
                 sample.step_stride = int(G * C);
                 sample.known = d_known;
                 sample.distributions = d_distributions;
+                sample.splits = d_splits;
                 sample.state = known ? nullptr : state;
                 sample.payload = d_payload;
                 sample.payload_bytes = payload_bytes;
@@ -358,6 +362,7 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
         frame.tokens = tokens;
         frame.known = d_known;
         frame.distributions = d_distributions;
+        frame.splits = d_splits;
         frame.state = known ? nullptr : state;
         frame.payload = d_payload;
         frame.payload_bytes = payload_bytes;
@@ -464,6 +469,10 @@ void Session::stepwise(const Header& h, const uint16_t* known, const uint8_t* pa
         check_hip(hipMemcpyAsync(distributions, d_distributions, symbols * g.alphabet * 2,
                                  hipMemcpyDeviceToHost, stream_),
                   "read distributions");
+    }
+    if (splits)
+    {
+        check_hip(hipMemcpyAsync(splits, d_splits, symbols * 16 * 2, hipMemcpyDeviceToHost, stream_), "read splits");
     }
     check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
 }

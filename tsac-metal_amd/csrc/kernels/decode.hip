@@ -535,12 +535,15 @@ __global__ __launch_bounds__(sample_waves * wave) void sample_kernel(const Sampl
         {
             store_row<16>(a.distributions + std::size_t(row) * 1024 + lane * 16, v);
         }
-        if (a.state)
+        if (a.state || a.splits)
         {
             store_row<16>(&leaves[warp][lane * 16], v);
             const bool ok = build_masses(p, lane, nodes[warp]);
             wait_shared_memory();
-            build_top_decisions(lane, Masses{nodes[warp], leaves[warp]}, top[warp]);
+            if (a.state)
+            {
+                build_top_decisions(lane, Masses{nodes[warp], leaves[warp]}, top[warp]);
+            }
             if (lane == 0)
             {
                 valid[warp] = ok;
@@ -566,6 +569,14 @@ __global__ __launch_bounds__(sample_waves * wave) void sample_kernel(const Sampl
         if (a.known)
         {
             token = a.known[r];
+            if (a.splits)
+            {
+                const uint16_t q = path_split(Masses{nodes[w], leaves[w]}, token, lane);
+                if (lane < 10)
+                {
+                    a.splits[std::size_t(r) * 16 + lane] = q;
+                }
+            }
         }
         else
         {

@@ -93,6 +93,7 @@ struct Sample
     int step_stride = 0;              // token offset between consecutive frames of a lane
     const uint16_t* known = nullptr;  // teacher forcing: take tokens from here
     uint16_t* distributions = nullptr; // optional [symbols][1024] BF16 output
+    uint16_t* splits = nullptr;       // known tokens, optional: [symbols][16], the ten Q15 splits of each
     DecoderState* state = nullptr;    // range decoder (null with known tokens)
     const uint8_t* payload = nullptr;
     unsigned long long payload_bytes = 0;

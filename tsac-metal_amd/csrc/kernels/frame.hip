@@ -1809,6 +1809,7 @@ struct Draw
     int step = 0, step_stride = 0;
     const uint16_t* known = nullptr;
     uint16_t* distributions = nullptr;
+    uint16_t* splits = nullptr; // known tokens: each token's ten Q15 splits at [row][16]
     const uint8_t* payload = nullptr;
     unsigned long long payload_bytes = 0;
 };
@@ -2091,6 +2092,7 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
     a.step_stride = uniform(job->step_stride);
     a.known = uniform(job->known);
     a.distributions = uniform(job->distributions);
+    a.splits = uniform(job->splits);
     a.payload = uniform(job->payload);
     a.payload_bytes = uniform(std::size_t(job->payload_bytes));
     M = uniform(M);
@@ -2106,6 +2108,9 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
     const int lane = threadIdx.x % wave, warp = __builtin_amdgcn_readfirstlane(int(threadIdx.x / wave));
     const bool active = warp < M;
     const bool decoding = a.known == nullptr;
+    // Known tokens with splits: the masses are built as for decoding, and each
+    // token's path splits are taken from them instead of a decode.
+    const bool splitting = !decoding && a.splits != nullptr;
     int row = 0;
     if (active)
     {
@@ -2137,7 +2142,7 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
         const int first_row = *global(a.row_base) + a.step * a.step_stride + a.book;
         const bool ok = first_lane_masses(a.logits, a.distributions ? a.distributions + std::size_t(first_row) * 1024
                                                                     : nullptr,
-                                          decoding, x, error, nodes, leaves, partials);
+                                          decoding || splitting, x, error, nodes, leaves, partials);
         if (warp == 0)
         {
             if (decoding)
@@ -2196,12 +2201,15 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
         {
             store_row<16>(a.distributions + std::size_t(row) * 1024 + lane * 16, v);
         }
-        if (decoding)
+        if (decoding || splitting)
         {
             store_row<16>(leaves + warp * 1024 + lane * 16, v);
             const bool ok = build_masses(prob, lane, nodes + warp * 1024);
             wait_shared_memory();
-            build_top_decisions(lane, Masses{nodes + warp * 1024, leaves + warp * 1024}, top + warp * 64);
+            if (decoding)
+            {
+                build_top_decisions(lane, Masses{nodes + warp * 1024, leaves + warp * 1024}, top + warp * 64);
+            }
             if (lane == 0)
             {
                 valid[warp] = ok;
@@ -2246,7 +2254,16 @@ __device__ __noinline__ JOB void draw_tokens(constant_ptr<Draw> job, int step, i
         for (int w = 0; w < M; ++w)
         {
             const int r = wait_for_lane(w);
-            output(w, r, *global(a.known + r));
+            const int token = *global(a.known + r);
+            output(w, r, token);
+            if (splitting)
+            {
+                const uint16_t q = path_split(Masses{nodes + w * 1024, leaves + w * 1024}, token, lane);
+                if (lane < 10)
+                {
+                    *global_out(a.splits + std::size_t(r) * 16 + lane) = q;
+                }
+            }
         }
         return;
     }
@@ -2788,6 +2805,7 @@ std::vector<uint8_t> frame_job_table(const FrameArgs& a)
         d.step_stride = a.step_stride;
         d.known = a.known;
         d.distributions = a.distributions;
+        d.splits = a.splits;
         d.payload = a.payload;
         d.payload_bytes = a.payload_bytes;
         put(T.draw_offset(b), d);

@@ -66,6 +66,7 @@ struct FrameArgs
     uint16_t* tokens = nullptr;
     const uint16_t* known = nullptr;
     uint16_t* distributions = nullptr;
+    uint16_t* splits = nullptr; // known tokens, optional: [symbols][16], the ten Q15 splits of each
     DecoderState* state = nullptr;
     const uint8_t* payload = nullptr;
     unsigned long long payload_bytes = 0;

@@ -155,6 +155,16 @@ __device__ __forceinline__ uint16_t node_q15(const Masses& mass, float entering,
     return q15(own_left, entering);
 }
 
+// encode_categorical (src/format/categorical.cpp:95-117) for a known symbol:
+// the Q15 split of each of the ten decisions along its bisection path. Lane k
+// (k < 10) returns decision k's: the node at depth k on the path to leaf
+// 1024 + symbol, entered from the root with mass 1.
+__device__ __forceinline__ uint16_t path_split(const Masses& mass, int symbol, int lane)
+{
+    const int depth = lane < 10 ? lane : 9;
+    return node_q15<9>(mass, 1.0f, (1024 + symbol) >> (10 - depth), depth);
+}
+
 // q(1..63), lane l computing node l; lane 0 writes nothing.
 __device__ __forceinline__ void build_top_decisions(int lane, const Masses& mass, uint16_t* top)
 {

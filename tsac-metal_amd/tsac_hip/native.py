@@ -590,10 +590,10 @@ class HipSession:
                     2: "plain (cooperative-launch resources held by another process)"}
 
     def timing(self):
-        t = (C.c_double * 7)()
-        check(library().tsac_hip_session_timing(self.handle, t, 7))
+        t = (C.c_double * 8)()
+        check(library().tsac_hip_session_timing(self.handle, t, 8))
         return {"model": t[0], "range_coding": t[1], "total": t[2], "input_upload": t[3], "steps_gpu": t[4],
-                "steps": int(t[5]), "frame_launch": self.FRAME_LAUNCH[int(t[6])]}
+                "steps": int(t[5]), "frame_launch": self.FRAME_LAUNCH[int(t[6])], "stepwise": bool(t[7])}
 
 
 def prepare_rvq(codebook, in_v, in_g, out_v, out_g):
