@@ -186,16 +186,26 @@ def test_reference_geometry_lane_counts(native, oracle, reference_model, frames,
     assert np.array_equal(session.decode(stream), tokens)
 
 
-def test_wide_geometry(native, oracle):
-    """Width 1024, FFN 4096, 16 x 64 heads."""
+@pytest.fixture(scope="module")
+def wide_model(native):
     model = random_model(WIDE, seed=2)
     hip_model = native.HipModel(model)
-    h = native.header(2, 2, 1, 12)
-    tokens = random_tokens(2, 1, 12, seed=4)
+    yield model, hip_model
+    hip_model.close()
+
+
+@pytest.mark.parametrize("frames,batch", [(2, 2), (3, 1), (8, 8)])
+def test_wide_geometry(native, oracle, wide_model, frames, batch):
+    """Width 1024, FFN 4096, 16 x 64 heads: two codebook heads per wave in the
+    out tiles, which run on the attention workgroups; with 8 lanes the groups
+    are scaled down and each of those workgroups takes several tiles."""
+    model, hip_model = wide_model
+    h = native.header(frames, batch, 1, 12)
+    tokens = random_tokens(frames, 1, 12, seed=4 + batch)
     encode, decode = _both_passes(native, hip_model, h, tokens)
     from oracle import header
 
-    expected = oracle.model(model).distributions(header(2, 2, 1, 12), tokens, threads=2)
+    expected = oracle.model(model).distributions(header(frames, batch, 1, 12), tokens, threads=4)
     assert np.array_equal(encode, decode)
     assert np.array_equal(encode, expected)
 

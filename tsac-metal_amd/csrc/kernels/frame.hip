@@ -571,83 +571,109 @@ template <int V> constexpr int projection_lds()
 // fp32 keys (padded rows), the value words and the query's weights.
 template <int HW> constexpr int book_head_floats = HW + max_books * staged_key_stride<HW> + max_books * HW / 2 + wave;
 
-// A projection computes codebook attention rows when every head has a wave of
-// its own (width / HW <= frame_waves): per-wave head regions, then the lane's
-// BF16 attention row, after the projection's own LDS.
-template <int V, int HW> constexpr bool book_attention_fits = HW > 0 && wave * V / HW <= frame_waves;
+// A projection computes codebook attention rows when each wave has at most
+// two heads (width / HW <= 2 * frame_waves; wave w takes heads w and
+// w + frame_waves): per-head regions, then the lane's BF16 attention row,
+// after the projection's own LDS.
+constexpr int max_book_heads_per_wave = 2;
+template <int V, int HW> constexpr int book_heads = HW > 0 ? wave * V / HW : 0;
+template <int V, int HW>
+constexpr bool book_attention_fits = HW > 0 && book_heads<V, HW> <= max_book_heads_per_wave * frame_waves;
 template <int V, int HW> constexpr int book_attention_lds()
 {
-    return book_attention_fits<V, HW> ? (wave * V / HW) * book_head_floats<HW> * 4 + wave * V * 2 : 0;
+    return book_attention_fits<V, HW> ? book_heads<V, HW> * book_head_floats<HW> * 4 + wave * V * 2 : 0;
 }
 
-// One codebook attention head of lane m over keys 0 .. time-1 (time <=
-// max_books: one block of attend_item, which computes the same values in the
-// same order) by one wave; the head's BF16 outputs go to row[head*HW ...].
-// The books before the current one were published long before this job, so
-// their key and value words are requested first, and only the current book's
-// query, key and value words are polled for.
+// The `count` (<= H) codebook attention heads head0, head0 + frame_waves, ...
+// of lane m over keys 0 .. time-1 (time <= max_books: one block of
+// attend_item, which computes the same values in the same order) by one wave;
+// head h is staged in regions + h * book_head_floats<HW> and its BF16 outputs
+// go to row[h*HW ...]. The books before the current one were published long
+// before this job, so the key and value words of all the wave's heads for
+// those books are requested first, and only then are the current book's
+// query, key and value words polled for.
 // A thread given `residual` also requests that word as soon as the current
 // book's words are in (the residual row is the layer's input, which the qkv
 // job consumed before it published them), into `residual_seen`.
-template <int HW>
-__device__ __forceinline__ void book_head(const word* qkv, std::size_t book_words, int time, int width, float scale,
-                                          int m, int head, const Exchange& x, float* scratch, uint16_t* row,
-                                          const word* residual, word& residual_seen)
+template <int HW, int H>
+__device__ __forceinline__ void wave_book_heads(const word* qkv, std::size_t book_words, int time, int width,
+                                                float scale, int m, int head0, int count, const Exchange& x,
+                                                float* regions, uint16_t* row, const word* residual,
+                                                word& residual_seen)
 {
     constexpr int per_lane = HW / 64, key_stride = staged_key_stride<HW>;
-    float* query = scratch;                                                          // [HW]
-    float* keys = query + HW;                                                        // [max_books][key_stride]
-    uint32_t* values = reinterpret_cast<uint32_t*>(keys + max_books * key_stride);  // [max_books][HW/2]
-    float* weights = reinterpret_cast<float*>(values + max_books * HW / 2);         // [wave]
     const int lane = threadIdx.x % wave;
-    const std::size_t query_word = (std::size_t(m) * 3 * width + head * HW) / 2;
-    const std::size_t key_word = query_word + width / 2, value_word = query_word + width;
+    // Staging of head h: the fp32 query [HW], fp32 keys [max_books][key_stride],
+    // value words [max_books][HW/2], the query's weights [wave].
+    const auto query_of = [&](int h) { return regions + h * book_head_floats<HW>; };
+    const auto keys_of = [&](int h) { return query_of(h) + HW; };
+    const auto values_of = [&](int h) { return reinterpret_cast<uint32_t*>(keys_of(h) + max_books * key_stride); };
+    const auto head_of = [&](int k) { return head0 + k * frame_waves; };
+    // Word of value index head*HW of lane m's qkv row: query, then key (+width/2), value (+width).
+    const auto query_word = [&](int h) { return (std::size_t(m) * 3 * width + std::size_t(h) * HW) / 2; };
     const auto pair = [](uint32_t w) { return make_float2(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)); };
 
-    // 1. Earlier books, four at a time (one request of all their words each):
-    //    word i of book r is key word i for i < HW/2, else value word i - HW/2.
-    const int older = (time - 1) * HW;
-    constexpr int chunk_books = 4, per_thread = chunk_books * HW / wave;
-    for (int first = 0; first < older; first += chunk_books * HW)
+    // 1. Earlier books, four at a time for all the wave's heads (one request
+    //    of all their words each): word i of (book r, head) is key word i for
+    //    i < HW/2, else value word i - HW/2.
+    const int older = (time - 1) * HW; // words per head
+    constexpr int chunk = 4 * HW, per_thread = H * chunk / wave;
+    for (int first = 0; first < older; first += chunk)
     {
         uint32_t got[per_thread];
+        // Word i of this lane: head k, offset o of that head's earlier words.
+        const auto locate = [&](int i, int& k, int& o)
+        {
+            const int w = lane + i * wave;
+            k = w / chunk;
+            o = first + w % chunk;
+            return k < count && o < older;
+        };
         const auto address = [&](int i) -> const word*
         {
-            int w = first + lane + i * wave;
-            w = w < older ? w : older - 1;
-            const int r = w / HW, c = w % HW;
-            return qkv + std::size_t(r) * book_words + (c < HW / 2 ? key_word + c : value_word + (c - HW / 2));
+            int k, o;
+            if (!locate(i, k, o))
+            {
+                k = 0;
+                o = first;
+            }
+            const int r = o / HW, c = o % HW;
+            const std::size_t q = query_word(head_of(k));
+            return qkv + std::size_t(r) * book_words + (c < HW / 2 ? q + width / 2 + c : q + width + (c - HW / 2));
         };
         take_words<per_thread>(address, x, got);
 #pragma unroll
         for (int i = 0; i < per_thread; ++i)
         {
-            const int w = first + lane + i * wave;
-            const int r = w / HW, c = w % HW;
-            if (w < older)
+            int k, o;
+            if (locate(i, k, o))
             {
+                const int h = head_of(k), r = o / HW, c = o % HW;
                 if (c < HW / 2)
                 {
-                    reinterpret_cast<float2*>(keys + r * key_stride)[c] = pair(got[i]);
+                    reinterpret_cast<float2*>(keys_of(h) + r * key_stride)[c] = pair(got[i]);
                 }
                 else
                 {
-                    values[r * (HW / 2) + c - HW / 2] = got[i];
+                    values_of(h)[r * (HW / 2) + c - HW / 2] = got[i];
                 }
             }
         }
     }
-    // 2. The current book: query words, then key words, then value words.
+    // 2. The current book, head by head: query words, then key words, then
+    //    value words.
     {
-        constexpr int count = 3 * HW / 2, per_thread = (count + wave - 1) / wave;
-        const int r = time - 1;
+        constexpr int row_words = 3 * HW / 2, per_thread = (H * row_words + wave - 1) / wave;
+        const int r = time - 1, total = count * row_words;
         const word* base = qkv + std::size_t(r) * book_words;
         uint32_t got[per_thread];
         const auto address = [&](int i) -> const word*
         {
             int w = lane + i * wave;
-            w = w < count ? w : count - 1;
-            return base + (w < HW / 2 ? query_word + w : w < HW ? key_word + (w - HW / 2) : value_word + (w - HW));
+            w = w < total ? w : total - 1;
+            const int k = w / row_words, c = w % row_words;
+            const std::size_t q = query_word(head_of(k));
+            return base + (c < HW / 2 ? q + c : c < HW ? q + width / 2 + (c - HW / 2) : q + width + (c - HW));
         };
         take_words<per_thread>(address, x, got);
         if (residual)
@@ -658,17 +684,21 @@ __device__ __forceinline__ void book_head(const word* qkv, std::size_t book_word
         for (int i = 0; i < per_thread; ++i)
         {
             const int w = lane + i * wave;
-            if (w < HW / 2)
+            if (w < total)
             {
-                reinterpret_cast<float2*>(query)[w] = pair(got[i]);
-            }
-            else if (w < HW)
-            {
-                reinterpret_cast<float2*>(keys + r * key_stride)[w - HW / 2] = pair(got[i]);
-            }
-            else if (w < count)
-            {
-                values[r * (HW / 2) + w - HW] = got[i];
+                const int h = head_of(w / row_words), c = w % row_words;
+                if (c < HW / 2)
+                {
+                    reinterpret_cast<float2*>(query_of(h))[c] = pair(got[i]);
+                }
+                else if (c < HW)
+                {
+                    reinterpret_cast<float2*>(keys_of(h) + r * key_stride)[c - HW / 2] = pair(got[i]);
+                }
+                else
+                {
+                    values_of(h)[r * (HW / 2) + c - HW] = got[i];
+                }
             }
         }
     }
@@ -678,117 +708,220 @@ __device__ __forceinline__ void book_head(const word* qkv, std::size_t book_word
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
 
-    // 3. Scores (src/scalar/attention.cpp:27-35): lane t dots key row t with
-    //    the query in ascending coordinates; operands requested `ahead`
-    //    chunks before their use.
-    float score = -__builtin_inff();
-    if (lane < time)
+    if constexpr (H == 2 && HW == 64)
     {
-        const float4* q4 = reinterpret_cast<const float4*>(query);
-        const float4* k4 = reinterpret_cast<const float4*>(keys + lane * key_stride);
-        constexpr int chunks = HW / 4, ahead = 4;
-        float4 qs[ahead], ks[ahead];
-#pragma unroll
-        for (int c = 0; c < ahead; ++c)
+        if (count == 2)
         {
-            qs[c] = q4[c];
-            ks[c] = k4[c];
-        }
-        float dot = 0.0f;
-#pragma unroll
-        for (int c = 0; c < chunks; ++c)
-        {
-            float4 qc = qs[c % ahead];
-            const float4 kc = ks[c % ahead];
-            if (c + ahead < chunks)
+            // Both heads at once, head head_of(h) in lanes [32h, 32h + 32): key
+            // t (< time <= max_books <= 32) in lane 32h + t for the scores, and
+            // value columns 2j, 2j + 1 in lane 32h + j for the sums. Each score,
+            // sum and column takes the same operations in the same order as in
+            // one block of attend_item; the 32-lane max and pair tree equal the
+            // 64-lane ones whose upper leaves are -inf and +0.
+            const int half = lane / 32, j = lane % 32, head = head_of(half);
+            const float* query = query_of(head);
+            const uint32_t* values = values_of(head);
+            float* weights = reinterpret_cast<float*>(values_of(head) + max_books * HW / 2);
+            float score = -__builtin_inff();
+            if (j < time)
             {
-                qs[c % ahead] = q4[c + ahead];
-                ks[c % ahead] = k4[c + ahead];
+                const float4* q4 = reinterpret_cast<const float4*>(query);
+                const float4* k4 = reinterpret_cast<const float4*>(keys_of(head) + j * key_stride);
+                constexpr int chunks = HW / 4, ahead = 4;
+                float4 qs[ahead], ks[ahead];
+#pragma unroll
+                for (int c = 0; c < ahead; ++c)
+                {
+                    qs[c] = q4[c];
+                    ks[c] = k4[c];
+                }
+                float dot = 0.0f;
+#pragma unroll
+                for (int c = 0; c < chunks; ++c)
+                {
+                    float4 qc = qs[c % ahead];
+                    const float4 kc = ks[c % ahead];
+                    if (c + ahead < chunks)
+                    {
+                        qs[c % ahead] = q4[c + ahead];
+                        ks[c % ahead] = k4[c + ahead];
+                    }
+                    in_vgprs(qc);
+                    dot = __builtin_fmaf(qc.x, kc.x, dot);
+                    dot = __builtin_fmaf(qc.y, kc.y, dot);
+                    dot = __builtin_fmaf(qc.z, kc.z, dot);
+                    dot = __builtin_fmaf(qc.w, kc.w, dot);
+                }
+                score = dot * scale;
             }
-            in_vgprs(qc);
-            dot = __builtin_fmaf(qc.x, kc.x, dot);
-            dot = __builtin_fmaf(qc.y, kc.y, dot);
-            dot = __builtin_fmaf(qc.z, kc.z, dot);
-            dot = __builtin_fmaf(qc.w, kc.w, dot);
-        }
-        score = dot * scale;
-    }
-    const float maximum = group_max<wave>(score);
-    float e = 0.0f;
-    if (lane < time)
-    {
-        e = original_exp(score - maximum);
-    }
-    const float sum = tree_sum<wave>(e);
-    weights[lane] = e;
-    asm volatile("" ::: "memory");
-    wait_shared_memory();
-    __builtin_amdgcn_wave_barrier();
-    asm volatile("" ::: "memory");
-
-    // 4. Value sums in ascending positions (src/scalar/attention.cpp:41-52).
-    float s[per_lane];
-#pragma unroll
-    for (int i = 0; i < per_lane; ++i)
-    {
-        s[i] = 0.0f;
-    }
-#pragma unroll
-    for (int t = 0; t < max_books; ++t)
-    {
-        if (t < time)
-        {
-            const float w = weights[t];
-            const uint32_t pw = values[t * (HW / 2) + (per_lane * lane) / 2];
-            if constexpr (per_lane == 2)
+            const float maximum = group_max<32>(score);
+            float e = 0.0f;
+            if (j < time)
             {
-                s[0] = __builtin_fmaf(__uint_as_float(pw << 16), w, s[0]);
-                s[1] = __builtin_fmaf(__uint_as_float(pw & 0xffff0000u), w, s[1]);
+                e = original_exp(score - maximum);
+            }
+            const float sum = tree_sum<32>(e);
+            weights[j] = e;
+            asm volatile("" ::: "memory");
+            wait_shared_memory();
+            __builtin_amdgcn_wave_barrier();
+            asm volatile("" ::: "memory");
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int t = 0; t < max_books; ++t)
+            {
+                if (t < time)
+                {
+                    const float w = weights[t];
+                    const uint32_t pw = values[t * (HW / 2) + j];
+                    s0 = __builtin_fmaf(__uint_as_float(pw << 16), w, s0);
+                    s1 = __builtin_fmaf(__uint_as_float(pw & 0xffff0000u), w, s1);
+                }
+            }
+            // The one block merged into the empty state (src/scalar/attention.cpp:86-101).
+            float total, n0, n1;
+            if (is_finite(maximum))
+            {
+                total = sum + 0.0f;
+                n0 = s0 + 0.0f;
+                n1 = s1 + 0.0f;
             }
             else
             {
-                const uint32_t v = (lane & 1) ? (pw >> 16) : (pw & 0xffffu);
-                s[0] = __builtin_fmaf(__uint_as_float(v << 16), w, s[0]);
+                const float running_maximum = -__builtin_inff();
+                const float factor = original_exp(-__builtin_fabsf(maximum - running_maximum));
+                const float old_scale = running_maximum > maximum ? 1.0f : factor;
+                const float new_scale = running_maximum > maximum ? factor : 1.0f;
+                total = __builtin_fmaf(sum, new_scale, 0.0f * old_scale);
+                n0 = __builtin_fmaf(s0, new_scale, 0.0f * old_scale);
+                n1 = __builtin_fmaf(s1, new_scale, 0.0f * old_scale);
+            }
+            const float reciprocal = 1.0f / total;
+            *reinterpret_cast<uint32_t*>(row + head * HW + 2 * j) =
+                float_to_bf16(n0 * reciprocal) | (uint32_t(float_to_bf16(n1 * reciprocal)) << 16);
+            return;
+        }
+    }
+#pragma unroll 1
+    for (int k = 0; k < count; ++k)
+    {
+        const int head = head_of(k);
+        const float* query = query_of(head);
+        const float* keys = keys_of(head);
+        const uint32_t* values = values_of(head);
+        float* weights = reinterpret_cast<float*>(values_of(head) + max_books * HW / 2);
+        // 3. Scores (src/scalar/attention.cpp:27-35): lane t dots key row t with
+        //    the query in ascending coordinates; operands requested `ahead`
+        //    chunks before their use.
+        float score = -__builtin_inff();
+        if (lane < time)
+        {
+            const float4* q4 = reinterpret_cast<const float4*>(query);
+            const float4* k4 = reinterpret_cast<const float4*>(keys + lane * key_stride);
+            constexpr int chunks = HW / 4, ahead = 4;
+            float4 qs[ahead], ks[ahead];
+#pragma unroll
+            for (int c = 0; c < ahead; ++c)
+            {
+                qs[c] = q4[c];
+                ks[c] = k4[c];
+            }
+            float dot = 0.0f;
+#pragma unroll
+            for (int c = 0; c < chunks; ++c)
+            {
+                float4 qc = qs[c % ahead];
+                const float4 kc = ks[c % ahead];
+                if (c + ahead < chunks)
+                {
+                    qs[c % ahead] = q4[c + ahead];
+                    ks[c % ahead] = k4[c + ahead];
+                }
+                in_vgprs(qc);
+                dot = __builtin_fmaf(qc.x, kc.x, dot);
+                dot = __builtin_fmaf(qc.y, kc.y, dot);
+                dot = __builtin_fmaf(qc.z, kc.z, dot);
+                dot = __builtin_fmaf(qc.w, kc.w, dot);
+            }
+            score = dot * scale;
+        }
+        const float maximum = group_max<wave>(score);
+        float e = 0.0f;
+        if (lane < time)
+        {
+            e = original_exp(score - maximum);
+        }
+        const float sum = tree_sum<wave>(e);
+        weights[lane] = e;
+        asm volatile("" ::: "memory");
+        wait_shared_memory();
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+
+        // 4. Value sums in ascending positions (src/scalar/attention.cpp:41-52).
+        float s[per_lane];
+#pragma unroll
+        for (int i = 0; i < per_lane; ++i)
+        {
+            s[i] = 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < max_books; ++t)
+        {
+            if (t < time)
+            {
+                const float w = weights[t];
+                const uint32_t pw = values[t * (HW / 2) + (per_lane * lane) / 2];
+                if constexpr (per_lane == 2)
+                {
+                    s[0] = __builtin_fmaf(__uint_as_float(pw << 16), w, s[0]);
+                    s[1] = __builtin_fmaf(__uint_as_float(pw & 0xffff0000u), w, s[1]);
+                }
+                else
+                {
+                    const uint32_t v = (lane & 1) ? (pw >> 16) : (pw & 0xffffu);
+                    s[0] = __builtin_fmaf(__uint_as_float(v << 16), w, s[0]);
+                }
             }
         }
-    }
 
-    // 5. The one block merged into the empty state (src/scalar/attention.cpp:86-101).
-    const float block_maximum = uniform(maximum), block_total = uniform(sum);
-    float total, numerator[per_lane];
-    if (is_finite(block_maximum))
-    {
-        // The finite original_exp(-88) scales the zero totals: each result is
-        // the block's value plus +0.
-        total = block_total + 0.0f;
-#pragma unroll
-        for (int i = 0; i < per_lane; ++i)
+        // 5. The one block merged into the empty state (src/scalar/attention.cpp:86-101).
+        const float block_maximum = uniform(maximum), block_total = uniform(sum);
+        float total, numerator[per_lane];
+        if (is_finite(block_maximum))
         {
-            numerator[i] = s[i] + 0.0f;
-        }
-    }
-    else
-    {
-        const float running_maximum = -__builtin_inff();
-        const float factor = original_exp(-__builtin_fabsf(block_maximum - running_maximum));
-        const float old_scale = running_maximum > block_maximum ? 1.0f : factor;
-        const float new_scale = running_maximum > block_maximum ? factor : 1.0f;
-        total = __builtin_fmaf(block_total, new_scale, 0.0f * old_scale);
+            // The finite original_exp(-88) scales the zero totals: each result is
+            // the block's value plus +0.
+            total = block_total + 0.0f;
 #pragma unroll
-        for (int i = 0; i < per_lane; ++i)
-        {
-            numerator[i] = __builtin_fmaf(s[i], new_scale, 0.0f * old_scale);
+            for (int i = 0; i < per_lane; ++i)
+            {
+                numerator[i] = s[i] + 0.0f;
+            }
         }
-    }
-    const float reciprocal = 1.0f / total;
-    if constexpr (per_lane == 2)
-    {
-        *reinterpret_cast<uint32_t*>(row + head * HW + 2 * lane) =
-            float_to_bf16(numerator[0] * reciprocal) | (uint32_t(float_to_bf16(numerator[1] * reciprocal)) << 16);
-    }
-    else
-    {
-        row[head * HW + lane] = float_to_bf16(numerator[0] * reciprocal);
+        else
+        {
+            const float running_maximum = -__builtin_inff();
+            const float factor = original_exp(-__builtin_fabsf(block_maximum - running_maximum));
+            const float old_scale = running_maximum > block_maximum ? 1.0f : factor;
+            const float new_scale = running_maximum > block_maximum ? factor : 1.0f;
+            total = __builtin_fmaf(block_total, new_scale, 0.0f * old_scale);
+#pragma unroll
+            for (int i = 0; i < per_lane; ++i)
+            {
+                numerator[i] = __builtin_fmaf(s[i], new_scale, 0.0f * old_scale);
+            }
+        }
+        const float reciprocal = 1.0f / total;
+        if constexpr (per_lane == 2)
+        {
+            *reinterpret_cast<uint32_t*>(row + head * HW + 2 * lane) =
+                float_to_bf16(numerator[0] * reciprocal) | (uint32_t(float_to_bf16(numerator[1] * reciprocal)) << 16);
+        }
+        else
+        {
+            row[head * HW + lane] = float_to_bf16(numerator[0] * reciprocal);
+        }
     }
 }
 
@@ -853,7 +986,7 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
     // Lanes one at a time whenever the weights fit registers for all of them.
     constexpr bool pipelined = rounds == 1;
     static_assert(I != In::attention || (pipelined && book_attention_fits<V, HW>),
-                  "attention rows: one lane at a time, a wave per head");
+                  "attention rows: one lane at a time, at most two heads per wave");
     // A pipelined tile spreads each input row over its first SW waves
     // (row_ops.hpp), Vw = V / SW values per lane; the other waves only keep
     // the row's barriers.
@@ -950,8 +1083,9 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
         bool residual_requested = false;
         // 2. Inputs, quantised into LDS: a spread row is taken, normalised and
         //    quantised by all waves together; an attention row is computed by
-        //    them (wave h takes head h) and then quantised the same way; other
-        //    inputs take one row per wave (wave m reads lane m).
+        //    them (wave w takes heads w, w + frame_waves, ...) and then
+        //    quantised the same way; other inputs take one row per wave (wave
+        //    m reads lane m).
         if constexpr (I == In::attention)
         {
             constexpr int heads = K / HW;
@@ -959,10 +1093,11 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
             uint16_t* row = reinterpret_cast<uint16_t*>(regions + heads * book_head_floats<HW>);
             if (warp < heads)
             {
+                constexpr int per_wave = (heads + frame_waves - 1) / frame_waves;
                 residual_requested = O == Out::residual_words && column == m0;
-                book_head<HW>(book.qkv, book.book_words, book.time, K, book.scale, m0, warp, x,
-                              regions + warp * book_head_floats<HW>, row,
-                              residual_requested ? p.residual + out_word : nullptr, residual_seen);
+                wave_book_heads<HW, per_wave>(book.qkv, book.book_words, book.time, K, book.scale, m0, warp,
+                                              (heads - warp + frame_waves - 1) / frame_waves, x, regions, row,
+                                              residual_requested ? p.residual + out_word : nullptr, residual_seen);
             }
             lds_barrier();
             if (warp < SW)
@@ -2303,9 +2438,14 @@ template <int VW, int VF, int VL, int HW> constexpr int frame_lds()
 //    sets of workgroups that alternate between consecutive layers, so a
 //    workgroup has two layers' time to finish its last lane and load the next
 //    layer's weights before that layer's first input arrives.
+// When the fused out tiles' extra workgroups do not fit, they are borrowed:
+// the codebook layers' out tiles, attention included, run on the attention
+// group, whose workgroups otherwise wait out the codebook stack (its
+// attention being fused); the out group keeps the temporal out tiles.
 struct FrameLayout
 {
     bool fused = false, paired = false;
+    bool borrowed = false; // fused codebook out tiles on the attention group
     bool split = false; // temporal queries in halves over two workgroups each
     // Down projections in tiles of narrow_rows output rows: their 64-row tiles
     // would hold more weight blocks than the waves can keep in registers, and a
@@ -2319,7 +2459,8 @@ struct FrameLayout
 
 __host__ __device__ inline FrameLayout frame_layout(int width, int heads, int ffn, int alphabet, int lanes, int workers)
 {
-    const bool fusable = heads <= frame_waves; // a wave per head (book_attention_fits)
+    // At most two heads per wave (book_attention_fits).
+    const bool fusable = heads <= max_book_heads_per_wave * frame_waves;
     const int w = width / tile_rows, f = ffn / tile_rows;
     FrameLayout l;
     l.narrow_down = ffn / 256 > frame_waves;
@@ -2340,8 +2481,12 @@ __host__ __device__ inline FrameLayout frame_layout(int width, int heads, int ff
     {
         l.paired = true;
     }
-    l.out_tiles = l.fused ? lanes * w : w;
-    l.workgroups = base + (l.fused ? fused_extra : 0) + (l.paired ? paired_extra : 0);
+    if (fusable && !l.fused)
+    {
+        l.fused = l.borrowed = true;
+    }
+    l.out_tiles = l.fused && !l.borrowed ? lanes * w : w;
+    l.workgroups = base + (l.fused && !l.borrowed ? fused_extra : 0) + (l.paired ? paired_extra : 0);
     if (l.workgroups + lanes * heads <= workers)
     {
         l.split = true;
@@ -2486,7 +2631,24 @@ __global__ __launch_bounds__(frame_threads) void frame_kernel(const FrameArgs a)
                 attend_item<HW>(attention, time, t % items, half, x, lds);
             }
         }
-        if (member(Kind::out))
+        if (fused && layout.borrowed)
+        {
+            // Tile t % width_tiles of lane t / width_tiles, on the attention group.
+            if constexpr (book_attention_fits<VW, HW>)
+            {
+                if (member(Kind::attend))
+                {
+                    const auto p = projection(q + 1);
+                    const auto book = constant<BookAttention>(jobs + T.book_offset(att - TL));
+                    for (int t = first_tile(Kind::attend); t < M * width_tiles; t += group_size[Kind::attend])
+                    {
+                        project_tile<VW, In::attention, Out::residual_words, HW>(p, 0, M, t % width_tiles, x, a.error,
+                                                                                 lds, book, t / width_tiles);
+                    }
+                }
+            }
+        }
+        else if (member(Kind::out))
         {
             const auto p = projection(q + 1);
             if (!fused)
