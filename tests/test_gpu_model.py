@@ -210,6 +210,21 @@ def test_wide_geometry(native, oracle, wide_model, frames, batch):
     assert np.array_equal(encode, expected)
 
 
+def test_wide_geometry_long_context(native, wide_model):
+    """Contexts past 512 frames at width 1024: every wave of a temporal query
+    then takes a second block of keys, requested into LDS at the job's start;
+    1030 frames also cross the 1024-frame rollover. The decode pass (frame
+    steps) equals the encode pass (batched known tokens) bit for bit, and the
+    stream decodes back to its tokens."""
+    _, hip_model = wide_model
+    h = native.header(1030, 1, 1, 12)
+    tokens = random_tokens(1030, 1, 12, seed=11)
+    encode, decode = _both_passes(native, hip_model, h, tokens)
+    assert np.array_equal(encode, decode)
+    session = hip_model.session()
+    assert np.array_equal(session.decode(session.encode(h, tokens)), tokens)
+
+
 def test_run_to_run_determinism(native, small):
     _, hip_model = small
     h = native.header(40, 3, 1, 12)

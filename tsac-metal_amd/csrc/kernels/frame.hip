@@ -1362,11 +1362,88 @@ struct Attend
     word* records = nullptr;
 };
 
-template <int HW> constexpr int attend_lds()
+// This lane's value columns of the 64 rows of a block: with two columns per
+// lane a word per row; with one, two rows per word (row 2i in the low half,
+// row 2i + 1 in the high half, loaded there directly), which halves the
+// registers. get(tt) returns the row's word with column c in bits 16c..16c+15.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+template <int per_lane> struct BlockValues;
+template <> struct BlockValues<2>
+{
+    uint32_t word[64];
+    __device__ __forceinline__ void set(int tt, uint32_t w)
+    {
+        word[tt] = w;
+    }
+    __device__ __forceinline__ uint32_t get(int tt) const
+    {
+        return word[tt];
+    }
+};
+template <> struct BlockValues<1>
+{
+    u16x2 half[32];
+    __device__ __forceinline__ void set(int tt, uint32_t w)
+    {
+        half[tt / 2][tt % 2] = uint16_t(w);
+    }
+    __device__ __forceinline__ uint32_t get(int tt) const
+    {
+        const uint32_t pair = __builtin_bit_cast(uint32_t, half[tt / 2]);
+        return tt % 2 == 0 ? pair & 0xffffu : pair >> 16;
+    }
+};
+
+// A temporal query of more than frame_waves blocks on one workgroup gives
+// each wave a second block. With 64-wide heads the cached key and value rows
+// of those blocks (16 KiB each) are requested into LDS at the job's start,
+// as whole-row 16-byte loads, beside the job's other LDS.
+template <int HW> constexpr bool stage_second_blocks = HW == 64;
+template <int HW> constexpr int second_block_bytes = 2 * 64 * HW * 2; // key rows, then value rows
+
+template <int HW> constexpr int attend_base_lds()
 {
     // partial records, the fp32 query, staged exchanged rows (key words then
     // value words), codebook keys in fp32, each wave's block weights
     return (max_blocks * (2 + HW) + HW + max_books * HW + max_books * staged_key_stride<HW> + frame_waves * 64) * 4;
+}
+template <int HW> constexpr int attend_lds()
+{
+    static_assert(attend_base_lds<HW>() % 16 == 0, "second blocks 16-byte aligned");
+    return attend_base_lds<HW>() + (stage_second_blocks<HW> ? frame_waves * second_block_bytes<HW> : 0);
+}
+
+// Position (16-byte slot) of chunk c of row r of a block staged by
+// stage_block: rows in groups of 64 / chunks_per_row per 1 KiB request, the
+// chunks of row r rotated by r, so that lanes reading "their" row at the same
+// chunk fall on distinct banks.
+template <int HW> __device__ __forceinline__ int staged_slot(int r, int c)
+{
+    constexpr int chunks = HW * 2 / 16, rows = 64 / chunks;
+    return 64 * (r / rows) + chunks * (r % rows) + (c + r) % chunks;
+}
+
+// Requests the cached rows [start, start + count) (count <= 64, each of HW
+// BF16 values) of `rows` into `to` (LDS) in staged_slot order, one 16-byte
+// chunk per lane and 1 KiB per request: lanes 8 g .. 8 g + 7 of request j
+// read row (64 / chunks) j + g whole. The data lands when the wave's vector
+// memory counter says so.
+template <int HW>
+__device__ __forceinline__ void stage_block(const uint16_t* rows, std::size_t stride, int start, int count,
+                                            uint8_t* to, int lane)
+{
+    constexpr int chunks = HW * 2 / 16, per_request = 64 / chunks, requests = 64 / per_request;
+#pragma unroll
+    for (int j = 0; j < requests; ++j)
+    {
+        const int r = j * per_request + lane / chunks, slot = lane % chunks;
+        const int c = ((slot - r) % chunks + chunks) % chunks;
+        if (r < count)
+        {
+            __builtin_amdgcn_global_load_lds(global(rows + std::size_t(start + r) * stride + c * 8),
+                                             (__attribute__((address_space(3))) void*)(to + j * 1024), 16, 0, 0);
+        }
+    }
 }
 
 // One (lane, head) query over all its keys (decode.hip attention_step_kernel).
@@ -1434,12 +1511,13 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
     const uint16_t* v = temporal ? a.values + std::size_t(m) * a.lane_stride + head * HW : nullptr;
 
     // Key words and value words of one 64-key block: lane l holds key row
-    // block*64 + l, value[tt] this lane's value columns of row block*64 + tt.
+    // block*64 + l, and this lane's value columns of row block*64 + tt
+    // (BlockValues).
     // Temporal attention reads every row but the last (time - 1) from the
     // cache; book attention reads all its rows (time <= max_books) from the
     // exchange.
     uint32_t key[HW / 2];
-    uint32_t value[64];
+    BlockValues<per_lane> value;
     // Cache rows need nothing from this step: requested before any wait.
     const auto load_cached = [&](int block)
     {
@@ -1459,14 +1537,30 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
                 key[4 * c + 3] = u.w;
             }
         }
-#pragma unroll
-        for (int tt = 0; tt < 64; ++tt)
+        if constexpr (per_lane == 2)
         {
-            const int row = start + tt;
-            if (tt < count && row < cached)
+#pragma unroll
+            for (int tt = 0; tt < 64; ++tt)
             {
-                const uint16_t* src = v + std::size_t(row) * width + per_lane * lane;
-                value[tt] = per_lane == 2 ? *global(reinterpret_cast<const uint32_t*>(src)) : uint32_t(*global(src));
+                const int row = start + tt;
+                if (tt < count && row < cached)
+                {
+                    value.word[tt] = *global(reinterpret_cast<const uint32_t*>(v + std::size_t(row) * width + 2 * lane));
+                }
+            }
+        }
+        else
+        {
+            // Every row is requested, rows past the cached ones as the last
+            // cached row (or row 0), whose values are never used: a request
+            // under a per-row branch would be waited for before the next one,
+            // as each row's value joins another in a register.
+            const int last = cached > 0 ? cached - 1 : 0;
+#pragma unroll
+            for (int tt = 0; tt < 64; ++tt)
+            {
+                const int row = start + tt < cached ? start + tt : last;
+                value.half[tt / 2][tt % 2] = *global(v + std::size_t(row) * width + lane);
             }
         }
     };
@@ -1480,6 +1574,17 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
     //    of codebook rows are stored as fp32 (exact: BF16 is the top half of
     //    an fp32), so the score chains read operands without unpacking them.
     lds_barrier(); // the previous job's readers of LDS are done
+    // The wave's second block, when it has one, is requested into LDS now.
+    const int second_block = first_block + warp + frame_waves;
+    const bool second_staged = stage_second_blocks<HW> && temporal && half < 0 && second_block < end_block;
+    uint8_t* const second = lds + attend_base_lds<HW>() + warp * second_block_bytes<HW>;
+    if (second_staged)
+    {
+        const int start = second_block * 64;
+        const int count = min(time - start, 64), from_cache = min(cached - start, count);
+        stage_block<HW>(k, width, start, from_cache, second, lane);
+        stage_block<HW>(v, width, start, from_cache, second + second_block_bytes<HW> / 2, lane);
+    }
     {
         constexpr int per_thread = (HW / 2 + max_books * row_words + frame_threads - 1) / frame_threads;
         const int total = HW / 2 + exchanged * row_words;
@@ -1545,7 +1650,7 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
         {
             if (tt < time)
             {
-                value[tt] = staged_value(tt);
+                value.set(tt, staged_value(tt));
             }
         }
     }
@@ -1555,7 +1660,44 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
     float kept[2 + per_lane]; // the last block's maximum, total and value sums
     for (int block = first_block + warp; block < end_block; block += frame_waves)
     {
-        if (block != first_block + warp)
+        if (block == second_block && second_staged)
+        {
+            // The cached rows requested at the start (staged_slot order).
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            const int start = block * 64;
+            const int count = time - start < 64 ? time - start : 64;
+            const int t = start + lane;
+            if (lane < count && t < cached)
+            {
+#pragma unroll
+                for (int c = 0; c < HW / 8; ++c)
+                {
+                    const uint4 u = *reinterpret_cast<const uint4*>(second + 16 * staged_slot<HW>(lane, c));
+                    key[4 * c] = u.x;
+                    key[4 * c + 1] = u.y;
+                    key[4 * c + 2] = u.z;
+                    key[4 * c + 3] = u.w;
+                }
+            }
+            // Every row's slot is read (those past the requested rows hold
+            // values that are never used).
+            const uint8_t* values_in = second + second_block_bytes<HW> / 2;
+            const int byte = 2 * per_lane * lane; // this lane's columns within a row
+#pragma unroll
+            for (int tt = 0; tt < 64; ++tt)
+            {
+                const uint8_t* at = values_in + 16 * staged_slot<HW>(tt, byte / 16) + byte % 16;
+                if constexpr (per_lane == 2)
+                {
+                    value.word[tt] = *reinterpret_cast<const uint32_t*>(at);
+                }
+                else
+                {
+                    value.half[tt / 2][tt % 2] = *reinterpret_cast<const uint16_t*>(at);
+                }
+            }
+        }
+        else if (block != first_block + warp)
         {
             load_cached(block);
         }
@@ -1688,7 +1830,7 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                 {
-                    accumulate(value[4 * t4 + i], w[i]);
+                    accumulate(value.get(4 * t4 + i), w[i]);
                 }
             }
             else if (4 * t4 < from_values)
@@ -1698,7 +1840,7 @@ __device__ __noinline__ JOB void attend_item(constant_ptr<Attend> job, int keys,
                 {
                     if (4 * t4 + i < from_values)
                     {
-                        accumulate(value[4 * t4 + i], w[i]);
+                        accumulate(value.get(4 * t4 + i), w[i]);
                     }
                 }
             }
