@@ -1081,6 +1081,7 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
     {
         word residual_seen = 0;
         bool residual_requested = false;
+        uint16_t prefix_row[I == In::embed_accumulate ? V : 1]; // tile 0's accumulated embedding row
         // 2. Inputs, quantised into LDS: a spread row is taken, normalised and
         //    quantised by all waves together; an attention row is computed by
         //    them (wave w takes heads w, w + frame_waves, ...) and then
@@ -1206,7 +1207,11 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
                 }
                 if (tile == 0)
                 {
-                    give_row<V>(p.prefix_out, first, x, v);
+#pragma unroll
+                    for (int i = 0; i < V; ++i)
+                    {
+                        prefix_row[i] = v[i];
+                    }
                 }
             }
             bf8l_lane<V>(v, lane, q + warp * K, scales + warp * blocks, error);
@@ -1264,62 +1269,73 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
         lds_barrier();
 
         // 4. Ordered chain per (row pair, column), then the output.
-        if (column < m0 || column >= m1)
+        if (column >= m0 && column < m1)
         {
-            return;
-        }
-        const int m = column;
-        float sum0 = 0.0f, sum1 = 0.0f;
+            const int m = column;
+            float sum0 = 0.0f, sum1 = 0.0f;
 #pragma unroll
-        for (int b = 0; b < blocks; ++b)
-        {
-            int d0 = 0, d1 = 0;
+            for (int b = 0; b < blocks; ++b)
+            {
+                int d0 = 0, d1 = 0;
 #pragma unroll
-            for (int s = 0; s < waves_per_block; ++s)
-            {
-                const int* d = dots + ((b * waves_per_block + s) * max_lanes + m) * R + 2 * pair;
-                d0 += d[0];
-                d1 += d[1];
+                for (int s = 0; s < waves_per_block; ++s)
+                {
+                    const int* d = dots + ((b * waves_per_block + s) * max_lanes + m) * R + 2 * pair;
+                    d0 += d[0];
+                    d1 += d[1];
+                }
+                const float as = scales[m * blocks + b];
+                const float scale0 = ws0[b] * as;
+                const float scale1 = ws1[b] * as;
+                sum0 = __builtin_fmaf(float(d0), scale0, sum0);
+                sum1 = __builtin_fmaf(float(d1), scale1, sum1);
             }
-            const float as = scales[m * blocks + b];
-            const float scale0 = ws0[b] * as;
-            const float scale1 = ws1[b] * as;
-            sum0 = __builtin_fmaf(float(d0), scale0, sum0);
-            sum1 = __builtin_fmaf(float(d1), scale1, sum1);
-        }
-        uint16_t y0 = float_to_bf16(sum0 + bias0);
-        uint16_t y1 = float_to_bf16(sum1 + bias1);
-        if constexpr (O == Out::residual_words)
-        {
-            const uint32_t r = settle(p.residual, out_word, residual_seen, x);
-            y0 = float_to_bf16(bf16_to_float(uint16_t(r & 0xffff)) + bf16_to_float(y0));
-            y1 = float_to_bf16(bf16_to_float(uint16_t(r >> 16)) + bf16_to_float(y1));
-        }
-        else if constexpr (O == Out::residual_row)
-        {
-            y0 = float_to_bf16(bf16_to_float(uint16_t(fixed_residual & 0xffff)) + bf16_to_float(y0));
-            y1 = float_to_bf16(bf16_to_float(uint16_t(fixed_residual >> 16)) + bf16_to_float(y1));
-        }
-        else if constexpr (O == Out::gelu)
-        {
-            y0 = gelu_bf16(y0);
-            y1 = gelu_bf16(y1);
-        }
-        else if constexpr (O == Out::qkv)
-        {
-            const int width = p.width;
-            if (n0 < 2 * width && p.rotations)
+            uint16_t y0 = float_to_bf16(sum0 + bias0);
+            uint16_t y1 = float_to_bf16(sum1 + bias1);
+            if constexpr (O == Out::residual_words)
             {
-                // rotate() of step_ops.hpp on the prefetched coefficients.
-                const float cosine = bf16_to_float(uint16_t(rotation & 0xffff)), sine = bf16_to_float(uint16_t(rotation >> 16));
-                const float re = bf16_to_float(y0), im = bf16_to_float(y1);
-                const float im_sine = im * sine;
-                const float re_sine = re * sine;
-                y0 = float_to_bf16(__builtin_fmaf(re, cosine, -im_sine));
-                y1 = float_to_bf16(__builtin_fmaf(im, cosine, re_sine));
+                const uint32_t r = settle(p.residual, out_word, residual_seen, x);
+                y0 = float_to_bf16(bf16_to_float(uint16_t(r & 0xffff)) + bf16_to_float(y0));
+                y1 = float_to_bf16(bf16_to_float(uint16_t(r >> 16)) + bf16_to_float(y1));
+            }
+            else if constexpr (O == Out::residual_row)
+            {
+                y0 = float_to_bf16(bf16_to_float(uint16_t(fixed_residual & 0xffff)) + bf16_to_float(y0));
+                y1 = float_to_bf16(bf16_to_float(uint16_t(fixed_residual >> 16)) + bf16_to_float(y1));
+            }
+            else if constexpr (O == Out::gelu)
+            {
+                y0 = gelu_bf16(y0);
+                y1 = gelu_bf16(y1);
+            }
+            else if constexpr (O == Out::qkv)
+            {
+                const int width = p.width;
+                if (n0 < 2 * width && p.rotations)
+                {
+                    // rotate() of step_ops.hpp on the prefetched coefficients.
+                    const float cosine = bf16_to_float(uint16_t(rotation & 0xffff)), sine = bf16_to_float(uint16_t(rotation >> 16));
+                    const float re = bf16_to_float(y0), im = bf16_to_float(y1);
+                    const float im_sine = im * sine;
+                    const float re_sine = re * sine;
+                    y0 = float_to_bf16(__builtin_fmaf(re, cosine, -im_sine));
+                    y1 = float_to_bf16(__builtin_fmaf(im, cosine, re_sine));
+                }
+            }
+            publish(p.y, out_word, y0 | (uint32_t(y1) << 16), x.epoch);
+        }
+        // The accumulated embedding row for the next book's prefix job goes
+        // out only now: published before the dots, its stores would hold up
+        // this tile's output (a later wait for any load also waits for the
+        // stores issued before it), and the next prefix job reads it a whole
+        // book later.
+        if constexpr (I == In::embed_accumulate)
+        {
+            if (tile == 0 && warp >= m0 && warp < m1)
+            {
+                give_row<V>(p.prefix_out, std::size_t(warp) * K + lane * V, x, prefix_row);
             }
         }
-        publish(p.y, out_word, y0 | (uint32_t(y1) << 16), x.epoch);
     };
     if constexpr (pipelined)
     {
