@@ -1272,6 +1272,23 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
         if (column >= m0 && column < m1)
         {
             const int m = column;
+            // Every partial dot and scale is requested before the first is
+            // used: one LDS round trip for the chain instead of one per few
+            // blocks.
+            int2 part[blocks][waves_per_block];
+            float as[blocks];
+#pragma unroll
+            for (int b = 0; b < blocks; ++b)
+            {
+#pragma unroll
+                for (int s = 0; s < waves_per_block; ++s)
+                {
+                    part[b][s] = *reinterpret_cast<const int2*>(dots + ((b * waves_per_block + s) * max_lanes + m) * R +
+                                                                2 * pair);
+                }
+                as[b] = scales[m * blocks + b];
+            }
+            __builtin_amdgcn_sched_barrier(0);
             float sum0 = 0.0f, sum1 = 0.0f;
 #pragma unroll
             for (int b = 0; b < blocks; ++b)
@@ -1280,13 +1297,11 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
 #pragma unroll
                 for (int s = 0; s < waves_per_block; ++s)
                 {
-                    const int* d = dots + ((b * waves_per_block + s) * max_lanes + m) * R + 2 * pair;
-                    d0 += d[0];
-                    d1 += d[1];
+                    d0 += part[b][s].x;
+                    d1 += part[b][s].y;
                 }
-                const float as = scales[m * blocks + b];
-                const float scale0 = ws0[b] * as;
-                const float scale1 = ws1[b] * as;
+                const float scale0 = ws0[b] * as[b];
+                const float scale1 = ws1[b] * as[b];
                 sum0 = __builtin_fmaf(float(d0), scale0, sum0);
                 sum1 = __builtin_fmaf(float(d1), scale1, sum1);
             }
