@@ -766,17 +766,26 @@ __device__ __forceinline__ void wave_book_heads(const word* qkv, std::size_t boo
             wait_shared_memory();
             __builtin_amdgcn_wave_barrier();
             asm volatile("" ::: "memory");
+            // Every key's weight and value word is requested before the first
+            // is used (rows past `time` hold stale words, and their steps are
+            // dropped by selects, not branches), so the sums take one LDS
+            // round trip rather than one per key.
+            float wt[max_books];
+            uint32_t pv[max_books];
+#pragma unroll
+            for (int t = 0; t < max_books; ++t)
+            {
+                wt[t] = weights[t];
+                pv[t] = values[t * (HW / 2) + j];
+            }
             float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
             for (int t = 0; t < max_books; ++t)
             {
-                if (t < time)
-                {
-                    const float w = weights[t];
-                    const uint32_t pw = values[t * (HW / 2) + j];
-                    s0 = __builtin_fmaf(__uint_as_float(pw << 16), w, s0);
-                    s1 = __builtin_fmaf(__uint_as_float(pw & 0xffff0000u), w, s1);
-                }
+                const float a0 = __builtin_fmaf(__uint_as_float(pv[t] << 16), wt[t], s0);
+                const float a1 = __builtin_fmaf(__uint_as_float(pv[t] & 0xffff0000u), wt[t], s1);
+                s0 = t < time ? a0 : s0;
+                s1 = t < time ? a1 : s1;
             }
             // The one block merged into the empty state (src/scalar/attention.cpp:86-101).
             float total, n0, n1;
@@ -865,23 +874,33 @@ __device__ __forceinline__ void wave_book_heads(const word* qkv, std::size_t boo
         {
             s[i] = 0.0f;
         }
+        // Every key's weight and value word requested before the first is
+        // used; steps past `time` are dropped by selects.
+        float wt[max_books];
+        uint32_t pv[max_books];
 #pragma unroll
         for (int t = 0; t < max_books; ++t)
         {
-            if (t < time)
+            wt[t] = weights[t];
+            pv[t] = values[t * (HW / 2) + (per_lane * lane) / 2];
+        }
+#pragma unroll
+        for (int t = 0; t < max_books; ++t)
+        {
+            const float w = wt[t];
+            const uint32_t pw = pv[t];
+            if constexpr (per_lane == 2)
             {
-                const float w = weights[t];
-                const uint32_t pw = values[t * (HW / 2) + (per_lane * lane) / 2];
-                if constexpr (per_lane == 2)
-                {
-                    s[0] = __builtin_fmaf(__uint_as_float(pw << 16), w, s[0]);
-                    s[1] = __builtin_fmaf(__uint_as_float(pw & 0xffff0000u), w, s[1]);
-                }
-                else
-                {
-                    const uint32_t v = (lane & 1) ? (pw >> 16) : (pw & 0xffffu);
-                    s[0] = __builtin_fmaf(__uint_as_float(v << 16), w, s[0]);
-                }
+                const float a0 = __builtin_fmaf(__uint_as_float(pw << 16), w, s[0]);
+                const float a1 = __builtin_fmaf(__uint_as_float(pw & 0xffff0000u), w, s[1]);
+                s[0] = t < time ? a0 : s[0];
+                s[1] = t < time ? a1 : s[1];
+            }
+            else
+            {
+                const uint32_t v = (lane & 1) ? (pw >> 16) : (pw & 0xffffu);
+                const float a0 = __builtin_fmaf(__uint_as_float(v << 16), w, s[0]);
+                s[0] = t < time ? a0 : s[0];
             }
         }
 
