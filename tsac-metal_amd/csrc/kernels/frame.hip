@@ -1182,31 +1182,65 @@ __device__ __noinline__ JOB void project_tile(constant_ptr<Projection> job, int 
                 // step (written before the launch), else from that step's
                 // token words.
                 const uint16_t* t = p.tokens + std::size_t(warp) * p.token_stride;
-                // Lane b polls book b's token word (all books' at once).
+                // Lane b holds book b's token: polled from its token word (all
+                // books' at once), or read from `tokens`.
                 uint32_t previous = 0;
-                if (previous_epoch != 0)
                 {
                     const int b = lane < p.books ? lane : p.books - 1;
-                    previous = take(p.token_words + std::size_t(b) * p.token_book_words, warp,
-                                    Exchange{previous_epoch, x.abort});
+                    if (previous_epoch != 0)
+                    {
+                        previous = take(p.token_words + std::size_t(b) * p.token_book_words, warp,
+                                        Exchange{previous_epoch, x.abort});
+                    }
+                    else
+                    {
+                        previous = *global(t + b);
+                    }
                 }
                 const auto token_of = [&](int b)
-                {
-                    const int token = previous_epoch != 0 ? int(__builtin_amdgcn_readlane(previous, b) & 0xffff)
-                                                          : int(*global(t + b));
-                    return min(token, p.alphabet - 1);
-                };
+                { return min(int(__builtin_amdgcn_readlane(previous, b) & 0xffff), p.alphabet - 1); };
                 const int t0 = token_of(0);
                 load_global_row<V>(p.embeddings + std::size_t(t0) * K + lane * V, v);
-                for (int b = 1; b < p.books; ++b)
+                // Book b's row is requested `ahead` books before it is added,
+                // so the sum waits for about one row's latency rather than one
+                // per book. Every request is made (past the last book it
+                // repeats the last book's row, never added), so the requests
+                // outstanding at each add do not depend on the book count.
+                constexpr int ahead = 4, chunks = V / 4;
+                static_assert(V % 4 == 0, "rows in 8-byte chunks");
+                unsigned long long raw[ahead][chunks];
+                const auto request = [&](int b, unsigned long long (&row)[chunks])
                 {
-                    const int tb = token_of(b);
-                    uint16_t e[V];
-                    load_global_row<V>(p.embeddings + (std::size_t(b) * p.alphabet + tb) * K + lane * V, e);
+                    const int book = b < p.books ? b : p.books - 1;
+                    const auto* src = reinterpret_cast<const unsigned long long*>(
+                        p.embeddings + (std::size_t(book) * p.alphabet + token_of(book)) * K + lane * V);
 #pragma unroll
-                    for (int i = 0; i < V; ++i)
+                    for (int c = 0; c < chunks; ++c)
                     {
-                        v[i] = float_to_bf16(bf16_to_float(v[i]) + bf16_to_float(e[i]));
+                        row[c] = *global(src + c);
+                    }
+                };
+#pragma unroll
+                for (int i = 0; i < ahead; ++i)
+                {
+                    request(1 + i, raw[i]);
+                }
+                // Groups of `ahead` books, slot k holding book b0 + k.
+                for (int b0 = 1; b0 < p.books; b0 += ahead)
+                {
+#pragma unroll
+                    for (int k = 0; k < ahead; ++k)
+                    {
+                        if (b0 + k < p.books)
+                        {
+#pragma unroll
+                            for (int i = 0; i < V; ++i)
+                            {
+                                const uint16_t e = uint16_t(raw[k][i / 4] >> (16 * (i % 4)));
+                                v[i] = float_to_bf16(bf16_to_float(v[i]) + bf16_to_float(e));
+                            }
+                        }
+                        request(b0 + k + ahead, raw[k]);
                     }
                 }
             }
