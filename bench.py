@@ -299,7 +299,11 @@ def qlinear_table(torch, native, rotate_bytes=1 << 30):
                 seconds = start.elapsed_time(stop) / 1000 / reps
                 how = "plain launches over 4 rotating weight copies"
             traffic = K * n + 20 * n + m * K + 16 * m + 2 * m * n
-            table.append({"N": n, "M": m, "path": "gemv" if m <= 8 else "small-M MFMA" if m <= 64 else "gemm",
+            # The automatic path's choice: the small-M kernel also takes M <= 1024
+            # when the GEMM's 128 x 128 tiles would fill at most a quarter of the CUs.
+            units = torch.cuda.get_device_properties(0).multi_processor_count
+            small = m <= 64 or (m <= 1024 and -(-m // 128) * -(-n // 128) * 4 <= units)
+            table.append({"N": n, "M": m, "path": "gemv" if m <= 8 else "small-M MFMA" if small else "gemm",
                           "us": round(seconds * 1e6, 2),
                           "GB/s": round(traffic / seconds / 1e9, 1),
                           "frac_hbm": round(traffic / seconds / 1e9 / HBM_PEAK_GBPS, 4),

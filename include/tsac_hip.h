@@ -398,9 +398,10 @@ int tsac_hip_linear_create(const tsac_hip_linear* weights, size_t K, size_t N,
 void tsac_hip_linear_destroy(tsac_hip_device_linear* linear);
 
 /* path: 0 automatic (GEMV for M <= 8, the small-M MFMA GEMM for M <= 64 when
- * K <= 2048, else the MFMA GEMM), 1 GEMV, 2 GEMM, 4 small-M MFMA GEMM (row-major
- * activations, M <= 64, K <= 2048); the GEMM needs y and residual 16-byte
- * aligned.
+ * K <= 2048, and for M <= 1024 when the GEMM's 128 x 128 tiles would occupy at
+ * most a quarter of the compute units, else the MFMA GEMM), 1 GEMV, 2 GEMM,
+ * 4 small-M MFMA GEMM (row-major activations, M <= 1024, K <= 2048); the GEMM
+ * needs y and residual 16-byte aligned.
  * 3 = GEMM on activations in MFMA operand tiles (tsac_hip_bf8l_tiles);
  * accepted by tsac_hip_linear_apply_quantized only. */
 #define TSAC_HIP_PATH_AUTO 0

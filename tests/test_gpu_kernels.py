@@ -61,7 +61,7 @@ def test_qlinear_config_shapes_match_oracle(torch, native, oracle, n, m):
     linear = native.DeviceLinear(values, scales, bias)
     dx = dev(torch, x)
     outputs = {}
-    paths = [native.PATH_GEMM] + ([native.PATH_GEMV] if m <= 8 else []) + ([native.PATH_SMALL] if m <= 64 else [])
+    paths = [native.PATH_GEMM] + ([native.PATH_GEMV] if m <= 8 else []) + ([native.PATH_SMALL] if m <= 1024 else [])
     for path in paths:
         y = empty(torch, (m, n), torch.int16)
         linear.apply(dx, y, path)
@@ -72,7 +72,7 @@ def test_qlinear_config_shapes_match_oracle(torch, native, oracle, n, m):
             linear.apply(dx[r:r + 8], y[r:r + 8], native.PATH_GEMV)
         outputs[native.PATH_GEMV] = host(y)
     assert np.array_equal(outputs[native.PATH_GEMM], outputs[native.PATH_GEMV])
-    if m <= 64:
+    if m <= 1024:
         assert np.array_equal(outputs[native.PATH_GEMM], outputs[native.PATH_SMALL])
     rows = np.arange(m) if m <= 64 else np.unique(np.r_[0, 1, 127, 128, m - 1, rng.integers(0, m, 40)])
     expected = oracle.qlinear(values, scales, bias, x[rows])
@@ -131,7 +131,9 @@ def test_qlinear_rejects_nonfinite(torch, native):
 def test_qlinear_fused_residual(torch, native, oracle):
     rng = np.random.default_rng(3)
     values, scales, bias = random_linear(rng, 2048, 512)
-    for m, path in ((3, native.PATH_AUTO), (77, native.PATH_AUTO), (40, native.PATH_SMALL), (64, native.PATH_AUTO)):
+    # 77 and 300 rows at N = 512 take the small-M kernel automatically (few GEMM tiles).
+    for m, path in ((3, native.PATH_AUTO), (77, native.PATH_AUTO), (40, native.PATH_SMALL), (64, native.PATH_AUTO),
+                    (300, native.PATH_AUTO), (300, native.PATH_GEMM)):
         x = _activations(rng, m, 2048)
         skip = bf16_bits(((np.arange(m * 512) % 31) - 15).astype(np.float32) / 32).reshape(m, 512)
         q = empty(torch, (m, 2048), torch.int8)

@@ -847,7 +847,8 @@ int tsac_hip_linear_apply(const tsac_hip_device_linear* linear, const uint16_t* 
             const LinearPath chosen = path_of(path);
             // The GEMM reads MFMA operand tiles; the GEMV and the small-M GEMM read rows.
             const bool tiles = chosen == LinearPath::gemm ||
-                               (chosen == LinearPath::automatic && M > small_gemm_max_rows());
+                               (chosen == LinearPath::automatic && M > small_gemm_max_rows() &&
+                                !small_gemm_chosen(M, linear->linear.N, K));
             const Layout layout = tiles ? Layout::tiles : Layout::rows;
             const std::size_t rows = tiles ? tile_padded_rows(M) : M;
             AsyncScratch scratch(rows * K + rows * (K / 256) * 4 + 256 + 8, s);

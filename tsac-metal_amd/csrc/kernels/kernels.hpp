@@ -102,6 +102,10 @@ std::size_t gemv_max_rows();
 // gemv_max_rows(), then the small-M MFMA GEMM where K <= 2048); above it the
 // GEMM reads MFMA operand tiles.
 std::size_t small_gemm_max_rows();
+// Whether the automatic path gives M row-major rows of an N x K projection to
+// the small-M MFMA GEMM (always for 8 < M <= small_gemm_max_rows() when
+// K <= 2048; up to 1024 rows when the GEMM would leave most units idle).
+bool small_gemm_chosen(std::size_t M, std::size_t N, std::size_t K);
 
 // x [M][K] BF16 -> y [M][N] like quantize_rows + linear, with the BF8L buffer in
 // a fixed per-device array (static_linear.hip) instead of caller or allocator

@@ -166,7 +166,8 @@ void launch_gemv(const DeviceLinear& w, const int8_t* q, const float* scales, st
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int small_max_rows = 64;
+constexpr int small_max_rows = 64;      // rows the automatic path always gives this kernel
+constexpr int small_launch_max_rows = 1024; // rows one launch accepts
 constexpr int small_max_blocks = 8;
 constexpr int small_columns = 32;
 constexpr int small_rows = 32;        // rows of a workgroup
@@ -251,8 +252,8 @@ __global__ __launch_bounds__(small_max_blocks * wave) void small_gemm_kernel(
 void launch_small_gemm(const DeviceLinear& w, const int8_t* q, const float* scales, std::size_t M, uint16_t* y,
                        const uint16_t* residual, hipStream_t stream)
 {
-    require(M >= 1 && M <= std::size_t(small_max_rows) && w.K <= std::size_t(small_max_blocks) * 256,
-            "small-M GEMM: at most 64 rows and K <= 2048");
+    require(M >= 1 && M <= std::size_t(small_launch_max_rows) && w.K <= std::size_t(small_max_blocks) * 256,
+            "small-M GEMM: at most 1024 rows and K <= 2048");
     const dim3 grid(unsigned(w.N / small_columns), unsigned((M + small_rows - 1) / small_rows));
     const unsigned threads = unsigned(w.K / 256) * wave;
     small_gemm_kernel<<<grid, threads, 0, stream>>>(w.values, w.scales, w.bias, int(w.N), int(w.K), q, scales,
@@ -764,6 +765,22 @@ std::size_t small_gemm_max_rows()
     return small_max_rows;
 }
 
+bool small_gemm_chosen(std::size_t M, std::size_t N, std::size_t K)
+{
+    // Up to 64 rows always. Up to 1024 rows too when the GEMM's 128 x 128
+    // tiles would occupy at most a quarter of the compute units: the small-M
+    // kernel's 32 x 32 workgroups then fill the chip instead (K = 1024,
+    // N = 1024, M = 1024: 8.9 us against 12.5 us for 64 GEMM tiles; at 256
+    // tiles, M = 4096 or N = 4096, the GEMM is twice as fast).
+    if (M <= gemv_max_columns || K > std::size_t(small_max_blocks) * 256)
+    {
+        return false;
+    }
+    const std::size_t gemm_tiles = (M + gemm::tile_m - 1) / gemm::tile_m * ((N + gemm::tile_n - 1) / gemm::tile_n);
+    return M <= std::size_t(small_max_rows) ||
+           (M <= std::size_t(small_launch_max_rows) && gemm_tiles * 4 <= std::size_t(compute_units()));
+}
+
 std::size_t gemv_max_rows()
 {
     return gemv_max_columns;
@@ -799,11 +816,10 @@ void linear(const DeviceLinear& w, const int8_t* q, const float* scales, std::si
     }
     if (path == LinearPath::automatic)
     {
-        path = layout != Layout::rows                          ? LinearPath::gemm
-               : M <= gemv_max_columns                         ? LinearPath::gemv
-               : M <= std::size_t(small_max_rows) && w.K <= std::size_t(small_max_blocks) * 256
-                   ? LinearPath::small
-                   : LinearPath::gemm;
+        path = layout != Layout::rows           ? LinearPath::gemm
+               : M <= gemv_max_columns          ? LinearPath::gemv
+               : small_gemm_chosen(M, w.N, w.K) ? LinearPath::small
+                                                : LinearPath::gemm;
     }
     if (path == LinearPath::gemv)
     {

@@ -66,7 +66,8 @@ void linear_apply_static(const DeviceLinear& w, const uint16_t* x, std::size_t M
                          hipStream_t stream)
 {
     const std::size_t K = w.K;
-    const bool tiles = path == LinearPath::gemm || (path == LinearPath::automatic && M > small_gemm_max_rows());
+    const bool tiles = path == LinearPath::gemm || (path == LinearPath::automatic && M > small_gemm_max_rows() &&
+                                                    !small_gemm_chosen(M, w.N, K));
     const Layout layout = tiles ? Layout::tiles : Layout::rows;
     const std::size_t rows = tiles ? tile_padded_rows(M) : M;
     require(K % 256 == 0 && rows * K <= static_values_bytes,

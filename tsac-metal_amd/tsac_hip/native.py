@@ -272,8 +272,8 @@ class SourceFile:
                                             C.byref(handle)))
         self.handle, self._library = handle, lib
 
-    def __del__(self):
-        _release(self, "tsac_hip_source_destroy")
+    def __del__(self, release=_release):  # bound now: module globals are cleared at shutdown
+        release(self, "tsac_hip_source_destroy")
 
     def close(self):
         _release(self, "tsac_hip_source_destroy")
@@ -485,8 +485,8 @@ class HipModel:
         self.handle, self._library = handle, lib
         return self
 
-    def __del__(self):
-        _release(self, "tsac_hip_model_destroy")
+    def __del__(self, release=_release):  # bound now: module globals are cleared at shutdown
+        release(self, "tsac_hip_model_destroy")
 
     def close(self):
         """Destroys the device model now (every session of it must be closed
@@ -512,8 +512,8 @@ class HipSession:
         check(library().tsac_hip_session_create(model.handle, C.byref(handle)))
         self.handle, self._library = handle, library()
 
-    def __del__(self):
-        _release(self, "tsac_hip_session_destroy")
+    def __del__(self, release=_release):  # bound now: module globals are cleared at shutdown
+        release(self, "tsac_hip_session_destroy")
 
     def close(self):
         """Destroys the session (its stream, caches and scratch) now; later
@@ -659,8 +659,8 @@ class HipDac:
         self.handle, self._library = handle, library()
         del keep
 
-    def __del__(self):
-        _release(self, "tsac_hip_dac_destroy")
+    def __del__(self, release=_release):  # bound now: module globals are cleared at shutdown
+        release(self, "tsac_hip_dac_destroy")
 
     def close(self):
         _release(self, "tsac_hip_dac_destroy")
@@ -754,8 +754,8 @@ class DeviceLinear:
         check(library().tsac_hip_linear_create(C.byref(desc), k, n, C.byref(handle)))
         self.handle, self._library = handle, library()
 
-    def __del__(self):
-        _release(self, "tsac_hip_linear_destroy")
+    def __del__(self, release=_release):  # bound now: module globals are cleared at shutdown
+        release(self, "tsac_hip_linear_destroy")
 
     def apply(self, x, y, path=PATH_AUTO, stream=None):
         """x: int16/uint16 cuda tensor [M][K] of BF16 bits -> y [M][N]."""
