@@ -191,131 +191,116 @@ __device__ __forceinline__ unsigned long long uniform64(unsigned long long v)
            __builtin_amdgcn_readfirstlane(uint32_t(v));
 }
 
-// The 16 payload bytes from `from` on, as RangeDecoder::read returns them (zero
-// past the end), in four words; and how many of them exist. One replay of at
-// most eight decisions reads at most 16: a decision leaves range >= 1, so at
-// most two renormalising shifts follow it.
-struct Bytes16
+// The 24 payload bytes from `from` on, as RangeDecoder::read returns them (zero
+// past the end), big-endian in three wave-uniform 64-bit words (byte 0 in the
+// top bits of part[0]), and how many of them exist. A symbol's ten decisions
+// read at most 20: a decision leaves range >= 1, so at most two renormalising
+// shifts follow it.
+struct PayloadBytes
 {
-    uint32_t word[4];
+    uint64_t part[3];
     uint32_t available;
-
-    // Byte k (< 16) by shifts of two 64-bit halves: an index into `word` with a
-    // per-lane k would put the array in scratch memory.
-    __device__ __forceinline__ uint32_t operator[](uint32_t k) const
-    {
-        const uint64_t low = word[0] | (uint64_t(word[1]) << 32), high = word[2] | (uint64_t(word[3]) << 32);
-        return uint32_t((k < 8 ? low >> (8 * k) : high >> (8 * (k - 8))) & 0xffu);
-    }
 };
 
 // `staged` is 4-byte aligned and holds zeros past the payload's end.
-__device__ __forceinline__ Bytes16 next_bytes(const ByteWindow& window, unsigned long long from)
+__device__ __forceinline__ PayloadBytes payload_bytes(const ByteWindow& window, unsigned long long from)
 {
-    Bytes16 b{{0, 0, 0, 0}, 0};
+    PayloadBytes b{{0, 0, 0}, 0};
     const unsigned long long end = uniform64(window.payload_bytes), base = uniform64(window.base);
     const uint32_t size = __builtin_amdgcn_readfirstlane(uint32_t(window.size));
-    b.available = from < end ? uint32_t(end - from < 16 ? end - from : 16) : 0u;
+    b.available = from < end ? uint32_t(end - from < 24 ? end - from : 24) : 0u;
     const unsigned long long at = from - base;
-    if (at + 20 <= size)
+    uint32_t word[6] = {0, 0, 0, 0, 0, 0}; // bytes 4i .. 4i + 3, the first on top
+    if (at + 28 <= size)
     {
-        // Five aligned words around the 16 bytes, realigned.
+        // Seven aligned words around the 24 bytes, realigned and byte-swapped.
         const Shared<uint32_t> words = (Shared<uint32_t>)(shared(window.staged));
         const uint32_t first = uint32_t(at) / 4, shift = uint32_t(at) % 4;
-        uint32_t w[5];
+        uint32_t w[7];
 #pragma unroll
-        for (int i = 0; i < 5; ++i)
+        for (int i = 0; i < 7; ++i)
         {
             w[i] = words[first + i];
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 6; ++i)
         {
-            b.word[i] = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_alignbyte(w[i + 1], w[i], shift));
+            const uint32_t little = __builtin_amdgcn_alignbyte(w[i + 1], w[i], shift);
+            word[i] = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_perm(little, little, 0x00010203u));
         }
-        return b;
     }
-    const Shared<uint8_t> staged = shared(window.staged);
-#pragma unroll
-    for (uint32_t i = 0; i < 16; ++i)
+    else
     {
-        uint32_t v = 0;
-        if (i < b.available)
+        const Shared<uint8_t> staged = shared(window.staged);
+#pragma unroll
+        for (uint32_t i = 0; i < 24; ++i)
         {
-            v = at + i < size ? uint32_t(staged[at + i])
-                              : uint32_t(*(const __attribute__((address_space(1))) uint8_t*)(window.payload + from + i));
+            uint32_t v = 0;
+            if (i < b.available)
+            {
+                v = at + i < size ? uint32_t(staged[at + i])
+                                  : uint32_t(*(const __attribute__((address_space(1))) uint8_t*)(window.payload + from + i));
+            }
+            word[i / 4] |= __builtin_amdgcn_readfirstlane(v) << (8 * (3 - i % 4));
         }
-        b.word[i / 4] |= __builtin_amdgcn_readfirstlane(v) << (8 * (i % 4));
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+    {
+        b.part[i] = (uint64_t(word[2 * i]) << 32) | word[2 * i + 1];
     }
     return b;
 }
 
-struct Coder
+// Bytes k .. k + 7 (k <= 16) as a 64-bit queue, byte k on top.
+__device__ __forceinline__ uint64_t byte_queue(const PayloadBytes& b, uint32_t k)
 {
-    uint32_t range, code;
-    uint32_t used; // payload bytes read since the replay's start
-};
-
-// RangeDecoder::get (src/format/range.cpp:136-152) forced along a path: for
-// decision d the path takes bit (path >> (levels - 1 - d)) & 1 with
-// probability-of-zero q[d]. Returns whether every decision the decoder makes
-// agrees with the path, up to the end or up to a failure, whose decision
-// index goes to `failed_at` (else -1); the state stops there. Branch free.
-template <int levels>
-__device__ __forceinline__ bool follow(Coder& c, const uint32_t (&q)[levels], int path, int& failed_at,
-                                       const Bytes16& bytes)
-{
-    bool agrees = true, live = true;
-    failed_at = -1;
-#pragma unroll
-    for (int d = 0; d < levels; ++d)
-    {
-        const bool right = (path >> (levels - 1 - d)) & 1;
-        const uint32_t range0 = uint32_t((uint64_t(c.range) * q[d]) >> 15);
-        agrees = agrees && (!live || (c.code >= range0) == right);
-        uint32_t code = right ? c.code - range0 : c.code;
-        uint32_t range = right ? c.range - range0 : range0;
-        uint32_t used = c.used;
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-        {
-            const bool shift = range < 0xff01u;
-            const bool read = shift && used < bytes.available;
-            const uint32_t next = read ? bytes[used] : 0u;
-            range = shift ? range << 8 : range;
-            code = shift ? (code << 8) + next : code;
-            used += read ? 1u : 0u;
-        }
-        if (live)
-        {
-            c.code = code;
-            c.range = range;
-            c.used = used;
-        }
-        if (live && !(code < range))
-        {
-            failed_at = d;
-            live = false;
-        }
-    }
-    return agrees;
+    const bool low = k < 8;
+    const uint64_t first = low ? b.part[0] : b.part[1], second = low ? b.part[1] : b.part[2];
+    const uint32_t s = 8 * (k & 7);
+    return (first << s) | ((second >> 1) >> (63 - s));
 }
 
-__device__ __forceinline__ Coder kept_coder(const Coder& c, int lane)
+// One RangeDecoder::get (src/format/range.cpp:136-152) on wave-uniform values:
+// the split, the bit, the interval and the renormalising shifts (one below
+// 0xff01, a second below 0x100), with the next payload bytes taken from the
+// top of `queue`; node becomes the child taken. Valid states have
+// code < range < 2^24, so the comparisons are sign bits of differences (no
+// condition register is kept across instructions).
+__device__ __forceinline__ void decide(uint32_t& range, uint32_t& code, uint64_t& queue, uint32_t& shifts, int& node,
+                                       uint32_t q)
 {
-    return Coder{uint32_t(__builtin_amdgcn_readlane(int(c.range), lane)),
-                 uint32_t(__builtin_amdgcn_readlane(int(c.code), lane)),
-                 uint32_t(__builtin_amdgcn_readlane(int(c.used), lane))};
+    const uint32_t range0 = uint32_t((uint64_t(range) * q) >> 15);
+    const int32_t left = int32_t(code - range0) >> 31; // -1 when code < range0: the zero branch
+    code -= range0 & ~uint32_t(left);
+    range = left ? range0 : range - range0;
+    const uint32_t n = (uint32_t(int32_t(range - 0xff01u)) >> 31) + (uint32_t(int32_t(range - 0x100u)) >> 31);
+    const uint32_t by = 8 * n;
+    range <<= by;
+    code = (code << by) | uint32_t((queue >> (63 - by)) >> 1);
+    queue <<= by;
+    shifts += n;
+    // Kept apart so that the child index stays a scalar add (a funnel shift
+    // would move it to a vector register and back before the next read).
+    int twice = 2 * node;
+    __asm__ volatile("" : "+s"(twice));
+    node = twice + 1 + left;
 }
 
 // One decode_categorical symbol with RangeDecoder::get. Called by a whole wave
-// with identical arguments. Instead of making the ten decisions one after the
-// other, lane j replays the first six along path j (the decisions' q from
-// `top`) and the lane whose path the decoder agrees with is kept; then 16
-// lanes do the same for the last four, below the node reached, with q
-// computed on the spot. Each replay is the reference's arithmetic, so the
-// kept lane's state is the serial decoder's. On a failure the symbol and
-// state are those at the failing decision, as the reference leaves them.
+// with identical arguments. The ten decisions run one after the other on
+// wave-uniform values; each decision's q is read from the lane that holds it
+// (v_readlane), so no decision waits for memory: lane l holds q(l) from `top`
+// for levels 0..5, and once the node at depth 6 is known, lanes 1..15 compute
+// the q's of its subtree for levels 6..9.
+//
+// RangeDecoder::get fails when a decision leaves code >= range. A decision
+// from a state with code < range keeps code < range (the zero branch sets
+// range = range0 > code, the one branch subtracts range0 from both, and a
+// renormalising shift appends a byte below 256), so a decode fails only from
+// a state entered with code >= range, and then at its first decision, which
+// goes to the one branch; the symbol and state are those there, as the
+// reference leaves them.
 __device__ __forceinline__ int decode_symbol(const uint16_t* top, const Masses& mass, DecoderState& s,
                                              const ByteWindow& window)
 {
@@ -325,79 +310,93 @@ __device__ __forceinline__ int decode_symbol(const uint16_t* top, const Masses& 
         return 0;
     }
     const unsigned long long offset = uniform64(s.offset);
-    const Coder start{uint32_t(__builtin_amdgcn_readfirstlane(s.range)),
-                      uint32_t(__builtin_amdgcn_readfirstlane(s.code)), 0u};
-    const Shared<uint16_t> shared_top = shared(top);
-    // Levels 0..5: path = lane.
-    uint32_t q6[6];
+    uint32_t range = uint32_t(__builtin_amdgcn_readfirstlane(s.range));
+    uint32_t code = uint32_t(__builtin_amdgcn_readfirstlane(s.code));
+    const int q_top = int(shared(top)[lane]); // lane 0's entry is not used
+    // Lane l: the left masses along the path to node 64 + l.
     float left6[6];
 #pragma unroll
     for (int d = 0; d < 6; ++d)
     {
-        const int node = (64 + lane) >> (6 - d);
-        q6[d] = shared_top[node];
-        left6[d] = mass.nodes[2 * node];
+        left6[d] = mass.nodes[2 * ((64 + lane) >> (6 - d))];
     }
-    const Bytes16 bytes6 = next_bytes(window, offset);
-    Coder c = start;
-    int failed_at;
-    const bool agrees = follow<6>(c, q6, lane, failed_at, bytes6);
-    const int j = __builtin_ctzll(__ballot(agrees)); // some lane always agrees
-    const int fail6 = __builtin_amdgcn_readlane(failed_at, j);
-    const Coder at = kept_coder(c, j);
-    const unsigned long long offset6 = offset + at.used;
-    if (fail6 >= 0)
+    const PayloadBytes bytes = payload_bytes(window, offset);
+    uint64_t queue = bytes.part[0];
+    uint32_t shifts = 0;
+    int node = 1;
+    if (code >= range)
     {
-        s.range = at.range;
-        s.code = at.code;
-        s.offset = offset6;
+        decide(range, code, queue, shifts, node, uint32_t(__builtin_amdgcn_readlane(q_top, 1)));
+        s.range = range;
+        s.code = code;
+        s.offset = offset + min(shifts, bytes.available);
         s.failed = 1;
-        const int node = (1 << (fail6 + 1)) + (j >> (5 - fail6)); // after fail6 + 1 decisions
-        return (node << (9 - fail6)) - 1024;
+        return (node << 9) - 1024;
     }
-    // Mass entering node 64 + j.
-    float entering = 1.0f;
+    // Levels 0..5; three decisions read at most six bytes of a queue.
+#pragma unroll
+    for (int d = 0; d < 6; ++d)
+    {
+        if (d == 3)
+        {
+            queue = byte_queue(bytes, shifts);
+        }
+        decide(range, code, queue, shifts, node, uint32_t(__builtin_amdgcn_readlane(q_top, node)));
+    }
+    // The mass the walk enters node (64 + lane) with, then node's.
+    float entering_lane = 1.0f;
 #pragma unroll
     for (int d = 0; d < 6; ++d)
     {
         const bool right = (lane >> (5 - d)) & 1;
-        entering = right ? flush(entering - left6[d]) : left6[d];
+        entering_lane = right ? flush(entering_lane - left6[d]) : left6[d];
     }
-    const int node6 = 64 + j;
-    entering = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(entering), j));
-    // Levels 6..9: lane u in 1..15 computes q of node6's subtree node u (heap
-    // order: node (node6 << depth) + u - (1 << depth)), then lanes 0..15
-    // replay path = lane, whose d-th node is subtree node (16 + lane) >> (4 - d).
-    const Bytes16 bytes4 = next_bytes(window, offset6);
-    uint32_t mine = 0;
-    if (lane >= 1 && lane < 16)
+    const float entering = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(entering_lane), node - 64));
+    // Lane u (1..15): q of subtree node u in heap order, node_q15 with every
+    // mass read made unconditionally (a leaf only for the own left child at
+    // depth 3), so that they go out together.
+    int q_sub;
     {
-        const int depth = 31 - __builtin_clz(uint32_t(lane));
-        mine = node_q15<3>(mass, entering, (node6 << depth) + (lane - (1 << depth)), depth);
+        const int u = (lane & 15) ? (lane & 15) : 1;
+        const int depth = 31 - __builtin_clz(uint32_t(u));
+        const int n = (node << depth) + (u - (1 << depth));
+        float left[3];
+#pragma unroll
+        for (int d = 0; d < 3; ++d)
+        {
+            left[d] = mass.nodes[2 * (n >> max(depth - d, 0))];
+        }
+        const int own = 2 * n; // 256 .. 2047
+        const float own_node = mass.nodes[own & 1023];
+        const float own_leaf = flush(bf16_to_float(mass.leaves[own & 1023]));
+        float e = entering;
+#pragma unroll
+        for (int d = 0; d < 3; ++d)
+        {
+            if (d < depth)
+            {
+                const bool right = (n >> (depth - 1 - d)) & 1;
+                e = right ? flush(e - left[d]) : left[d];
+            }
+        }
+        q_sub = q15(own < 1024 ? own_node : own_leaf, e);
     }
-    uint32_t q4[4];
+    // Levels 6..9; two decisions per queue.
+    const int node6 = node;
+    node = 1;
 #pragma unroll
     for (int d = 0; d < 4; ++d)
     {
-        q4[d] = uint32_t(__shfl(int(mine), (16 + (lane & 15)) >> (4 - d), wave));
+        if (d % 2 == 0)
+        {
+            queue = byte_queue(bytes, shifts);
+        }
+        decide(range, code, queue, shifts, node, uint32_t(__builtin_amdgcn_readlane(q_sub, node)));
     }
-    Coder c2{at.range, at.code, 0u};
-    int failed2;
-    const bool agrees2 = follow<4>(c2, q4, lane & 15, failed2, bytes4) && lane < 16;
-    const int j2 = __builtin_ctzll(__ballot(agrees2));
-    const int fail4 = __builtin_amdgcn_readlane(failed2, j2);
-    const Coder end = kept_coder(c2, j2);
-    s.range = end.range;
-    s.code = end.code;
-    s.offset = offset6 + end.used;
-    if (fail4 >= 0)
-    {
-        s.failed = 1;
-        const int node = (node6 << (fail4 + 1)) + (j2 >> (3 - fail4)); // after 7 + fail4 decisions
-        return (node << (3 - fail4)) - 1024;
-    }
-    return 16 * node6 + j2 - 1024;
+    s.range = range;
+    s.code = code;
+    s.offset = offset + min(shifts, bytes.available);
+    return 16 * node6 + (node - 16) - 1024;
 }
-
 } // namespace step
 } // namespace tsac_hip
