@@ -69,21 +69,24 @@ __device__ __forceinline__ float snake(float y, float a, bool& finite)
     return result;
 }
 
-// One wave: 64 output frames (one per lane) x 16 output channels. Ordinary
+// One wave: 64 output frames (one per lane) x CH output channels. Ordinary
 // convolutions take consecutive frames; transposed ones the frames of one
 // residue class mod the stride, so every tap is either valid for the whole wave
-// or only at its edges.
-template <bool Transposed> __global__ __launch_bounds__(conv_threads) void conv_kernel(const ConvArgs a)
+// or only at its edges. Each input value loaded serves CH serial sums; layers
+// with few frames take CH = 8 or 4 so that their grid still fills the SIMDs
+// (each sum stays one serial chain, so CH changes no value).
+template <bool Transposed, int CH> __global__ __launch_bounds__(conv_threads) void conv_kernel(const ConvArgs a)
 {
+    static_assert(dac_channel_block % CH == 0, "channel groups within the weights' padding");
     const int lane = threadIdx.x % lanes;
     const int block = blockIdx.y * conv_waves + __builtin_amdgcn_readfirstlane(int(threadIdx.x / lanes));
     const ConvShape s = a.conv.shape;
     const int out_padded = a.conv.out_padded;
-    if (block * dac_channel_block >= out_padded)
+    if (block * CH >= out_padded)
     {
         return;
     }
-    const int c0 = block * dac_channel_block;
+    const int c0 = block * CH;
     const int out_frames = s.output_frames(a.frames);
     int f;
     int first_tap = 0, tap_step = 1;
@@ -99,9 +102,9 @@ template <bool Transposed> __global__ __launch_bounds__(conv_threads) void conv_
         f = blockIdx.x * lanes + lane;
     }
     const bool in_range = f < out_frames && f >= a.first && f < a.last;
-    float sum[dac_channel_block];
+    float sum[CH];
 #pragma unroll
-    for (int j = 0; j < dac_channel_block; ++j)
+    for (int j = 0; j < CH; ++j)
     {
         sum[j] = 0.0f;
     }
@@ -131,13 +134,15 @@ template <bool Transposed> __global__ __launch_bounds__(conv_threads) void conv_
         }
         const float* xs = x + source * xf;
         const float* wt = w + std::size_t(tap) * s.in * out_padded;
-#pragma unroll 4
+        // About 64 products per lane between the loads' issue and their use.
+        constexpr int ahead = 64 / CH;
+#pragma unroll ahead
         for (int i = 0; i < s.in; ++i)
         {
             const float xv = xs[i * xc];
             const constant_ptr<float> wv = constant(wt + std::size_t(i) * out_padded);
 #pragma unroll
-            for (int j = 0; j < dac_channel_block; ++j)
+            for (int j = 0; j < CH; ++j)
             {
                 const float product = xv * wv[j];
                 sum[j] = sum[j] + product;
@@ -151,7 +156,7 @@ template <bool Transposed> __global__ __launch_bounds__(conv_threads) void conv_
     bool finite = true;
     const constant_ptr<float> bias = constant(a.conv.bias);
 #pragma unroll
-    for (int j = 0; j < dac_channel_block; ++j)
+    for (int j = 0; j < CH; ++j)
     {
         const int c = c0 + j;
         if (c >= s.out)
@@ -364,6 +369,22 @@ void dac_conv_layout(const ConvShape& s, const float* stored, float* out, int ou
     }
 }
 
+namespace
+{
+int compute_units()
+{
+    static const int count = []
+    {
+        int device = 0, units = 0;
+        check_hip(hipGetDevice(&device), "hipGetDevice");
+        check_hip(hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device),
+                  "hipDeviceGetAttribute");
+        return units > 0 ? units : 1;
+    }();
+    return count;
+}
+} // namespace
+
 void dac_conv(const ConvArgs& a, hipStream_t stream)
 {
     const ConvShape& s = a.conv.shape;
@@ -373,17 +394,29 @@ void dac_conv(const ConvArgs& a, hipStream_t stream)
     require(!s.transposed || s.dilation == 1, "dac convolution: dilated transposed convolution");
     const int out_frames = s.output_frames(a.frames);
     require(out_frames > 0, "dac convolution has no output frames");
-    const int blocks = a.conv.out_padded / dac_channel_block;
-    const unsigned grid_y = unsigned((blocks + conv_waves - 1) / conv_waves);
+    const unsigned tiles = s.transposed
+                               ? unsigned(((out_frames + s.stride - 1) / s.stride + lanes - 1) / lanes) * s.stride
+                               : unsigned((out_frames + lanes - 1) / lanes);
+    // The widest channel group whose grid gives every SIMD two waves, else 4.
+    // A strided (downsampling) convolution keeps 16: its lanes read frames
+    // `stride` apart, so each load touches up to 16 cache lines, and fewer
+    // channels per load multiply those loads (measured on the 400-frame
+    // analysis chunks: 256 -> 512 channels, stride 8, 884 us at 16 channels
+    // per wave, 2,478 us at 8).
+    const std::size_t simds = std::size_t(compute_units()) * 4;
+    const auto waves = [&](int ch) { return std::size_t(tiles) * std::size_t(a.conv.out_padded / ch); };
+    const bool strided = !s.transposed && s.stride > 1;
+    const int ch = strided || waves(16) >= 2 * simds ? 16 : waves(8) >= 2 * simds ? 8 : 4;
+    const unsigned grid_y = unsigned((a.conv.out_padded / ch + conv_waves - 1) / conv_waves);
+    const auto launch = [&](auto kernel) { kernel<<<dim3(tiles, grid_y), conv_threads, 0, stream>>>(a); };
     if (s.transposed)
     {
-        const int per_residue = (out_frames + s.stride - 1) / s.stride;
-        const unsigned tiles = unsigned((per_residue + lanes - 1) / lanes);
-        conv_kernel<true><<<dim3(tiles * s.stride, grid_y), conv_threads, 0, stream>>>(a);
+        ch == 16 ? launch(conv_kernel<true, 16>) : ch == 8 ? launch(conv_kernel<true, 8>) : launch(conv_kernel<true, 4>);
     }
     else
     {
-        conv_kernel<false><<<dim3(unsigned((out_frames + lanes - 1) / lanes), grid_y), conv_threads, 0, stream>>>(a);
+        ch == 16 ? launch(conv_kernel<false, 16>) : ch == 8 ? launch(conv_kernel<false, 8>)
+                                                        : launch(conv_kernel<false, 4>);
     }
     check_hip(hipGetLastError(), "dac convolution launch");
 }
