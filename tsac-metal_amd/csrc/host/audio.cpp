@@ -424,6 +424,16 @@ void Session::analysis_graph(const DacModel& dac, Strided input, int samples, St
     int length = samples;
     int x = 0, s = 1, t = 2;
     const auto signal = [&](int slot, int frames) { return Strided{slots[slot], frames, 1}; };
+    // The downsampling input in `phases` planes of frames / phases (frame t
+    // of a channel at (t % phases) * frames / phases + t / phases): each
+    // plane is one residue of the stride, so the downsampling's lanes read
+    // consecutive frames. Chunks hold whole latent frames, so every stage's
+    // length is a multiple of its stride.
+    const auto polyphase = [&](int slot, int frames, int phases)
+    {
+        require(frames % phases == 0, "analysis: a stage's length is a multiple of its stride");
+        return Strided{slots[slot], frames, 1, phases, frames / phases};
+    };
     const auto conv = [&](unsigned index, Strided in, Strided out, Strided activated, unsigned alpha, bool residual)
     {
         ConvArgs a;
@@ -445,17 +455,19 @@ void Session::analysis_graph(const DacModel& dac, Strided input, int samples, St
     conv(0, input, signal(x, entry), signal(s, entry), 0, false);
     for (unsigned stage = 0; stage < 4; ++stage)
     {
+        const int stride = dac.convolution(false, 1 + stage * 7 + 6).shape.stride;
         for (unsigned unit = 0; unit < 3; ++unit)
         {
             const unsigned act = stage * 7 + unit * 2, index = 1 + stage * 7 + unit * 2;
             conv(index, signal(s, length), Strided{}, signal(t, length), act + 1, false);
-            conv(index + 1, signal(t, length), signal(x, length), signal(s, length), unit < 2 ? act + 2 : stage * 7 + 6,
+            conv(index + 1, signal(t, length), signal(x, length),
+                 unit < 2 ? signal(s, length) : polyphase(s, length, stride), unit < 2 ? act + 2 : stage * 7 + 6,
                  true);
         }
-        // downsample: its input (the resample Snake) is in s, x is free
+        // downsample: its input (the resample Snake) is in s, polyphase; x is free
         const int down = dac.convolution(false, 1 + stage * 7 + 6).shape.output_frames(length);
-        conv(1 + stage * 7 + 6, signal(s, length), signal(x, down), signal(t, down), stage < 3 ? (stage + 1) * 7 : 28,
-             false);
+        conv(1 + stage * 7 + 6, polyphase(s, length, stride), signal(x, down), signal(t, down),
+             stage < 3 ? (stage + 1) * 7 : 28, false);
         std::swap(s, t);
     }
     require(dac.convolution(false, 29).shape.output_frames(length) == samples / int(hop),

@@ -132,7 +132,8 @@ template <bool Transposed, int CH> __global__ __launch_bounds__(conv_threads) vo
         {
             continue;
         }
-        const float* xs = x + source * xf;
+        const float* xs = x + (a.x.phases > 1 ? (source % a.x.phases) * a.x.phase + (source / a.x.phases) * xf
+                                              : source * xf);
         const float* wt = w + std::size_t(tap) * s.in * out_padded;
         // About 64 products per lane between the loads' issue and their use.
         constexpr int ahead = 64 / CH;
@@ -175,7 +176,10 @@ template <bool Transposed, int CH> __global__ __launch_bounds__(conv_threads) vo
         }
         if (a.activated.data)
         {
-            a.activated.data[c * a.activated.channel + f * a.activated.frame] = snake(y, a.alpha[c], finite);
+            const long long at = a.activated.phases > 1 ? (f % a.activated.phases) * a.activated.phase +
+                                                              (f / a.activated.phases) * a.activated.frame
+                                                        : f * a.activated.frame;
+            a.activated.data[c * a.activated.channel + at] = snake(y, a.alpha[c], finite);
         }
     }
     if (!finite)
@@ -392,20 +396,23 @@ void dac_conv(const ConvArgs& a, hipStream_t stream)
     require(!a.activated.data || a.alpha, "dac convolution: Snake needs its alpha");
     require(a.conv.out_padded % dac_channel_block == 0 && a.conv.out_padded >= s.out, "dac convolution: layout");
     require(!s.transposed || s.dilation == 1, "dac convolution: dilated transposed convolution");
+    require(a.x.phases >= 1 && a.activated.phases >= 1 && a.out.phases == 1 && a.residual.phases == 1,
+            "dac convolution: only the input and the Snake output may be polyphase");
     const int out_frames = s.output_frames(a.frames);
     require(out_frames > 0, "dac convolution has no output frames");
     const unsigned tiles = s.transposed
                                ? unsigned(((out_frames + s.stride - 1) / s.stride + lanes - 1) / lanes) * s.stride
                                : unsigned((out_frames + lanes - 1) / lanes);
     // The widest channel group whose grid gives every SIMD two waves, else 4.
-    // A strided (downsampling) convolution keeps 16: its lanes read frames
-    // `stride` apart, so each load touches up to 16 cache lines, and fewer
-    // channels per load multiply those loads (measured on the 400-frame
-    // analysis chunks: 256 -> 512 channels, stride 8, 884 us at 16 channels
-    // per wave, 2,478 us at 8).
+    // A strided (downsampling) convolution on frames in plain order keeps 16:
+    // its lanes read frames `stride` apart, so each load touches up to 16
+    // cache lines, and fewer channels per load multiply those loads (measured
+    // on the 400-frame analysis chunks: 256 -> 512 channels, stride 8, 884 us
+    // at 16 channels per wave, 2,478 us at 8). On polyphase input (phases ==
+    // stride) its lanes read consecutive addresses.
     const std::size_t simds = std::size_t(compute_units()) * 4;
     const auto waves = [&](int ch) { return std::size_t(tiles) * std::size_t(a.conv.out_padded / ch); };
-    const bool strided = !s.transposed && s.stride > 1;
+    const bool strided = !s.transposed && s.stride > 1 && a.x.phases != s.stride;
     const int ch = strided || waves(16) >= 2 * simds ? 16 : waves(8) >= 2 * simds ? 8 : 4;
     const unsigned grid_y = unsigned((a.conv.out_padded / ch + conv_waves - 1) / conv_waves);
     const auto launch = [&](auto kernel) { kernel<<<dim3(tiles, grid_y), conv_threads, 0, stream>>>(a); };

@@ -53,6 +53,11 @@ struct Strided
 {
     float* data = nullptr;
     long long channel = 0, frame = 0; // element strides
+    // Polyphase frames (phases > 1): frame t at (t % phases) * phase + (t / phases) * frame,
+    // so a convolution of stride `phases` reads its lanes' frames contiguously.
+    // Only a convolution's input and its Snake output may be polyphase.
+    int phases = 1;
+    long long phase = 0;
 };
 
 // y = conv(x) + bias; then optionally y = residual + y; stores y to `out` and
