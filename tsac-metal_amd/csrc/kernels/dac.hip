@@ -73,7 +73,7 @@ __device__ __forceinline__ float snake(float y, float a, bool& finite)
 // convolutions take consecutive frames; transposed ones the frames of one
 // residue class mod the stride, so every tap is either valid for the whole wave
 // or only at its edges. Each input value loaded serves CH serial sums; layers
-// with few frames take CH = 8 or 4 so that their grid still fills the SIMDs
+// with few frames take CH = 8, 4 or 2 so that their grid still fills the SIMDs
 // (each sum stays one serial chain, so CH changes no value).
 template <bool Transposed, int CH> __global__ __launch_bounds__(conv_threads) void conv_kernel(const ConvArgs a)
 {
@@ -136,7 +136,7 @@ template <bool Transposed, int CH> __global__ __launch_bounds__(conv_threads) vo
                                               : source * xf);
         const float* wt = w + std::size_t(tap) * s.in * out_padded;
         // About 64 products per lane between the loads' issue and their use.
-        constexpr int ahead = 64 / CH;
+        constexpr int ahead = 64 / CH < 16 ? 64 / CH : 16;
 #pragma unroll ahead
         for (int i = 0; i < s.in; ++i)
         {
@@ -403,7 +403,9 @@ void dac_conv(const ConvArgs& a, hipStream_t stream)
     const unsigned tiles = s.transposed
                                ? unsigned(((out_frames + s.stride - 1) / s.stride + lanes - 1) / lanes) * s.stride
                                : unsigned((out_frames + lanes - 1) / lanes);
-    // The widest channel group whose grid gives every SIMD two waves, else 4.
+    // 16 channels per wave while the grid gives every SIMD four waves, else
+    // the widest group that gives two, down to 2 (measured on the 400-frame
+    // chunks: 8 channels beat 16 at 2,496 waves, 4 lost to 8 at 3,328).
     // A strided (downsampling) convolution on frames in plain order keeps 16:
     // its lanes read frames `stride` apart, so each load touches up to 16
     // cache lines, and fewer channels per load multiply those loads (measured
@@ -413,17 +415,21 @@ void dac_conv(const ConvArgs& a, hipStream_t stream)
     const std::size_t simds = std::size_t(compute_units()) * 4;
     const auto waves = [&](int ch) { return std::size_t(tiles) * std::size_t(a.conv.out_padded / ch); };
     const bool strided = !s.transposed && s.stride > 1 && a.x.phases != s.stride;
-    const int ch = strided || waves(16) >= 2 * simds ? 16 : waves(8) >= 2 * simds ? 8 : 4;
+    const int ch = strided || waves(16) >= 4 * simds ? 16
+                   : waves(8) >= 2 * simds             ? 8
+                   : waves(4) >= 2 * simds             ? 4
+                                                       : 2;
     const unsigned grid_y = unsigned((a.conv.out_padded / ch + conv_waves - 1) / conv_waves);
     const auto launch = [&](auto kernel) { kernel<<<dim3(tiles, grid_y), conv_threads, 0, stream>>>(a); };
     if (s.transposed)
     {
-        ch == 16 ? launch(conv_kernel<true, 16>) : ch == 8 ? launch(conv_kernel<true, 8>) : launch(conv_kernel<true, 4>);
+        ch == 16 ? launch(conv_kernel<true, 16>) : ch == 8 ? launch(conv_kernel<true, 8>)
+            : ch == 4 ? launch(conv_kernel<true, 4>) : launch(conv_kernel<true, 2>);
     }
     else
     {
         ch == 16 ? launch(conv_kernel<false, 16>) : ch == 8 ? launch(conv_kernel<false, 8>)
-                                                        : launch(conv_kernel<false, 4>);
+            : ch == 4 ? launch(conv_kernel<false, 4>) : launch(conv_kernel<false, 2>);
     }
     check_hip(hipGetLastError(), "dac convolution launch");
 }
