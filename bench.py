@@ -371,9 +371,6 @@ def attention_rates(torch, native, lengths=(256, 1290, 2580), batch=3, heads=16,
         rows.append({"T": T, "prefill_us": round(prefill_s * 1e6, 1),
                      "prefill_TFLOPs": round(flops / prefill_s / 1e12, 2),
                      "prefill_frac_fp32_valu": round(flops / prefill_s / 1e12 / FP32_PEAK_TFLOPS, 4),
-                     # The chains are non-packed FMAs (packed FP32 is kept out of
-                     # the build): half the published figure is their ceiling.
-                     "prefill_frac_nonpacked_fma": round(flops / prefill_s / 1e12 / (FP32_PEAK_TFLOPS / 2), 4),
                      "decode_us": round(decode_s * 1e6, 2), "decode_cache_copies": copies,
                      "decode_GBps": round(kv_bytes / decode_s / 1e9, 1),
                      "decode_frac_hbm": round(kv_bytes / decode_s / 1e9 / HBM_PEAK_GBPS, 4)})
