@@ -604,7 +604,82 @@ __global__ __launch_bounds__(256) void prefill_kernel(
             block_maximum[a] = maximum;
         }
         __syncthreads();
-        // Value sums: serial fma over the block's live keys, ascending.
+        // Value sums: serial fma over each query's live keys, ascending. Keys
+        // are the outer loop, so each value row read and widened serves the
+        // thread's four queries; a query's chain stops at its own last key.
+        int count[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+        {
+            const int query = q0 + 4 * group + a;
+            const int live = (query < k0 + tile - 1 ? query : k0 + tile - 1) - k0 + 1;
+            count[a] = query >= length ? 0 : live < length - k0 ? live : length - k0;
+        }
+        // Queries past the sequence (count 0) are never merged, so they need
+        // not stop the others' unchecked loop.
+        int common = tile, most = 0;
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+        {
+            if (count[a] > 0)
+            {
+                common = min(common, count[a]);
+                most = max(most, count[a]);
+            }
+        }
+        common = min(common, most);
+        float sums[4][columns];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+        {
+#pragma unroll
+            for (int c = 0; c < columns; ++c)
+            {
+                sums[a][c] = 0.0f;
+            }
+        }
+        const auto accumulate = [&](int t, const float (&w)[4], bool every)
+        {
+            const uint16_t* vrow = shared.v + t * row + slot * columns;
+            float value[columns];
+#pragma unroll
+            for (int c = 0; c < columns; ++c)
+            {
+                value[c] = bf16_to_float(vrow[c]);
+            }
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+            {
+                if (every || t < count[a])
+                {
+#pragma unroll
+                    for (int c = 0; c < columns; ++c)
+                    {
+                        sums[a][c] = __builtin_fmaf(value[c], w[a], sums[a][c]);
+                    }
+                }
+            }
+        };
+        int t = 0;
+        for (; t + 4 <= common; t += 4)
+        {
+            float4 w4[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+            {
+                w4[a] = *reinterpret_cast<const float4*>(&shared.p[4 * group + a][t]);
+            }
+            accumulate(t, {w4[0].x, w4[1].x, w4[2].x, w4[3].x}, true);
+            accumulate(t + 1, {w4[0].y, w4[1].y, w4[2].y, w4[3].y}, true);
+            accumulate(t + 2, {w4[0].z, w4[1].z, w4[2].z, w4[3].z}, true);
+            accumulate(t + 3, {w4[0].w, w4[1].w, w4[2].w, w4[3].w}, true);
+        }
+        for (; t < most; ++t)
+        {
+            accumulate(t, {shared.p[4 * group][t], shared.p[4 * group + 1][t], shared.p[4 * group + 2][t],
+                           shared.p[4 * group + 3][t]},
+                       false);
+        }
 #pragma unroll
         for (int a = 0; a < 4; ++a)
         {
@@ -612,24 +687,6 @@ __global__ __launch_bounds__(256) void prefill_kernel(
             if (query >= length)
             {
                 continue;
-            }
-            const int live = (query < k0 + tile - 1 ? query : k0 + tile - 1) - k0 + 1;
-            const int count = live < length - k0 ? live : length - k0;
-            float sums[columns];
-#pragma unroll
-            for (int c = 0; c < columns; ++c)
-            {
-                sums[c] = 0.0f;
-            }
-            for (int t = 0; t < count; ++t)
-            {
-                const float w = shared.p[4 * group + a][t];
-                const uint16_t* vrow = shared.v + t * row + slot * columns;
-#pragma unroll
-                for (int c = 0; c < columns; ++c)
-                {
-                    sums[c] = __builtin_fmaf(bf16_to_float(vrow[c]), w, sums[c]);
-                }
             }
             const bool round_values = query + 1 > 64 || query < replay;
             const float maximum = block_maximum[a];
@@ -642,7 +699,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(
 #pragma unroll
             for (int c = 0; c < columns; ++c)
             {
-                const float s = round_values ? round_bf16(sums[c]) : sums[c];
+                const float s = round_values ? round_bf16(sums[a][c]) : sums[a][c];
                 const float old = numerator[a][c] * old_scale;
                 numerator[a][c] = __builtin_fmaf(s, new_scale, old);
             }
