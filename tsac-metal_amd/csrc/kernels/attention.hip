@@ -423,23 +423,32 @@ __global__ __launch_bounds__(decode_waves * 64) void decode_attention_kernel(
 
 constexpr int tile = 64;
 
+// With 64-wide heads the key tile is widened to fp32 as it is stored, once
+// per block, instead of by each of the 16 threads that read a key row (the
+// workgroup still fits three to a CU); 128-wide heads keep BF16 keys.
+template <int HW> constexpr bool wide_keys = HW == 64;
+
 template <int HW> struct PrefillShared
 {
-    static constexpr int row = HW + 8; // BF16 elements per LDS row (16-byte pad)
+    static constexpr int row = HW + 8;  // BF16 elements per LDS row (16-byte pad)
+    static constexpr int key_row = HW + 4; // fp32 elements per widened key row
     uint16_t q[tile * row];
-    uint16_t k[tile * row];
+    uint16_t k[wide_keys<HW> ? 8 : tile * row];
+    float kf[wide_keys<HW> ? tile * key_row : 4];
     uint16_t v[tile * row];
     float p[tile][tile + 4];
 };
 
 // Loads a [64][HW] tile from rows of `source` (row stride `stride` elements)
 // with optional rotary at positions first..first+63. Rows at or beyond `limit`
-// are zero.
-template <int HW>
-__device__ __forceinline__ void load_tile(uint16_t* dst, const uint16_t* source, std::size_t stride,
+// are zero. With a float destination the values are stored widened (rows of
+// key_row floats).
+template <int HW, class T>
+__device__ __forceinline__ void load_tile(T* dst, const uint16_t* source, std::size_t stride,
                                           int first, int limit, const uint16_t* rotations)
 {
-    constexpr int row = PrefillShared<HW>::row;
+    constexpr bool widen = sizeof(T) == 4;
+    constexpr int row = widen ? PrefillShared<HW>::key_row : PrefillShared<HW>::row;
     constexpr int chunks = HW / 8;
     for (int i = threadIdx.x; i < tile * chunks; i += blockDim.x)
     {
@@ -464,7 +473,19 @@ __device__ __forceinline__ void load_tile(uint16_t* dst, const uint16_t* source,
                 u = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
-        *reinterpret_cast<uint4*>(dst + r * row + c * 8) = u;
+        if constexpr (widen)
+        {
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+            float4* out = reinterpret_cast<float4*>(dst + r * row + c * 8);
+            out[0] = make_float4(__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u),
+                                 __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u));
+            out[1] = make_float4(__uint_as_float(w[2] << 16), __uint_as_float(w[2] & 0xffff0000u),
+                                 __uint_as_float(w[3] << 16), __uint_as_float(w[3] & 0xffff0000u));
+        }
+        else
+        {
+            *reinterpret_cast<uint4*>(dst + r * row + c * 8) = u;
+        }
     }
 }
 
@@ -515,7 +536,14 @@ __global__ __launch_bounds__(256) void prefill_kernel(
     {
         const int k0 = block * tile;
         __syncthreads(); // previous block's K/V/P reads are done
-        load_tile<HW>(shared.k, base + width, stride, k0, length, rotations);
+        if constexpr (wide_keys<HW>)
+        {
+            load_tile<HW>(shared.kf, base + width, stride, k0, length, rotations);
+        }
+        else
+        {
+            load_tile<HW>(shared.k, base + width, stride, k0, length, rotations);
+        }
         load_tile<HW>(shared.v, base + 2 * width, stride, k0, length, nullptr);
         __syncthreads();
 
@@ -531,11 +559,22 @@ __global__ __launch_bounds__(256) void prefill_kernel(
         for (int c = 0; c < HW / 8; ++c)
         {
             uint4 qu[4], ku[4];
+            float4 kf[4][2];
 #pragma unroll
             for (int a = 0; a < 4; ++a)
             {
                 qu[a] = *reinterpret_cast<const uint4*>(shared.q + (4 * group + a) * row + c * 8);
-                ku[a] = *reinterpret_cast<const uint4*>(shared.k + (slot + 16 * a) * row + c * 8);
+                if constexpr (wide_keys<HW>)
+                {
+                    const float4* k = reinterpret_cast<const float4*>(
+                        shared.kf + (slot + 16 * a) * PrefillShared<HW>::key_row + c * 8);
+                    kf[a][0] = k[0];
+                    kf[a][1] = k[1];
+                }
+                else
+                {
+                    ku[a] = *reinterpret_cast<const uint4*>(shared.k + (slot + 16 * a) * row + c * 8);
+                }
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e)
@@ -545,9 +584,18 @@ __global__ __launch_bounds__(256) void prefill_kernel(
                 for (int a = 0; a < 4; ++a)
                 {
                     const uint32_t qw[4] = {qu[a].x, qu[a].y, qu[a].z, qu[a].w};
-                    const uint32_t kw[4] = {ku[a].x, ku[a].y, ku[a].z, ku[a].w};
                     qv[a] = bf16_to_float(uint16_t(e % 2 ? qw[e / 2] >> 16 : qw[e / 2] & 0xffff));
-                    kv[a] = bf16_to_float(uint16_t(e % 2 ? kw[e / 2] >> 16 : kw[e / 2] & 0xffff));
+                    if constexpr (wide_keys<HW>)
+                    {
+                        const float4 h = kf[a][e / 4];
+                        const float k4[4] = {h.x, h.y, h.z, h.w};
+                        kv[a] = k4[e % 4];
+                    }
+                    else
+                    {
+                        const uint32_t kw[4] = {ku[a].x, ku[a].y, ku[a].z, ku[a].w};
+                        kv[a] = bf16_to_float(uint16_t(e % 2 ? kw[e / 2] >> 16 : kw[e / 2] & 0xffff));
+                    }
                 }
 #pragma unroll
                 for (int a = 0; a < 4; ++a)
